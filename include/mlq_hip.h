@@ -1,0 +1,172 @@
+/*
+ * mlq_hip.h -- C ABI of the MI355X (gfx950) quantized-linear path for
+ * mini-llama.cpp (yus3nable/mini-llama-cpp-release).
+ *
+ * Plain C: no HIP, torch or C++ types in any signature.  Pointers are either
+ * host pointers or device pointers obtained from this library (or any HIP
+ * allocation on the same device); which one is stated per argument.  Streams
+ * are passed as `void*` holding a hipStream_t (NULL = the library's stream for
+ * that device).
+ *
+ * Every entry point returns MLQ_OK (0) or a nonzero MLQ_ERR_* code; the message
+ * of the last failure on the calling thread is returned by mlq_hip_last_error().
+ * Messages follow the reference's own wording so callers that match on them
+ * keep working (src/cuda_quant.cu:150-243, 253-255, 299-301).
+ *
+ * Citations name the reference interface each entry replaces (paths relative
+ * to the reference repository).
+ */
+#ifndef MLQ_HIP_H
+#define MLQ_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Quant types, numbered as mini_llama::QuantType
+ * (include/mini_llama/quantized_tensor.h:13-18). */
+#define MLQ_F32 0
+#define MLQ_Q8_0 1
+#define MLQ_Q4_0 2
+#define MLQ_Q4_1 3
+
+/* Bytes per 32-element block: BlockQ8_0 / BlockQ4_0 / BlockQ4_1
+ * (include/mini_llama/quantized_tensor.h:26-59; src/gguf.cpp:178-197). */
+#define MLQ_BLOCK_ELEMS 32
+#define MLQ_Q8_0_BLOCK_BYTES 34
+#define MLQ_Q4_0_BLOCK_BYTES 18
+#define MLQ_Q4_1_BLOCK_BYTES 20
+
+/* Error codes. */
+#define MLQ_OK 0
+#define MLQ_ERR_INVALID 1    /* bad argument: null pointer, unknown type, bad flags  */
+#define MLQ_ERR_SHAPE 2      /* shape or block-count mismatch, empty tensor          */
+#define MLQ_ERR_DEVICE 3     /* no such device / tensor on another device            */
+#define MLQ_ERR_HIP 4        /* a HIP runtime call failed                            */
+#define MLQ_ERR_NOT_BUILT 5  /* library built without kernels for this device        */
+#define MLQ_ERR_LIMIT 6      /* a size exceeds a documented limit                    */
+
+/* Flags for mlq_hip_quant_linear. */
+#define MLQ_X_ON_DEVICE 0x1  /* x is a device pointer (else host, copied in)          */
+#define MLQ_Y_ON_DEVICE 0x2  /* y is a device pointer (else host, copied out)         */
+#define MLQ_ASYNC 0x4        /* device x and y: return without synchronizing          */
+
+typedef struct mlq_weight_s* mlq_weight_t;
+
+/* Thread-local message of the last failure ("" if none). */
+const char* mlq_hip_last_error(void);
+
+/* 1 when the HIP kernels are compiled in (cuda_quant_built,
+ * include/mini_llama/cuda_quant.h:11; cuda_backend_built, backend.h:21). */
+int mlq_hip_built(void);
+
+/* Number of visible HIP devices (cuda_device_count,
+ * include/mini_llama/cuda_runtime.h; used by cuda_backend_available,
+ * src/backend.cpp:34-41). */
+int mlq_hip_device_count(int* count);
+
+/* One-line device summary into buf (cuda_format_device_info /
+ * cuda_device_summary, src/backend.cpp:43-49). */
+int mlq_hip_device_info(int device, char* buf, size_t len);
+
+/* Select `device` for the calling thread and create its stream (the
+ * cudaSetDevice every CudaDeviceBuffer op does, src/cuda_runtime.cpp:187-218). */
+int mlq_hip_init(int device);
+
+/* Copy `n_blocks` raw blocks of an [out_features, in_features] weight from host
+ * memory to `device` and return a handle
+ * (upload_q8_0/q4_0/q4_1_linear_weight, src/model.cpp:145-272; validation
+ * mirrors their messages).  The bytes are stored exactly as given. */
+int mlq_hip_upload_weight(int device, int qtype, const void* host_blocks, size_t n_blocks,
+                          int out_features, int in_features, mlq_weight_t* out);
+
+/* Wrap blocks already resident on `device` (not owned; the caller keeps them
+ * alive).  Mirrors the `const void* q*_device, size_t block_count` pair of
+ * cuda_q*_linear_device_weight / _device_input (include/mini_llama/cuda_quant.h:21-86). */
+int mlq_hip_wrap_weight(int device, int qtype, const void* device_blocks, size_t n_blocks,
+                        int out_features, int in_features, mlq_weight_t* out);
+
+/* Release a handle (and its device memory if uploaded).  NULL is a no-op. */
+int mlq_hip_free_weight(mlq_weight_t w);
+
+/* Properties of a handle; any out pointer may be NULL. */
+int mlq_hip_weight_info(mlq_weight_t w, int* qtype, int* out_features, int* in_features,
+                        size_t* n_blocks, const void** device_blocks, int* device);
+
+/* y[rows, out_features] = x[rows, in_features] * W^T in f32.
+ * rows == 1 is decode (the GEMV kernels); rows > 1 is the batched prefill
+ * GEMM.  With flags 0, x and y are host pointers: x is copied in, y copied back
+ * and the call returns when y is ready (cuda_q*_linear_device_weight,
+ * include/mini_llama/cuda_quant.h:21-28).  With MLQ_X_ON_DEVICE |
+ * MLQ_Y_ON_DEVICE both live on the weight's device
+ * (cuda_q*_linear_device_input, include/mini_llama/cuda_quant.h:30-36); add
+ * MLQ_ASYNC to return right after the launch on `stream`. */
+int mlq_hip_quant_linear(mlq_weight_t w, const float* x, int rows, float* y, int flags,
+                         void* stream);
+
+/* Device-pointer form without a handle: cuda_q8_0/q4_0/q4_1_linear_device_input
+ * (include/mini_llama/cuda_quant.h:30-86, src/cuda_quant.cu:289-496).  x and y
+ * are device pointers on `device`; the call is asynchronous on `stream`. */
+int mlq_hip_quant_linear_device(int device, int qtype, const void* device_blocks, size_t n_blocks,
+                                int out_features, int in_features, const float* x, int rows,
+                                float* y, void* stream);
+
+/* Several independent linears in one call (one launch each, issued from C):
+ * the decode step's per-layer projections without a host round trip per call.
+ * All handles must be on one device; x/y are device pointers. */
+typedef struct mlq_linear_call {
+    mlq_weight_t w;
+    const float* x;
+    float* y;
+    int rows;
+} mlq_linear_call;
+int mlq_hip_quant_linear_many(const mlq_linear_call* calls, int n, void* stream);
+
+/* Quantize an f32 [rows, row_len] matrix that is already on `device` into
+ * blocks on the same device, bit-identical to the reference quantizers:
+ * quantize_to_q8_0 / quantize_to_q4_0 (src/quant.cpp:112-170, 207-270) and
+ * the Q4_1 routine of tests/test_cuda_quant.cpp:129-180 (including its
+ * round-half-up fp16 scale encoding, src/quant.cpp:19-55). */
+int mlq_hip_quantize(int device, int qtype, const float* src, int rows, int row_len,
+                     void* device_blocks, void* stream);
+
+/* ---- device memory, streams, events and graphs (plumbing for callers that
+ * have no HIP runtime of their own, e.g. ctypes/cgo bindings) ---- */
+int mlq_hip_malloc(int device, size_t bytes, void** out);
+int mlq_hip_free(void* ptr);
+int mlq_hip_memcpy_htod(void* dst, const void* src, size_t bytes);
+int mlq_hip_memcpy_dtoh(void* dst, const void* src, size_t bytes);
+int mlq_hip_memcpy_dtod(void* dst, const void* src, size_t bytes, void* stream);
+int mlq_hip_memset(void* ptr, int value, size_t bytes);
+int mlq_hip_stream(int device, void** stream);       /* the library's stream for device */
+int mlq_hip_synchronize(void* stream);
+int mlq_hip_event_create(void** ev);
+int mlq_hip_event_destroy(void* ev);
+int mlq_hip_event_record(void* ev, void* stream);
+int mlq_hip_event_elapsed_ms(void* start, void* stop, float* ms);
+
+/* Capture mlq_hip_quant_linear_many(calls, n) into a graph and instantiate it;
+ * replay with mlq_hip_graph_launch.  Buffers are baked in at capture time. */
+typedef struct mlq_graph_s* mlq_graph_t;
+int mlq_hip_graph_capture_many(const mlq_linear_call* calls, int n, void* stream, mlq_graph_t* out);
+int mlq_hip_graph_launch(mlq_graph_t g, void* stream);
+int mlq_hip_graph_destroy(mlq_graph_t g);
+
+/* Fill an f32 device array with N(mean, std) from a counter-based generator
+ * (splitmix64 + Box-Muller) -- synthetic weights and inputs for benchmarks. */
+int mlq_hip_fill_normal(float* device_dst, size_t n, uint64_t seed, float mean, float stddev,
+                        void* stream);
+
+/* Kernel selection introspection: name of the kernel the next call with this
+ * shape would launch (for profiles and tests). */
+int mlq_hip_kernel_name(int qtype, int rows, int out_features, int in_features, char* buf,
+                        size_t len);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MLQ_HIP_H */

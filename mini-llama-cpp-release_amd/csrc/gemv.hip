@@ -1,0 +1,484 @@
+// Decode GEMV for Q8_0 / Q4_0 / Q4_1 weights on gfx950 (MI355X).
+//
+// y[M] = W[M, K] . x[K], W stored as the reference's 32-element blocks
+// (quantized_tensor.h:26-59), x and y f32.  This replaces the
+// one-thread-per-output kernels of src/cuda_quant.cu:37-137.
+//
+// Layout and work split (the "pair" kernel):
+//  * A *pair* is two consecutive blocks of a row: 36 / 68 / 40 bytes for
+//    Q4_0 / Q8_0 / Q4_1, always a multiple of 4 bytes.  When a row holds an even
+//    number of blocks every pair starts 4-byte aligned, so one lane reads its
+//    pair with 9 / 17 / 10 dword loads and a wavefront covers a contiguous
+//    2.25 / 4.25 / 2.5 KiB of the row: fully coalesced, no repacking of the
+//    stored format.
+//  * LPR lanes share one set of R rows ("slot"); a wave holds 64 / LPR slots,
+//    a workgroup WAVES waves.  Lane l of a slot walks pairs l, l + LPR, ...
+//    of its R rows, so every x element it loads is reused R times.
+//  * x is staged once per workgroup in LDS as f32 (high-nibble halves of Q4
+//    blocks pre-scaled by 1/16, see below) together with per-block constants;
+//    LDS slots are XOR-swizzled so a wave's 16-byte reads hit distinct banks.
+//
+// Arithmetic (VALU, fp32 accumulate; ~1.7 VALU ops per weight):
+//  * A stored nibble or biased byte is turned into an exact fp16 integer with
+//    one AND-OR (or one byte permute) against the fp16 pattern 0x6400 (1024.0):
+//    Q4 low nibble q -> 1024 + q, Q4 high nibble (masked in place) -> 1024 + 16q,
+//    Q8 byte q ^ 0x80 -> 1024 + 128 + q.  Two such values share a dword.
+//  * v_fma_mix_f32 multiplies the fp16 half by the f32 x element and
+//    accumulates in f32; the 1/16 pre-scale of x makes 16q * x/16 == q * x.
+//  * Each block's accumulator starts at -bias, where bias = 1024 * sum(x') +
+//    8 * sum(x) (Q4_0), 1024 * sum(x') (Q4_1), 1152 * sum(x) (Q8_0) is computed
+//    once per workgroup, so the accumulator ends at sum(q_signed * x) for the
+//    block; then y += d * acc (and + m * sum(x) for Q4_1), with d and m read as
+//    fp16 operands of the same fma_mix.
+//  Products are exact; only the f32 accumulations round.  The intermediate
+//  magnitude (~1024 * |partial sum of x|) costs ~10 bits of the f32 sum, i.e.
+//  ~1e-4 relative error per block sum, far inside the 1e-3 tolerance.
+//
+// Rows with an odd block count (pairs would straddle rows) and very long rows
+// go to a simple one-wave-per-row kernel with byte loads.
+
+#include "mlq_kernels.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+
+namespace mlq {
+namespace {
+
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float h_lo(uint32_t v) { return (float)__builtin_bit_cast(h2_t, v).x; }
+__device__ __forceinline__ float h_hi(uint32_t v) { return (float)__builtin_bit_cast(h2_t, v).y; }
+
+constexpr uint32_t kF16Magic2 = 0x64006400u;   // {1024.0h, 1024.0h}
+constexpr uint32_t kF16MagicB = 0x64646464u;   // byte source for v_perm
+
+template <int QT> struct Fmt;
+template <> struct Fmt<1> { static constexpr int BB = 34, DW = 17; };  // Q8_0
+template <> struct Fmt<2> { static constexpr int BB = 18, DW = 9; };   // Q4_0
+template <> struct Fmt<3> { static constexpr int BB = 20, DW = 10; };  // Q4_1
+
+constexpr int kMaxPairLdsBytes = 64 * 1024;
+
+// ---------------------------------------------------------------------------
+// x staging: 8 threads per block, 4 elements each.  Writes x' (f32, Q4 high
+// halves scaled by 1/16) into 16-byte slots swizzled by pair, and per-block
+// constants {c0, c1}:
+//   Q8_0: c0 = 1152 * X          Q4_0: c0 = 1024 * S + 8 * X
+//   Q4_1: c0 = 1024 * S, c1 = X  with X = sum(x), S = sum(x') over the block.
+// Elements past K read as 0, so a partial last block contributes nothing
+// (the reference loops only k < K, src/quant.cpp:421-426).
+template <int QT>
+__device__ __forceinline__ void stage_x(const float* __restrict__ x, int K, int nb,
+                                        float4* __restrict__ xs4, float2* __restrict__ cb) {
+    const int t = threadIdx.x;
+    const int groups = blockDim.x >> 3;
+    const int j = t & 7;
+    for (int g = t >> 3; g < nb; g += groups) {
+        const int k0 = g * kQK + 4 * j;
+        float4 v;
+        v.x = (k0 + 0 < K) ? x[k0 + 0] : 0.0f;
+        v.y = (k0 + 1 < K) ? x[k0 + 1] : 0.0f;
+        v.z = (k0 + 2 < K) ? x[k0 + 2] : 0.0f;
+        v.w = (k0 + 3 < K) ? x[k0 + 3] : 0.0f;
+        const float sc = (QT != 1 && j >= 4) ? 0.0625f : 1.0f;
+        float4 xp;
+        xp.x = v.x * sc;
+        xp.y = v.y * sc;
+        xp.z = v.z * sc;
+        xp.w = v.w * sc;
+        float X = (v.x + v.y) + (v.z + v.w);
+        float S = (xp.x + xp.y) + (xp.z + xp.w);
+#pragma unroll
+        for (int o = 1; o < 8; o <<= 1) {
+            X += __shfl_xor(X, o, 64);
+            S += __shfl_xor(S, o, 64);
+        }
+        const int p = g >> 1;
+        const int slot = ((g & 1) << 3) + j;
+        xs4[p * 16 + (slot ^ (p & 15))] = xp;
+        if (j == 0) {
+            float2 c;
+            if (QT == 1) {
+                c.x = 1152.0f * X;
+                c.y = 0.0f;
+            } else if (QT == 2) {
+                c.x = 1024.0f * S + 8.0f * X;
+                c.y = 0.0f;
+            } else {
+                c.x = 1024.0f * S;
+                c.y = X;
+            }
+            cb[g] = c;
+        }
+    }
+}
+
+// Bit patterns the nibble expansion needs, held in VGPRs: gfx9 VOP3 encodings
+// take no literal, so only register operands let (d & mask) | magic issue as a
+// single v_and_or_b32.  The empty asm makes the values opaque to the compiler,
+// which would otherwise rematerialise them as literals of two VOP2 ops.
+struct NibConsts {
+    uint32_t lo;     // 0x000F000F: low nibbles of bytes 0 and 2
+    uint32_t hi;     // 0x00F000F0: high nibbles of bytes 0 and 2, in place
+    uint32_t magic;  // 0x64006400
+    __device__ __forceinline__ static NibConsts make() {
+        NibConsts c{0x000F000Fu, 0x00F000F0u, kF16Magic2};
+        asm volatile("" : "+v"(c.lo), "+v"(c.hi), "+v"(c.magic));
+        return c;
+    }
+};
+
+// One dword of Q4 nibbles: bytes hold qs[j0..j3] of one block (low nibble =
+// element j, high nibble = element j + 16, src/quant.cpp:259, 442-447).
+template <int J0, int J1, int J2, int J3, int BASE>
+__device__ __forceinline__ float nib_dot(uint32_t d, const float* xv, float a, const NibConsts& k) {
+    const uint32_t lo02 = (d & k.lo) | k.magic;
+    const uint32_t hi02 = (d & k.hi) | k.magic;
+    const uint32_t d8 = d >> 8;
+    const uint32_t lo13 = (d8 & k.lo) | k.magic;
+    const uint32_t hi13 = (d8 & k.hi) | k.magic;
+    a = __builtin_fmaf(h_lo(lo02), xv[BASE + J0], a);
+    a = __builtin_fmaf(h_hi(lo02), xv[BASE + J2], a);
+    a = __builtin_fmaf(h_lo(hi02), xv[BASE + J0 + 16], a);
+    a = __builtin_fmaf(h_hi(hi02), xv[BASE + J2 + 16], a);
+    a = __builtin_fmaf(h_lo(lo13), xv[BASE + J1], a);
+    a = __builtin_fmaf(h_hi(lo13), xv[BASE + J3], a);
+    a = __builtin_fmaf(h_lo(hi13), xv[BASE + J1 + 16], a);
+    a = __builtin_fmaf(h_hi(hi13), xv[BASE + J3 + 16], a);
+    return a;
+}
+
+// One dword of Q8_0 bytes qs[j0..j3].
+template <int J0, int J1, int J2, int J3, int BASE>
+__device__ __forceinline__ float byte_dot(uint32_t d, const float* xv, float a) {
+    const uint32_t dx = d ^ 0x80808080u;
+    const uint32_t p01 = __builtin_amdgcn_perm(kF16MagicB, dx, 0x04010400u);
+    const uint32_t p23 = __builtin_amdgcn_perm(kF16MagicB, dx, 0x04030402u);
+    a = __builtin_fmaf(h_lo(p01), xv[BASE + J0], a);
+    a = __builtin_fmaf(h_hi(p01), xv[BASE + J1], a);
+    a = __builtin_fmaf(h_lo(p23), xv[BASE + J2], a);
+    a = __builtin_fmaf(h_hi(p23), xv[BASE + J3], a);
+    return a;
+}
+
+// acc += contribution of one pair (two blocks) of one row.
+template <int QT> struct PairDot;
+
+template <> struct PairDot<2> {  // Q4_0: w0 = {d0, qs0[0..1]}, w4 = {qs0[14..15], d1}
+    __device__ __forceinline__ static float run(const uint32_t* w, const float* xv, float2 c0,
+                                                float2 c1, float acc, const NibConsts& k) {
+        const uint32_t t = __builtin_amdgcn_perm(w[4], w[0], 0x05040302u);  // qs0[0,1,14,15]
+        float a = -c0.x;
+        a = nib_dot<0, 1, 14, 15, 0>(t, xv, a, k);
+        a = nib_dot<2, 3, 4, 5, 0>(w[1], xv, a, k);
+        a = nib_dot<6, 7, 8, 9, 0>(w[2], xv, a, k);
+        a = nib_dot<10, 11, 12, 13, 0>(w[3], xv, a, k);
+        acc = __builtin_fmaf(h_lo(w[0]), a, acc);
+        float b = -c1.x;
+        b = nib_dot<0, 1, 2, 3, 32>(w[5], xv, b, k);
+        b = nib_dot<4, 5, 6, 7, 32>(w[6], xv, b, k);
+        b = nib_dot<8, 9, 10, 11, 32>(w[7], xv, b, k);
+        b = nib_dot<12, 13, 14, 15, 32>(w[8], xv, b, k);
+        acc = __builtin_fmaf(h_hi(w[4]), b, acc);
+        return acc;
+    }
+};
+
+template <> struct PairDot<3> {  // Q4_1: w0 = {d0, m0}, w5 = {d1, m1}
+    __device__ __forceinline__ static float run(const uint32_t* w, const float* xv, float2 c0,
+                                                float2 c1, float acc, const NibConsts& k) {
+        float a = -c0.x;
+        a = nib_dot<0, 1, 2, 3, 0>(w[1], xv, a, k);
+        a = nib_dot<4, 5, 6, 7, 0>(w[2], xv, a, k);
+        a = nib_dot<8, 9, 10, 11, 0>(w[3], xv, a, k);
+        a = nib_dot<12, 13, 14, 15, 0>(w[4], xv, a, k);
+        acc = __builtin_fmaf(h_lo(w[0]), a, acc);
+        acc = __builtin_fmaf(h_hi(w[0]), c0.y, acc);
+        float b = -c1.x;
+        b = nib_dot<0, 1, 2, 3, 32>(w[6], xv, b, k);
+        b = nib_dot<4, 5, 6, 7, 32>(w[7], xv, b, k);
+        b = nib_dot<8, 9, 10, 11, 32>(w[8], xv, b, k);
+        b = nib_dot<12, 13, 14, 15, 32>(w[9], xv, b, k);
+        acc = __builtin_fmaf(h_lo(w[5]), b, acc);
+        acc = __builtin_fmaf(h_hi(w[5]), c1.y, acc);
+        return acc;
+    }
+};
+
+template <> struct PairDot<1> {  // Q8_0: w0 = {d0, qs0[0..1]}, w8 = {qs0[30..31], d1}
+    __device__ __forceinline__ static float run(const uint32_t* w, const float* xv, float2 c0,
+                                                float2 c1, float acc, const NibConsts&) {
+        const uint32_t t = __builtin_amdgcn_perm(w[8], w[0], 0x05040302u);  // qs0[0,1,30,31]
+        float a = -c0.x;
+        a = byte_dot<0, 1, 30, 31, 0>(t, xv, a);
+        a = byte_dot<2, 3, 4, 5, 0>(w[1], xv, a);
+        a = byte_dot<6, 7, 8, 9, 0>(w[2], xv, a);
+        a = byte_dot<10, 11, 12, 13, 0>(w[3], xv, a);
+        a = byte_dot<14, 15, 16, 17, 0>(w[4], xv, a);
+        a = byte_dot<18, 19, 20, 21, 0>(w[5], xv, a);
+        a = byte_dot<22, 23, 24, 25, 0>(w[6], xv, a);
+        a = byte_dot<26, 27, 28, 29, 0>(w[7], xv, a);
+        acc = __builtin_fmaf(h_lo(w[0]), a, acc);
+        float b = -c1.x;
+        b = byte_dot<0, 1, 2, 3, 32>(w[9], xv, b);
+        b = byte_dot<4, 5, 6, 7, 32>(w[10], xv, b);
+        b = byte_dot<8, 9, 10, 11, 32>(w[11], xv, b);
+        b = byte_dot<12, 13, 14, 15, 32>(w[12], xv, b);
+        b = byte_dot<16, 17, 18, 19, 32>(w[13], xv, b);
+        b = byte_dot<20, 21, 22, 23, 32>(w[14], xv, b);
+        b = byte_dot<24, 25, 26, 27, 32>(w[15], xv, b);
+        b = byte_dot<28, 29, 30, 31, 32>(w[16], xv, b);
+        acc = __builtin_fmaf(h_hi(w[8]), b, acc);
+        return acc;
+    }
+};
+
+template <int QT, int LPR, int R, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void gemv_pair_kernel(
+    const uint8_t* __restrict__ W, const float* __restrict__ x, float* __restrict__ y, int M,
+    int K, int nb) {
+    constexpr int DW = Fmt<QT>::DW;
+    constexpr int SUB = 64 / LPR;
+    extern __shared__ float4 lds4[];
+    const int np = nb >> 1;
+    float4* xs4 = lds4;
+    float2* cb = reinterpret_cast<float2*>(lds4 + np * 16);
+
+    x += static_cast<size_t>(blockIdx.y) * K;
+    y += static_cast<size_t>(blockIdx.y) * M;
+
+    stage_x<QT>(x, K, nb, xs4, cb);
+    __syncthreads();
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int slot = lane / LPR;
+    const int pl = lane % LPR;
+    const int row0 = (blockIdx.x * WAVES + wave) * (SUB * R) + slot * R;
+    const size_t row_dw = static_cast<size_t>(np) * DW;  // dwords per row
+
+    const uint32_t* rowp[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int row = min(row0 + r, M - 1);  // rows past M are computed on row M-1 and dropped
+        rowp[r] = reinterpret_cast<const uint32_t*>(W) + static_cast<size_t>(row) * row_dw;
+    }
+
+    const NibConsts nk = NibConsts::make();
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+
+    for (int p = pl; p < np; p += LPR) {
+        uint32_t w[R][DW];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint32_t* src = rowp[r] + static_cast<size_t>(p) * DW;
+#pragma unroll
+            for (int i = 0; i < DW; ++i) w[r][i] = __builtin_nontemporal_load(src + i);
+        }
+        float xv[64];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const float4 v = xs4[p * 16 + (i ^ (p & 15))];
+            xv[4 * i + 0] = v.x;
+            xv[4 * i + 1] = v.y;
+            xv[4 * i + 2] = v.z;
+            xv[4 * i + 3] = v.w;
+        }
+        const float2 c0 = cb[2 * p];
+        const float2 c1 = cb[2 * p + 1];
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r] = PairDot<QT>::run(w[r], xv, c0, c1, acc[r], nk);
+    }
+
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+#pragma unroll
+        for (int o = LPR / 2; o > 0; o >>= 1) acc[r] += __shfl_xor(acc[r], o, 64);
+    }
+    if (pl < R) {
+        float v = acc[0];
+#pragma unroll
+        for (int r = 1; r < R; ++r) v = (pl == r) ? acc[r] : v;
+        const int row = row0 + pl;
+        if (row < M) y[row] = v;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Generic kernel: one wave per output row, lanes over blocks, byte loads.
+// Handles every shape (odd block counts, K beyond the LDS budget).
+template <int QT>
+__global__ __launch_bounds__(256) void gemv_generic_kernel(const uint8_t* __restrict__ W,
+                                                           const float* __restrict__ x,
+                                                           float* __restrict__ y, int M, int K,
+                                                           int nb) {
+    constexpr int BB = Fmt<QT>::BB;
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= M) return;
+    x += static_cast<size_t>(blockIdx.y) * K;
+    y += static_cast<size_t>(blockIdx.y) * M;
+    float acc = 0.0f;
+    for (int b = lane; b < nb; b += 64) {
+        const uint8_t* blk = W + (static_cast<size_t>(row) * nb + b) * BB;
+        const uint16_t dbits = static_cast<uint16_t>(blk[0] | (blk[1] << 8));
+        const float d = (float)__builtin_bit_cast(_Float16, dbits);
+        const int k0 = b * kQK;
+        const int len = min(kQK, K - k0);
+        float s = 0.0f;
+        float sx = 0.0f;
+        for (int i = 0; i < len; ++i) {
+            float q;
+            if (QT == 1) {
+                q = static_cast<float>(static_cast<int8_t>(blk[2 + i]));
+            } else {
+                const int off = (QT == 2) ? 2 : 4;
+                const uint8_t byte = blk[off + (i & 15)];
+                const int nib = (i < 16) ? (byte & 15) : (byte >> 4);
+                q = static_cast<float>(QT == 2 ? nib - 8 : nib);
+            }
+            s = __builtin_fmaf(q, x[k0 + i], s);
+            sx += x[k0 + i];
+        }
+        acc = __builtin_fmaf(d, s, acc);
+        if (QT == 3) {
+            const uint16_t mbits = static_cast<uint16_t>(blk[2] | (blk[3] << 8));
+            acc = __builtin_fmaf((float)__builtin_bit_cast(_Float16, mbits), sx, acc);
+        }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+    if (lane == 0) y[row] = acc;
+}
+
+// ---------------------------------------------------------------------------
+// Host-side selection.
+
+struct PairCfg {
+    int lpr;
+    int r;
+    bool ok;
+};
+
+constexpr int kWaves = 8;
+
+int pair_lds_bytes(int nb) { return (nb / 2) * 256 + nb * 8; }
+
+PairCfg choose_pair(const LinearShape& s) {
+    PairCfg c{64, 1, false};
+    if (s.nb % 2 != 0 || pair_lds_bytes(s.nb) > kMaxPairLdsBytes) return c;
+    const int np = s.nb / 2;
+    // Lanes per row: the widest group whose last sweep over the pairs leaves at
+    // most ~12% of lanes idle; else the most efficient one.
+    const int cands[4] = {64, 32, 16, 8};
+    double best_eff = -1.0;
+    int best = 64;
+    for (int lpr : cands) {
+        const int iters = (np + lpr - 1) / lpr;
+        const double eff = static_cast<double>(np) / (static_cast<double>(lpr) * iters);
+        if (eff >= 0.875) {
+            best = lpr;
+            best_eff = eff;
+            break;
+        }
+        if (eff > best_eff + 1e-9) {
+            best_eff = eff;
+            best = lpr;
+        }
+    }
+    c.lpr = best;
+    // Rows per slot: reuse each staged x element over more rows while the grid
+    // still has >= 2 workgroups per CU (256 CUs on MI355X).
+    const int sub = 64 / best;
+    c.r = 1;
+    for (int r : {4, 2}) {
+        const long long rows_per_wg = static_cast<long long>(kWaves) * sub * r;
+        if ((s.M + rows_per_wg - 1) / rows_per_wg >= 512) {
+            c.r = r;
+            break;
+        }
+    }
+    c.ok = true;
+    return c;
+}
+
+template <int QT, int LPR, int R>
+hipError_t launch_pair_t(const LinearShape& s, const void* w, const float* x, float* y,
+                         hipStream_t stream) {
+    constexpr int rows_per_wg = kWaves * (64 / LPR) * R;
+    dim3 grid((s.M + rows_per_wg - 1) / rows_per_wg, s.rows);
+    dim3 block(kWaves * 64);
+    hipLaunchKernelGGL((gemv_pair_kernel<QT, LPR, R, kWaves>), grid, block, pair_lds_bytes(s.nb),
+                       stream, static_cast<const uint8_t*>(w), x, y, s.M, s.K, s.nb);
+    return hipGetLastError();
+}
+
+template <int QT, int LPR>
+hipError_t launch_pair_r(const LinearShape& s, int r, const void* w, const float* x, float* y,
+                         hipStream_t stream) {
+    switch (r) {
+        case 4: return launch_pair_t<QT, LPR, 4>(s, w, x, y, stream);
+        case 2: return launch_pair_t<QT, LPR, 2>(s, w, x, y, stream);
+        default: return launch_pair_t<QT, LPR, 1>(s, w, x, y, stream);
+    }
+}
+
+template <int QT>
+hipError_t launch_pair_q(const LinearShape& s, const PairCfg& c, const void* w, const float* x,
+                         float* y, hipStream_t stream) {
+    switch (c.lpr) {
+        case 64: return launch_pair_r<QT, 64>(s, c.r, w, x, y, stream);
+        case 32: return launch_pair_r<QT, 32>(s, c.r, w, x, y, stream);
+        case 16: return launch_pair_r<QT, 16>(s, c.r, w, x, y, stream);
+        default: return launch_pair_r<QT, 8>(s, c.r, w, x, y, stream);
+    }
+}
+
+template <int QT>
+hipError_t launch_generic_q(const LinearShape& s, const void* w, const float* x, float* y,
+                            hipStream_t stream) {
+    dim3 grid((s.M + 3) / 4, s.rows);
+    hipLaunchKernelGGL((gemv_generic_kernel<QT>), grid, dim3(256), 0, stream,
+                       static_cast<const uint8_t*>(w), x, y, s.M, s.K, s.nb);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_gemv(const LinearShape& s, const void* w, const float* x, float* y,
+                       hipStream_t stream) {
+    const PairCfg c = choose_pair(s);
+    if (c.ok) {
+        switch (s.qtype) {
+            case 1: return launch_pair_q<1>(s, c, w, x, y, stream);
+            case 2: return launch_pair_q<2>(s, c, w, x, y, stream);
+            case 3: return launch_pair_q<3>(s, c, w, x, y, stream);
+            default: return hipErrorInvalidValue;
+        }
+    }
+    switch (s.qtype) {
+        case 1: return launch_generic_q<1>(s, w, x, y, stream);
+        case 2: return launch_generic_q<2>(s, w, x, y, stream);
+        case 3: return launch_generic_q<3>(s, w, x, y, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+const char* gemv_kernel_name(const LinearShape& s) {
+    static thread_local char buf[96];
+    const char* fmt = s.qtype == 1 ? "q8_0" : s.qtype == 2 ? "q4_0" : "q4_1";
+    const PairCfg c = choose_pair(s);
+    if (c.ok) {
+        snprintf(buf, sizeof buf, "gemv_pair_%s_lpr%d_r%d_w%d", fmt, c.lpr, c.r, kWaves);
+    } else {
+        snprintf(buf, sizeof buf, "gemv_generic_%s", fmt);
+    }
+    return buf;
+}
+
+}  // namespace mlq

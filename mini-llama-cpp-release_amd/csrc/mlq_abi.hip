@@ -1,0 +1,576 @@
+// C-ABI of the MI355X quantized-linear path (declared in include/mlq_hip.h).
+//
+// Validation order and messages mirror the reference's CUDA wrappers
+// (src/cuda_quant.cu:150-243 shape checks, :253-255 null weight, :299-301
+// device mismatch) and weight upload (src/model.cpp:145-272), with "cuda"
+// replaced by "hip".  Every check runs on the host before any launch, so a
+// malformed call never reaches a kernel.
+
+#include "mlq_kernels.h"
+
+#include "../../include/mlq_hip.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+struct mlq_weight_s {
+    int device;
+    int qtype;
+    int M;
+    int K;
+    int nb;
+    size_t n_blocks;
+    void* ptr;
+    bool owned;
+};
+
+struct mlq_graph_s {
+    hipGraph_t graph;
+    hipGraphExec_t exec;
+    int device;
+};
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int code, const std::string& msg) {
+    g_error = msg;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    return fail(MLQ_ERR_HIP, std::string("HIP error in ") + what + ": " + hipGetErrorString(e));
+}
+
+#define MLQ_HIP_CHECK(expr)                                   \
+    do {                                                      \
+        hipError_t mlq_e_ = (expr);                           \
+        if (mlq_e_ != hipSuccess) return hip_fail(mlq_e_, #expr); \
+    } while (0)
+
+constexpr int kMaxDevices = 64;
+
+struct DeviceState {
+    std::once_flag once;
+    hipError_t init_err = hipSuccess;
+    hipStream_t stream = nullptr;
+    std::mutex mu;             // guards the host-pointer staging buffers
+    void* stage = nullptr;     // x and y staging for host-pointer calls
+    size_t stage_bytes = 0;
+};
+
+DeviceState g_dev[kMaxDevices];
+
+const char* caller_for(int qtype) {
+    switch (qtype) {
+        case MLQ_Q8_0: return "hip_q8_0_linear";
+        case MLQ_Q4_0: return "hip_q4_0_linear";
+        case MLQ_Q4_1: return "hip_q4_1_linear";
+        default: return "hip_quant_linear";
+    }
+}
+
+const char* type_name(int qtype) {
+    switch (qtype) {
+        case MLQ_Q8_0: return "Q8_0";
+        case MLQ_Q4_0: return "Q4_0";
+        case MLQ_Q4_1: return "Q4_1";
+        default: return "F32";
+    }
+}
+
+int ensure_device(int device) {
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDeviceCount");
+    if (device < 0 || device >= count || device >= kMaxDevices) {
+        return fail(MLQ_ERR_DEVICE, "HIP device " + std::to_string(device) + " is not available (" +
+                                        std::to_string(count) + " visible)");
+    }
+    DeviceState& st = g_dev[device];
+    std::call_once(st.once, [&] {
+        st.init_err = hipSetDevice(device);
+        if (st.init_err == hipSuccess) {
+            // Default priority, non-blocking with respect to the null stream.
+            st.init_err = hipStreamCreateWithFlags(&st.stream, hipStreamNonBlocking);
+        }
+    });
+    if (st.init_err != hipSuccess) return hip_fail(st.init_err, "device init");
+    e = hipSetDevice(device);
+    if (e != hipSuccess) return hip_fail(e, "hipSetDevice");
+    return MLQ_OK;
+}
+
+hipStream_t resolve_stream(int device, void* stream) {
+    return stream != nullptr ? static_cast<hipStream_t>(stream) : g_dev[device].stream;
+}
+
+// Checks that `p` is device memory on `device` (device or managed allocation).
+// A host pointer handed over as a device pointer would fault the GPU, so this
+// runs before every launch that takes caller pointers.
+int check_device_ptr(const void* p, int device, const char* caller, const char* what) {
+    if (p == nullptr) return fail(MLQ_ERR_INVALID, std::string(caller) + ": " + what + " pointer is null");
+    hipPointerAttribute_t attr;
+    std::memset(&attr, 0, sizeof attr);
+    hipError_t e = hipPointerGetAttributes(&attr, p);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();  // clear the sticky error of a failed lookup
+        return fail(MLQ_ERR_DEVICE, std::string(caller) + ": " + what + " is not a HIP device pointer");
+    }
+    if (attr.type != hipMemoryTypeDevice && attr.type != hipMemoryTypeManaged) {
+        return fail(MLQ_ERR_DEVICE, std::string(caller) + ": " + what + " is not a HIP device pointer");
+    }
+    if (attr.device != device) {
+        return fail(MLQ_ERR_DEVICE, std::string(caller) + ": " + what +
+                                        " tensor is on a different HIP device");
+    }
+    return MLQ_OK;
+}
+
+// src/cuda_quant.cu:214-243 for the device-weight linear.
+int validate_linear(int qtype, int M, int K, size_t n_blocks, int rows) {
+    const char* caller = caller_for(qtype);
+    if (qtype != MLQ_Q8_0 && qtype != MLQ_Q4_0 && qtype != MLQ_Q4_1) {
+        return fail(MLQ_ERR_INVALID, std::string(caller) + ": unsupported quant type " + std::to_string(qtype));
+    }
+    if (rows <= 0 || K <= 0 || M <= 0) {
+        return fail(MLQ_ERR_SHAPE, std::string(caller) + ": empty tensors are not supported");
+    }
+    const int nb = (K + mlq::kQK - 1) / mlq::kQK;
+    const size_t expected = static_cast<size_t>(M) * nb;
+    if (n_blocks != expected) {
+        return fail(MLQ_ERR_SHAPE, std::string(caller) + ": block count mismatch: expected " +
+                                       std::to_string(expected) + ", got " + std::to_string(n_blocks));
+    }
+    // Indices inside the kernels are 32-bit for rows and dwords per row.
+    if (static_cast<long long>(nb) * mlq::block_bytes(qtype) >= (1ll << 31) || rows > 65535) {
+        return fail(MLQ_ERR_LIMIT, std::string(caller) + ": shape exceeds the kernel limits");
+    }
+    return MLQ_OK;
+}
+
+hipError_t dispatch(const mlq::LinearShape& s, const void* w, const float* x, float* y,
+                    hipStream_t stream) {
+    if (s.rows > 1 && mlq::gemm_supported(s)) return mlq::launch_gemm(s, w, x, y, stream);
+    return mlq::launch_gemv(s, w, x, y, stream);
+}
+
+int grow_stage(DeviceState& st, size_t bytes) {
+    if (st.stage_bytes >= bytes) return MLQ_OK;
+    if (st.stage != nullptr) {
+        MLQ_HIP_CHECK(hipStreamSynchronize(st.stream));
+        MLQ_HIP_CHECK(hipFree(st.stage));
+        st.stage = nullptr;
+        st.stage_bytes = 0;
+    }
+    size_t cap = 1 << 20;
+    while (cap < bytes) cap <<= 1;
+    MLQ_HIP_CHECK(hipMalloc(&st.stage, cap));
+    st.stage_bytes = cap;
+    return MLQ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* mlq_hip_last_error(void) { return g_error.c_str(); }
+
+int mlq_hip_built(void) { return 1; }
+
+int mlq_hip_device_count(int* count) {
+    if (count == nullptr) return fail(MLQ_ERR_INVALID, "mlq_hip_device_count: null output");
+    *count = 0;
+    hipError_t e = hipGetDeviceCount(count);
+    if (e == hipErrorNoDevice) {
+        *count = 0;
+        (void)hipGetLastError();
+        return MLQ_OK;
+    }
+    if (e != hipSuccess) return hip_fail(e, "hipGetDeviceCount");
+    return MLQ_OK;
+}
+
+int mlq_hip_device_info(int device, char* buf, size_t len) {
+    int rc = ensure_device(device);
+    if (rc != MLQ_OK) return rc;
+    hipDeviceProp_t p;
+    MLQ_HIP_CHECK(hipGetDeviceProperties(&p, device));
+    if (buf != nullptr && len > 0) {
+        std::snprintf(buf, len, "HIP device %d: %s (%s), %d CUs, %.1f GiB HBM, LDS %zu KiB/CU",
+                      device, p.name, p.gcnArchName, p.multiProcessorCount,
+                      static_cast<double>(p.totalGlobalMem) / (1024.0 * 1024.0 * 1024.0),
+                      static_cast<size_t>(p.maxSharedMemoryPerMultiProcessor) / 1024);
+    }
+    return MLQ_OK;
+}
+
+int mlq_hip_init(int device) { return ensure_device(device); }
+
+int mlq_hip_upload_weight(int device, int qtype, const void* host_blocks, size_t n_blocks,
+                          int out_features, int in_features, mlq_weight_t* out) {
+    if (out == nullptr) return fail(MLQ_ERR_INVALID, "HIP weight upload: null output handle");
+    *out = nullptr;
+    if (qtype != MLQ_Q8_0 && qtype != MLQ_Q4_0 && qtype != MLQ_Q4_1) {
+        return fail(MLQ_ERR_INVALID, "HIP weight upload: unsupported quant type " + std::to_string(qtype));
+    }
+    if (out_features <= 0 || in_features <= 0) {
+        return fail(MLQ_ERR_SHAPE, std::string("HIP weight upload: expected 2D ") + type_name(qtype) + " weight");
+    }
+    if (host_blocks == nullptr || n_blocks == 0) {
+        return fail(MLQ_ERR_SHAPE, std::string("HIP weight upload: empty ") + type_name(qtype) + " data");
+    }
+    const int nb = (in_features + mlq::kQK - 1) / mlq::kQK;
+    const size_t expected = static_cast<size_t>(out_features) * nb;
+    if (n_blocks != expected) {
+        return fail(MLQ_ERR_SHAPE, std::string("HIP weight upload: ") + type_name(qtype) +
+                                       " block count mismatch, expected " + std::to_string(expected) +
+                                       ", got " + std::to_string(n_blocks));
+    }
+    int rc = ensure_device(device);
+    if (rc != MLQ_OK) return rc;
+    const size_t bytes = n_blocks * static_cast<size_t>(mlq::block_bytes(qtype));
+    void* ptr = nullptr;
+    MLQ_HIP_CHECK(hipMalloc(&ptr, bytes));
+    hipError_t e = hipMemcpy(ptr, host_blocks, bytes, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        (void)hipFree(ptr);
+        return hip_fail(e, "hipMemcpy(weight)");
+    }
+    *out = new mlq_weight_s{device, qtype, out_features, in_features, nb, n_blocks, ptr, true};
+    return MLQ_OK;
+}
+
+int mlq_hip_wrap_weight(int device, int qtype, const void* device_blocks, size_t n_blocks,
+                        int out_features, int in_features, mlq_weight_t* out) {
+    if (out == nullptr) return fail(MLQ_ERR_INVALID, "mlq_hip_wrap_weight: null output handle");
+    *out = nullptr;
+    const char* caller = caller_for(qtype);
+    if (device_blocks == nullptr) {
+        return fail(MLQ_ERR_INVALID, std::string(caller) + ": device weight pointer is null");
+    }
+    int rc = validate_linear(qtype, out_features, in_features, n_blocks, 1);
+    if (rc != MLQ_OK) return rc;
+    rc = ensure_device(device);
+    if (rc != MLQ_OK) return rc;
+    rc = check_device_ptr(device_blocks, device, caller, "device weight");
+    if (rc != MLQ_OK) return rc;
+    const int nb = (in_features + mlq::kQK - 1) / mlq::kQK;
+    *out = new mlq_weight_s{device, qtype, out_features, in_features, nb, n_blocks,
+                            const_cast<void*>(device_blocks), false};
+    return MLQ_OK;
+}
+
+int mlq_hip_free_weight(mlq_weight_t w) {
+    if (w == nullptr) return MLQ_OK;
+    if (w->owned && w->ptr != nullptr) {
+        (void)hipSetDevice(w->device);
+        hipError_t e = hipFree(w->ptr);
+        delete w;
+        if (e != hipSuccess) return hip_fail(e, "hipFree(weight)");
+        return MLQ_OK;
+    }
+    delete w;
+    return MLQ_OK;
+}
+
+int mlq_hip_weight_info(mlq_weight_t w, int* qtype, int* out_features, int* in_features,
+                        size_t* n_blocks, const void** device_blocks, int* device) {
+    if (w == nullptr) return fail(MLQ_ERR_INVALID, "mlq_hip_weight_info: null handle");
+    if (qtype) *qtype = w->qtype;
+    if (out_features) *out_features = w->M;
+    if (in_features) *in_features = w->K;
+    if (n_blocks) *n_blocks = w->n_blocks;
+    if (device_blocks) *device_blocks = w->ptr;
+    if (device) *device = w->device;
+    return MLQ_OK;
+}
+
+int mlq_hip_quant_linear_device(int device, int qtype, const void* device_blocks, size_t n_blocks,
+                                int out_features, int in_features, const float* x, int rows,
+                                float* y, void* stream) {
+    const char* caller = caller_for(qtype);
+    if (device_blocks == nullptr) {
+        return fail(MLQ_ERR_INVALID, std::string(caller) + ": device weight pointer is null");
+    }
+    int rc = validate_linear(qtype, out_features, in_features, n_blocks, rows);
+    if (rc != MLQ_OK) return rc;
+    rc = ensure_device(device);
+    if (rc != MLQ_OK) return rc;
+    if ((rc = check_device_ptr(device_blocks, device, caller, "device weight")) != MLQ_OK) return rc;
+    if ((rc = check_device_ptr(x, device, caller, "input")) != MLQ_OK) return rc;
+    if ((rc = check_device_ptr(y, device, caller, "output")) != MLQ_OK) return rc;
+    mlq::LinearShape s{qtype, out_features, in_features, (in_features + 31) / 32, rows};
+    hipError_t e = dispatch(s, device_blocks, x, y, resolve_stream(device, stream));
+    if (e != hipSuccess) return hip_fail(e, caller);
+    return MLQ_OK;
+}
+
+int mlq_hip_quant_linear(mlq_weight_t w, const float* x, int rows, float* y, int flags,
+                         void* stream) {
+    if (w == nullptr) return fail(MLQ_ERR_INVALID, "hip_quant_linear: null weight handle");
+    const char* caller = caller_for(w->qtype);
+    if (flags & ~(MLQ_X_ON_DEVICE | MLQ_Y_ON_DEVICE | MLQ_ASYNC)) {
+        return fail(MLQ_ERR_INVALID, std::string(caller) + ": unknown flags");
+    }
+    if (x == nullptr) return fail(MLQ_ERR_INVALID, std::string(caller) + ": input pointer is null");
+    if (y == nullptr) return fail(MLQ_ERR_INVALID, std::string(caller) + ": output pointer is null");
+    int rc = validate_linear(w->qtype, w->M, w->K, w->n_blocks, rows);
+    if (rc != MLQ_OK) return rc;
+    rc = ensure_device(w->device);
+    if (rc != MLQ_OK) return rc;
+    DeviceState& st = g_dev[w->device];
+    hipStream_t s = resolve_stream(w->device, stream);
+    mlq::LinearShape shape{w->qtype, w->M, w->K, w->nb, rows};
+    const size_t xb = static_cast<size_t>(rows) * w->K * sizeof(float);
+    const size_t yb = static_cast<size_t>(rows) * w->M * sizeof(float);
+
+    const bool xd = flags & MLQ_X_ON_DEVICE;
+    const bool yd = flags & MLQ_Y_ON_DEVICE;
+    if (xd && (rc = check_device_ptr(x, w->device, caller, "input")) != MLQ_OK) return rc;
+    if (yd && (rc = check_device_ptr(y, w->device, caller, "output")) != MLQ_OK) return rc;
+    if (xd && yd) {
+        hipError_t e = dispatch(shape, w->ptr, x, y, s);
+        if (e != hipSuccess) return hip_fail(e, caller);
+        if (!(flags & MLQ_ASYNC)) MLQ_HIP_CHECK(hipStreamSynchronize(s));
+        return MLQ_OK;
+    }
+    // Host x and/or y: stage through the device's buffer (x first, 256-B aligned y).
+    std::lock_guard<std::mutex> lock(st.mu);
+    const size_t xoff = 0;
+    const size_t yoff = (xb + 255) & ~static_cast<size_t>(255);
+    if ((rc = grow_stage(st, yoff + yb)) != MLQ_OK) return rc;
+    char* base = static_cast<char*>(st.stage);
+    const float* xdev = x;
+    float* ydev = y;
+    if (!xd) {
+        MLQ_HIP_CHECK(hipMemcpyAsync(base + xoff, x, xb, hipMemcpyHostToDevice, s));
+        xdev = reinterpret_cast<const float*>(base + xoff);
+    }
+    if (!yd) ydev = reinterpret_cast<float*>(base + yoff);
+    hipError_t e = dispatch(shape, w->ptr, xdev, ydev, s);
+    if (e != hipSuccess) return hip_fail(e, caller);
+    if (!yd) MLQ_HIP_CHECK(hipMemcpyAsync(y, ydev, yb, hipMemcpyDeviceToHost, s));
+    MLQ_HIP_CHECK(hipStreamSynchronize(s));
+    return MLQ_OK;
+}
+
+int mlq_hip_quant_linear_many(const mlq_linear_call* calls, int n, void* stream) {
+    if (calls == nullptr || n <= 0) return fail(MLQ_ERR_INVALID, "mlq_hip_quant_linear_many: no calls");
+    const int device = calls[0].w != nullptr ? calls[0].w->device : -1;
+    for (int i = 0; i < n; ++i) {
+        const mlq_linear_call& c = calls[i];
+        if (c.w == nullptr) return fail(MLQ_ERR_INVALID, "mlq_hip_quant_linear_many: null weight handle");
+        if (c.w->device != device) {
+            return fail(MLQ_ERR_DEVICE, "mlq_hip_quant_linear_many: weights on different devices");
+        }
+        int rc = validate_linear(c.w->qtype, c.w->M, c.w->K, c.w->n_blocks, c.rows);
+        if (rc != MLQ_OK) return rc;
+    }
+    int rc = ensure_device(device);
+    if (rc != MLQ_OK) return rc;
+    for (int i = 0; i < n; ++i) {
+        const char* caller = caller_for(calls[i].w->qtype);
+        if ((rc = check_device_ptr(calls[i].x, device, caller, "input")) != MLQ_OK) return rc;
+        if ((rc = check_device_ptr(calls[i].y, device, caller, "output")) != MLQ_OK) return rc;
+    }
+    hipStream_t s = resolve_stream(device, stream);
+    for (int i = 0; i < n; ++i) {
+        const mlq_linear_call& c = calls[i];
+        mlq::LinearShape shape{c.w->qtype, c.w->M, c.w->K, c.w->nb, c.rows};
+        hipError_t e = dispatch(shape, c.w->ptr, c.x, c.y, s);
+        if (e != hipSuccess) return hip_fail(e, caller_for(c.w->qtype));
+    }
+    return MLQ_OK;
+}
+
+int mlq_hip_quantize(int device, int qtype, const float* src, int rows, int row_len,
+                     void* device_blocks, void* stream) {
+    if (qtype != MLQ_Q8_0 && qtype != MLQ_Q4_0 && qtype != MLQ_Q4_1) {
+        return fail(MLQ_ERR_INVALID, "mlq_hip_quantize: unsupported quant type " + std::to_string(qtype));
+    }
+    if (rows <= 0 || row_len <= 0) return fail(MLQ_ERR_SHAPE, "mlq_hip_quantize: empty tensors are not supported");
+    int rc = ensure_device(device);
+    if (rc != MLQ_OK) return rc;
+    if ((rc = check_device_ptr(src, device, "mlq_hip_quantize", "source")) != MLQ_OK) return rc;
+    if ((rc = check_device_ptr(device_blocks, device, "mlq_hip_quantize", "block")) != MLQ_OK) return rc;
+    hipError_t e = mlq::launch_quantize(qtype, src, rows, row_len, device_blocks, resolve_stream(device, stream));
+    if (e != hipSuccess) return hip_fail(e, "quantize_kernel");
+    return MLQ_OK;
+}
+
+int mlq_hip_malloc(int device, size_t bytes, void** out) {
+    if (out == nullptr) return fail(MLQ_ERR_INVALID, "mlq_hip_malloc: null output");
+    *out = nullptr;
+    int rc = ensure_device(device);
+    if (rc != MLQ_OK) return rc;
+    MLQ_HIP_CHECK(hipMalloc(out, bytes == 0 ? 1 : bytes));
+    return MLQ_OK;
+}
+
+int mlq_hip_free(void* ptr) {
+    if (ptr == nullptr) return MLQ_OK;
+    MLQ_HIP_CHECK(hipFree(ptr));
+    return MLQ_OK;
+}
+
+int mlq_hip_memcpy_htod(void* dst, const void* src, size_t bytes) {
+    MLQ_HIP_CHECK(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+    return MLQ_OK;
+}
+
+int mlq_hip_memcpy_dtoh(void* dst, const void* src, size_t bytes) {
+    MLQ_HIP_CHECK(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
+    return MLQ_OK;
+}
+
+int mlq_hip_memcpy_dtod(void* dst, const void* src, size_t bytes, void* stream) {
+    int dev = 0;
+    MLQ_HIP_CHECK(hipGetDevice(&dev));
+    MLQ_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice,
+                                 stream ? static_cast<hipStream_t>(stream) : g_dev[dev].stream));
+    return MLQ_OK;
+}
+
+int mlq_hip_memset(void* ptr, int value, size_t bytes) {
+    MLQ_HIP_CHECK(hipMemset(ptr, value, bytes));
+    return MLQ_OK;
+}
+
+int mlq_hip_stream(int device, void** stream) {
+    if (stream == nullptr) return fail(MLQ_ERR_INVALID, "mlq_hip_stream: null output");
+    int rc = ensure_device(device);
+    if (rc != MLQ_OK) return rc;
+    *stream = g_dev[device].stream;
+    return MLQ_OK;
+}
+
+int mlq_hip_synchronize(void* stream) {
+    if (stream == nullptr) {
+        MLQ_HIP_CHECK(hipDeviceSynchronize());
+    } else {
+        MLQ_HIP_CHECK(hipStreamSynchronize(static_cast<hipStream_t>(stream)));
+    }
+    return MLQ_OK;
+}
+
+int mlq_hip_event_create(void** ev) {
+    if (ev == nullptr) return fail(MLQ_ERR_INVALID, "mlq_hip_event_create: null output");
+    hipEvent_t e;
+    MLQ_HIP_CHECK(hipEventCreate(&e));
+    *ev = e;
+    return MLQ_OK;
+}
+
+int mlq_hip_event_destroy(void* ev) {
+    if (ev != nullptr) MLQ_HIP_CHECK(hipEventDestroy(static_cast<hipEvent_t>(ev)));
+    return MLQ_OK;
+}
+
+int mlq_hip_event_record(void* ev, void* stream) {
+    int dev = 0;
+    MLQ_HIP_CHECK(hipGetDevice(&dev));
+    MLQ_HIP_CHECK(hipEventRecord(static_cast<hipEvent_t>(ev),
+                                 stream ? static_cast<hipStream_t>(stream) : g_dev[dev].stream));
+    return MLQ_OK;
+}
+
+int mlq_hip_event_elapsed_ms(void* start, void* stop, float* ms) {
+    if (ms == nullptr) return fail(MLQ_ERR_INVALID, "mlq_hip_event_elapsed_ms: null output");
+    MLQ_HIP_CHECK(hipEventSynchronize(static_cast<hipEvent_t>(stop)));
+    MLQ_HIP_CHECK(hipEventElapsedTime(ms, static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(stop)));
+    return MLQ_OK;
+}
+
+int mlq_hip_graph_capture_many(const mlq_linear_call* calls, int n, void* stream, mlq_graph_t* out) {
+    if (out == nullptr) return fail(MLQ_ERR_INVALID, "mlq_hip_graph_capture_many: null output");
+    *out = nullptr;
+    if (calls == nullptr || n <= 0 || calls[0].w == nullptr) {
+        return fail(MLQ_ERR_INVALID, "mlq_hip_graph_capture_many: no calls");
+    }
+    const int device = calls[0].w->device;
+    int rc = ensure_device(device);
+    if (rc != MLQ_OK) return rc;
+    // Validate everything before capture starts; nothing below may fail midway
+    // except HIP itself.
+    for (int i = 0; i < n; ++i) {
+        const mlq_linear_call& c = calls[i];
+        if (c.w == nullptr || c.w->device != device) {
+            return fail(MLQ_ERR_INVALID, "mlq_hip_graph_capture_many: bad weight handle");
+        }
+        if ((rc = validate_linear(c.w->qtype, c.w->M, c.w->K, c.w->n_blocks, c.rows)) != MLQ_OK) return rc;
+        const char* caller = caller_for(c.w->qtype);
+        if ((rc = check_device_ptr(c.x, device, caller, "input")) != MLQ_OK) return rc;
+        if ((rc = check_device_ptr(c.y, device, caller, "output")) != MLQ_OK) return rc;
+    }
+    hipStream_t s = resolve_stream(device, stream);
+    MLQ_HIP_CHECK(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+    hipError_t launch_err = hipSuccess;
+    for (int i = 0; i < n && launch_err == hipSuccess; ++i) {
+        const mlq_linear_call& c = calls[i];
+        mlq::LinearShape shape{c.w->qtype, c.w->M, c.w->K, c.w->nb, c.rows};
+        launch_err = dispatch(shape, c.w->ptr, c.x, c.y, s);
+    }
+    hipGraph_t graph = nullptr;
+    hipError_t end_err = hipStreamEndCapture(s, &graph);
+    if (launch_err != hipSuccess) {
+        if (graph) (void)hipGraphDestroy(graph);
+        return hip_fail(launch_err, "graph capture launch");
+    }
+    if (end_err != hipSuccess) return hip_fail(end_err, "hipStreamEndCapture");
+    hipGraphExec_t exec = nullptr;
+    hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        (void)hipGraphDestroy(graph);
+        return hip_fail(e, "hipGraphInstantiate");
+    }
+    *out = new mlq_graph_s{graph, exec, device};
+    return MLQ_OK;
+}
+
+int mlq_hip_graph_launch(mlq_graph_t g, void* stream) {
+    if (g == nullptr) return fail(MLQ_ERR_INVALID, "mlq_hip_graph_launch: null graph");
+    int rc = ensure_device(g->device);
+    if (rc != MLQ_OK) return rc;
+    MLQ_HIP_CHECK(hipGraphLaunch(g->exec, resolve_stream(g->device, stream)));
+    return MLQ_OK;
+}
+
+int mlq_hip_graph_destroy(mlq_graph_t g) {
+    if (g == nullptr) return MLQ_OK;
+    if (g->exec) (void)hipGraphExecDestroy(g->exec);
+    if (g->graph) (void)hipGraphDestroy(g->graph);
+    delete g;
+    return MLQ_OK;
+}
+
+int mlq_hip_fill_normal(float* device_dst, size_t n, uint64_t seed, float mean, float stddev,
+                        void* stream) {
+    int dev = 0;
+    MLQ_HIP_CHECK(hipGetDevice(&dev));
+    int rc = ensure_device(dev);
+    if (rc != MLQ_OK) return rc;
+    if (n == 0) return MLQ_OK;
+    if ((rc = check_device_ptr(device_dst, dev, "mlq_hip_fill_normal", "destination")) != MLQ_OK) return rc;
+    hipError_t e = mlq::launch_fill_normal(device_dst, n, seed, mean, stddev, resolve_stream(dev, stream));
+    if (e != hipSuccess) return hip_fail(e, "fill_normal_kernel");
+    return MLQ_OK;
+}
+
+int mlq_hip_kernel_name(int qtype, int rows, int out_features, int in_features, char* buf,
+                        size_t len) {
+    if (buf == nullptr || len == 0) return fail(MLQ_ERR_INVALID, "mlq_hip_kernel_name: null buffer");
+    mlq::LinearShape s{qtype, out_features, in_features, (in_features + 31) / 32, rows};
+    const char* name = (rows > 1 && mlq::gemm_supported(s)) ? mlq::gemm_kernel_name(s)
+                                                               : mlq::gemv_kernel_name(s);
+    std::snprintf(buf, len, "%s", name);
+    return MLQ_OK;
+}
+
+}  // extern "C"

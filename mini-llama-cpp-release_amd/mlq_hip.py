@@ -1,0 +1,315 @@
+"""ctypes binding of libmlq_hip.so (include/mlq_hip.h) for tests, bench and smoke.
+
+This is plumbing, not a second implementation: every entry calls the C ABI,
+and there is no CPU fallback -- ``load()`` raises if the HIP library was not
+built, and every call raises ``MlqError`` with the library's message when the
+C ABI returns a nonzero code.
+
+The module deliberately does not import torch: the library owns its device
+memory, streams and events, so a process never carries two HIP runtimes.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libmlq_hip.so")
+
+F32, Q8_0, Q4_0, Q4_1 = 0, 1, 2, 3
+BLOCK_BYTES = {Q8_0: 34, Q4_0: 18, Q4_1: 20}
+QK = 32
+X_ON_DEVICE, Y_ON_DEVICE, ASYNC = 1, 2, 4
+
+_vp = ctypes.c_void_p
+
+
+class MlqError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"[mlq {code}] {msg}")
+        self.code = code
+        self.msg = msg
+
+
+class LinearCall(ctypes.Structure):
+    _fields_ = [("w", _vp), ("x", _vp), ("y", _vp), ("rows", ctypes.c_int)]
+
+
+_LIB = None
+
+_SIGS = {
+    "mlq_hip_last_error": (ctypes.c_char_p, []),
+    "mlq_hip_built": (ctypes.c_int, []),
+    "mlq_hip_device_count": (ctypes.c_int, [ctypes.POINTER(ctypes.c_int)]),
+    "mlq_hip_device_info": (ctypes.c_int, [ctypes.c_int, ctypes.c_char_p, ctypes.c_size_t]),
+    "mlq_hip_init": (ctypes.c_int, [ctypes.c_int]),
+    "mlq_hip_upload_weight": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, _vp, ctypes.c_size_t,
+                                              ctypes.c_int, ctypes.c_int, ctypes.POINTER(_vp)]),
+    "mlq_hip_wrap_weight": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, _vp, ctypes.c_size_t,
+                                            ctypes.c_int, ctypes.c_int, ctypes.POINTER(_vp)]),
+    "mlq_hip_free_weight": (ctypes.c_int, [_vp]),
+    "mlq_hip_weight_info": (ctypes.c_int, [_vp, ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int),
+                                            ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_size_t),
+                                            ctypes.POINTER(_vp), ctypes.POINTER(ctypes.c_int)]),
+    "mlq_hip_quant_linear": (ctypes.c_int, [_vp, _vp, ctypes.c_int, _vp, ctypes.c_int, _vp]),
+    "mlq_hip_quant_linear_device": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, _vp, ctypes.c_size_t,
+                                                    ctypes.c_int, ctypes.c_int, _vp, ctypes.c_int, _vp, _vp]),
+    "mlq_hip_quant_linear_many": (ctypes.c_int, [ctypes.POINTER(LinearCall), ctypes.c_int, _vp]),
+    "mlq_hip_quantize": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, _vp, ctypes.c_int, ctypes.c_int, _vp, _vp]),
+    "mlq_hip_malloc": (ctypes.c_int, [ctypes.c_int, ctypes.c_size_t, ctypes.POINTER(_vp)]),
+    "mlq_hip_free": (ctypes.c_int, [_vp]),
+    "mlq_hip_memcpy_htod": (ctypes.c_int, [_vp, _vp, ctypes.c_size_t]),
+    "mlq_hip_memcpy_dtoh": (ctypes.c_int, [_vp, _vp, ctypes.c_size_t]),
+    "mlq_hip_memcpy_dtod": (ctypes.c_int, [_vp, _vp, ctypes.c_size_t, _vp]),
+    "mlq_hip_memset": (ctypes.c_int, [_vp, ctypes.c_int, ctypes.c_size_t]),
+    "mlq_hip_stream": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(_vp)]),
+    "mlq_hip_synchronize": (ctypes.c_int, [_vp]),
+    "mlq_hip_event_create": (ctypes.c_int, [ctypes.POINTER(_vp)]),
+    "mlq_hip_event_destroy": (ctypes.c_int, [_vp]),
+    "mlq_hip_event_record": (ctypes.c_int, [_vp, _vp]),
+    "mlq_hip_event_elapsed_ms": (ctypes.c_int, [_vp, _vp, ctypes.POINTER(ctypes.c_float)]),
+    "mlq_hip_graph_capture_many": (ctypes.c_int, [ctypes.POINTER(LinearCall), ctypes.c_int, _vp,
+                                                   ctypes.POINTER(_vp)]),
+    "mlq_hip_graph_launch": (ctypes.c_int, [_vp, _vp]),
+    "mlq_hip_graph_destroy": (ctypes.c_int, [_vp]),
+    "mlq_hip_fill_normal": (ctypes.c_int, [_vp, ctypes.c_size_t, ctypes.c_uint64, ctypes.c_float,
+                                            ctypes.c_float, _vp]),
+    "mlq_hip_kernel_name": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                            ctypes.c_char_p, ctypes.c_size_t]),
+}
+
+EXPORTED = tuple(_SIGS)
+
+
+def load(path: str = LIB_PATH):
+    """Load the HIP library (raises if it is not built: there is no fallback)."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    if not os.path.exists(path):
+        raise FileNotFoundError(
+            f"{path} is missing: build it with `make -C mini-llama-cpp-release_amd` "
+            "(there is no CPU fallback for the HIP path)")
+    lib = ctypes.CDLL(path)
+    for name, (res, args) in _SIGS.items():
+        f = getattr(lib, name)
+        f.restype = res
+        f.argtypes = args
+    _LIB = lib
+    return lib
+
+
+def _check(rc: int) -> None:
+    if rc != 0:
+        raise MlqError(rc, _LIB.mlq_hip_last_error().decode())
+
+
+def last_error() -> str:
+    return load().mlq_hip_last_error().decode()
+
+
+def device_count() -> int:
+    n = ctypes.c_int(0)
+    _check(load().mlq_hip_device_count(ctypes.byref(n)))
+    return n.value
+
+
+def device_info(device: int = 0) -> str:
+    buf = ctypes.create_string_buffer(256)
+    _check(load().mlq_hip_device_info(device, buf, 256))
+    return buf.value.decode()
+
+
+def init(device: int = 0) -> None:
+    _check(load().mlq_hip_init(device))
+
+
+def kernel_name(qtype: int, rows: int, m: int, k: int) -> str:
+    buf = ctypes.create_string_buffer(128)
+    _check(load().mlq_hip_kernel_name(qtype, rows, m, k, buf, 128))
+    return buf.value.decode()
+
+
+class DeviceBuffer:
+    """Owned device allocation (hipMalloc through the C ABI)."""
+
+    def __init__(self, nbytes: int, device: int = 0):
+        lib = load()
+        p = _vp()
+        _check(lib.mlq_hip_malloc(device, max(int(nbytes), 1), ctypes.byref(p)))
+        self.ptr = p.value
+        self.nbytes = int(nbytes)
+        self.device = device
+
+    @classmethod
+    def from_array(cls, a: np.ndarray, device: int = 0) -> "DeviceBuffer":
+        a = np.ascontiguousarray(a)
+        b = cls(a.nbytes, device)
+        b.upload(a)
+        return b
+
+    def upload(self, a: np.ndarray, offset: int = 0) -> None:
+        a = np.ascontiguousarray(a)
+        assert offset + a.nbytes <= self.nbytes
+        _check(_LIB.mlq_hip_memcpy_htod(self.ptr + offset, a.ctypes.data, a.nbytes))
+
+    def download(self, dtype, count: int | None = None, offset: int = 0) -> np.ndarray:
+        dtype = np.dtype(dtype)
+        if count is None:
+            count = (self.nbytes - offset) // dtype.itemsize
+        out = np.empty(count, dtype=dtype)
+        assert offset + out.nbytes <= self.nbytes
+        _check(_LIB.mlq_hip_memcpy_dtoh(out.ctypes.data, self.ptr + offset, out.nbytes))
+        return out
+
+    def fill(self, value: int = 0) -> None:
+        _check(_LIB.mlq_hip_memset(self.ptr, value, self.nbytes))
+
+    def free(self) -> None:
+        if getattr(self, "ptr", None):
+            _LIB.mlq_hip_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Weight:
+    """A quantized [M, K] weight resident on the device (mlq_weight_t)."""
+
+    def __init__(self, handle: int, qtype: int, m: int, k: int, keep=None):
+        self.h = handle
+        self.qtype, self.m, self.k = qtype, m, k
+        self.nb = (k + QK - 1) // QK
+        self._keep = keep  # a wrapped DeviceBuffer must outlive the handle
+
+    @classmethod
+    def upload(cls, qtype: int, blocks: np.ndarray, m: int, k: int, device: int = 0) -> "Weight":
+        blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+        h = _vp()
+        _check(load().mlq_hip_upload_weight(device, qtype, blocks.ctypes.data, blocks.shape[0], m, k,
+                                            ctypes.byref(h)))
+        return cls(h.value, qtype, m, k)
+
+    @classmethod
+    def wrap(cls, qtype: int, buf: DeviceBuffer, n_blocks: int, m: int, k: int, device: int = 0) -> "Weight":
+        h = _vp()
+        _check(load().mlq_hip_wrap_weight(device, qtype, buf.ptr, n_blocks, m, k, ctypes.byref(h)))
+        return cls(h.value, qtype, m, k, keep=buf)
+
+    def linear_host(self, x: np.ndarray) -> np.ndarray:
+        """y = x W^T with host x / y (the *_device_weight form)."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        rows = x.size // self.k
+        y = np.empty(x.shape[:-1] + (self.m,), dtype=np.float32)
+        _check(_LIB.mlq_hip_quant_linear(self.h, x.ctypes.data, rows, y.ctypes.data, 0, None))
+        return y
+
+    def linear_device(self, x: DeviceBuffer, y: DeviceBuffer, rows: int = 1, stream=None,
+                      sync: bool = True) -> None:
+        flags = X_ON_DEVICE | Y_ON_DEVICE | (0 if sync else ASYNC)
+        _check(_LIB.mlq_hip_quant_linear(self.h, x.ptr, rows, y.ptr, flags, stream))
+
+    def free(self) -> None:
+        if getattr(self, "h", None):
+            _LIB.mlq_hip_free_weight(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def quantize_device(qtype: int, src: DeviceBuffer, rows: int, row_len: int, dst: DeviceBuffer,
+                    device: int = 0, stream=None) -> None:
+    _check(load().mlq_hip_quantize(device, qtype, src.ptr, rows, row_len, dst.ptr, stream))
+
+
+def fill_normal(buf: DeviceBuffer, n: int, seed: int, mean: float = 0.0, std: float = 1.0,
+                stream=None) -> None:
+    _check(load().mlq_hip_fill_normal(buf.ptr, n, seed & (2 ** 64 - 1), mean, std, stream))
+
+
+def linear_device_raw(qtype: int, w: DeviceBuffer, n_blocks: int, m: int, k: int, x: DeviceBuffer,
+                      rows: int, y: DeviceBuffer, device: int = 0, stream=None) -> None:
+    _check(load().mlq_hip_quant_linear_device(device, qtype, w.ptr, n_blocks, m, k, x.ptr, rows, y.ptr,
+                                              stream))
+
+
+def make_calls(calls) -> ctypes.Array:
+    """calls: iterable of (Weight, x DeviceBuffer/ptr, y DeviceBuffer/ptr, rows)."""
+    calls = list(calls)
+    arr = (LinearCall * len(calls))()
+    for i, (w, x, y, rows) in enumerate(calls):
+        arr[i].w = w.h
+        arr[i].x = x if isinstance(x, int) else x.ptr
+        arr[i].y = y if isinstance(y, int) else y.ptr
+        arr[i].rows = rows
+    return arr
+
+
+def linear_many(arr: ctypes.Array, stream=None) -> None:
+    _check(load().mlq_hip_quant_linear_many(arr, len(arr), stream))
+
+
+class Graph:
+    def __init__(self, arr: ctypes.Array, stream=None):
+        h = _vp()
+        _check(load().mlq_hip_graph_capture_many(arr, len(arr), stream, ctypes.byref(h)))
+        self.h = h.value
+        self._arr = arr
+
+    def launch(self, stream=None) -> None:
+        _check(_LIB.mlq_hip_graph_launch(self.h, stream))
+
+    def destroy(self) -> None:
+        if getattr(self, "h", None):
+            _LIB.mlq_hip_graph_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.destroy()
+        except Exception:
+            pass
+
+
+def stream(device: int = 0) -> int:
+    s = _vp()
+    _check(load().mlq_hip_stream(device, ctypes.byref(s)))
+    return s.value
+
+
+def synchronize(stream=None) -> None:
+    _check(load().mlq_hip_synchronize(stream))
+
+
+class Event:
+    def __init__(self):
+        e = _vp()
+        _check(load().mlq_hip_event_create(ctypes.byref(e)))
+        self.h = e.value
+
+    def record(self, stream=None) -> None:
+        _check(_LIB.mlq_hip_event_record(self.h, stream))
+
+    def elapsed_ms(self, end: "Event") -> float:
+        ms = ctypes.c_float(0)
+        _check(_LIB.mlq_hip_event_elapsed_ms(self.h, end.h, ctypes.byref(ms)))
+        return float(ms.value)
+
+    def __del__(self):
+        try:
+            if getattr(self, "h", None):
+                _LIB.mlq_hip_event_destroy(self.h)
+                self.h = None
+        except Exception:
+            pass

@@ -1,0 +1,182 @@
+// mlq reference shim -- TEST INFRASTRUCTURE ONLY.
+//
+// A C-ABI over the reference's own CPU quant functions, compiled by
+// oracle/Makefile (target `ref`) from the sources where they lie under
+// /root/reference, into oracle/_ref/libmlq_ref.so.  It exists to (1) generate
+// the golden vectors in tests/golden/ and (2) serve as the "reference" CPU
+// baseline in bench.py.  The product never links it.
+//
+// Nothing from the reference is copied here: the reference headers are found
+// through -I at build time, and the Q4_1 quantizer, which exists only as a
+// test-local function in tests/test_cuda_quant.cpp:129-180, is reached by
+// including that test's translation unit (with its main() renamed) below.
+
+#define main mlq_ref_unused_test_main
+#include "tests/test_cuda_quant.cpp"
+#undef main
+
+#include "mini_llama/ops.h"
+#include "mini_llama/quant.h"
+#include "mini_llama/thread_pool.h"
+
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+namespace {
+
+using namespace mini_llama;
+
+Tensor make_tensor(const float* src, int rows, int cols, bool as_1d) {
+    Tensor t(as_1d ? std::vector<int>{cols} : std::vector<int>{rows, cols}, 0.0f);
+    std::memcpy(t.data.data(), src, sizeof(float) * t.data.size());
+    return t;
+}
+
+template <typename Block>
+std::vector<Block> blocks_from(const void* src, size_t n) {
+    std::vector<Block> v(n);
+    std::memcpy(v.data(), src, n * sizeof(Block));
+    return v;
+}
+
+}  // namespace
+
+extern "C" {
+
+// The reference fp16 encoders are file-local; they are observed through
+// one-element blocks.  A one-element Q4_1 block has range 0, so its m field is
+// exactly fp16(v) from the test copy of the codec (tests/test_cuda_quant.cpp:60-96,
+// identical to src/quant.cpp:19-55) for every v except +Inf and NaN, which that
+// routine maps to 0.  A one-element Q8_0 block has d = fp16(|v| / 127) from the
+// product copy (src/quant.cpp:141-142).
+uint16_t mlq_ref_fp16_probe_q4_1(float v) {
+    Tensor t({1}, v);
+    std::vector<BlockQ4_1> b = quantize_to_q4_1_for_test(t);
+    return b.empty() ? 0 : b[0].m;
+}
+
+uint16_t mlq_ref_fp16_probe_q8_0(float v) {
+    Tensor t({1}, v);
+    std::vector<BlockQ8_0> b = quantize_to_q8_0(t);
+    return b.empty() ? 0 : b[0].d;
+}
+
+long long mlq_ref_quantize(int qtype, const float* src, int rows, int row_len, void* out) {
+    Tensor t = make_tensor(src, rows, row_len, rows == 1);
+    size_t n = 0;
+    if (qtype == 1) {
+        std::vector<BlockQ8_0> b = quantize_to_q8_0(t);
+        n = b.size();
+        std::memcpy(out, b.data(), n * sizeof(BlockQ8_0));
+    } else if (qtype == 2) {
+        std::vector<BlockQ4_0> b = quantize_to_q4_0(t);
+        n = b.size();
+        std::memcpy(out, b.data(), n * sizeof(BlockQ4_0));
+    } else if (qtype == 3) {
+        std::vector<BlockQ4_1> b = quantize_to_q4_1_for_test(t);
+        n = b.size();
+        std::memcpy(out, b.data(), n * sizeof(BlockQ4_1));
+    } else {
+        return -1;
+    }
+    return static_cast<long long>(n);
+}
+
+int mlq_ref_dequantize(int qtype, const void* blocks, int rows, int row_len, float* dst) {
+    const int nb = (row_len + 31) / 32;
+    const size_t n = static_cast<size_t>(rows) * nb;
+    std::vector<int> shape = rows == 1 ? std::vector<int>{row_len} : std::vector<int>{rows, row_len};
+    Tensor y;
+    if (qtype == 1) {
+        y = dequantize_from_q8_0(blocks_from<BlockQ8_0>(blocks, n), shape);
+    } else if (qtype == 2) {
+        y = dequantize_from_q4_0(blocks_from<BlockQ4_0>(blocks, n), shape);
+    } else if (qtype == 3) {
+        y = dequantize_from_q4_1(blocks_from<BlockQ4_1>(blocks, n), shape);
+    } else {
+        return -1;
+    }
+    std::memcpy(dst, y.data.data(), y.data.size() * sizeof(float));
+    return 0;
+}
+
+// y = linear(x, W) through the reference's dispatch (src/ops.cpp:197-209) with
+// the global thread count set to `threads` (src/thread_pool.cpp:19-21).
+int mlq_ref_linear(int qtype, const float* x, int rows, int K, const void* blocks,
+                   size_t n_blocks, int M, float* y, int threads, char* err, size_t err_len) {
+    try {
+        set_thread_count(threads);
+        QuantizedTensor w;
+        w.shape = {M, K};
+        if (qtype == 1) {
+            w.type = QuantType::Q8_0;
+            w.q8_0_data = blocks_from<BlockQ8_0>(blocks, n_blocks);
+        } else if (qtype == 2) {
+            w.type = QuantType::Q4_0;
+            w.q4_0_data = blocks_from<BlockQ4_0>(blocks, n_blocks);
+        } else if (qtype == 3) {
+            w.type = QuantType::Q4_1;
+            w.q4_1_data = blocks_from<BlockQ4_1>(blocks, n_blocks);
+        } else {
+            throw std::runtime_error("mlq_ref_linear: unsupported type");
+        }
+        Tensor xt = make_tensor(x, rows, K, rows == 1);
+        Tensor out = linear(xt, w);
+        std::memcpy(y, out.data.data(), out.data.size() * sizeof(float));
+        return 0;
+    } catch (const std::exception& e) {
+        if (err != nullptr && err_len > 0) std::snprintf(err, err_len, "%s", e.what());
+        return -1;
+    }
+}
+
+// Same, but with the caller's blocks borrowed for many calls: the weight is
+// wrapped once so that timing loops measure only linear().
+void* mlq_ref_weight_new(int qtype, const void* blocks, size_t n_blocks, int M, int K) {
+    QuantizedTensor* w = new QuantizedTensor();
+    w->shape = {M, K};
+    if (qtype == 1) {
+        w->type = QuantType::Q8_0;
+        w->q8_0_data = blocks_from<BlockQ8_0>(blocks, n_blocks);
+    } else if (qtype == 2) {
+        w->type = QuantType::Q4_0;
+        w->q4_0_data = blocks_from<BlockQ4_0>(blocks, n_blocks);
+    } else if (qtype == 3) {
+        w->type = QuantType::Q4_1;
+        w->q4_1_data = blocks_from<BlockQ4_1>(blocks, n_blocks);
+    } else {
+        delete w;
+        return nullptr;
+    }
+    return w;
+}
+
+void mlq_ref_weight_free(void* w) { delete static_cast<QuantizedTensor*>(w); }
+
+int mlq_ref_weight_linear(void* w, const float* x, int rows, float* y, int threads) {
+    try {
+        set_thread_count(threads);
+        QuantizedTensor* qt = static_cast<QuantizedTensor*>(w);
+        Tensor xt = make_tensor(x, rows, qt->shape[1], rows == 1);
+        Tensor out = linear(xt, *qt);
+        std::memcpy(y, out.data.data(), out.data.size() * sizeof(float));
+        return 0;
+    } catch (const std::exception&) {
+        return -1;
+    }
+}
+
+int mlq_ref_argmax(const float* v, int n) {
+    Tensor t({n}, 0.0f);
+    std::memcpy(t.data.data(), v, sizeof(float) * n);
+    return argmax(t);
+}
+
+int mlq_ref_hardware_threads(void) {
+    set_thread_count(0);
+    return get_thread_count();
+}
+
+}  // extern "C"

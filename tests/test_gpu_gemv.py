@@ -1,0 +1,173 @@
+"""GPU parity of the decode GEMV (and the batched path) against the CPU oracle.
+
+Every comparison goes through the C ABI (libmlq_hip.so via ctypes) and checks
+both the BASELINE bound and the reference's own bound (tests/tolerance.py).
+Weights are seeded N(0, 0.02) quantised by the oracle (which is bit-exact with
+the reference quantizers), x is seeded N(0, 1): BASELINE.json configs 1-3 at
+their full shapes, the reference's CUDA parity shapes
+(tests/test_cuda_quant.cpp:293-420) and the tiny model's tail-block linears.
+"""
+
+import os
+import sys
+
+import numpy as np
+import pytest
+
+import oracle
+from tolerance import check_close
+
+pytestmark = pytest.mark.gpu
+
+FMTS = {"q8_0": oracle.Q8_0, "q4_0": oracle.Q4_0, "q4_1": oracle.Q4_1}
+THREADS = min(16, os.cpu_count() or 1)
+
+_W_CACHE = {}
+
+
+def weights(m, k, seed=0):
+    key = (m, k, seed)
+    if key not in _W_CACHE:
+        _W_CACHE.clear()
+        rng = np.random.default_rng(1000 + 7 * m + 13 * k + seed)
+        _W_CACHE[key] = (rng.standard_normal((m, k), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+    return _W_CACHE[key]
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def run_case(hip, orc, fmt, m, k, rows=1, seed=0):
+    qt = FMTS[fmt]
+    w = weights(m, k, seed)
+    rng = np.random.default_rng(77 + m + k + rows)
+    x = rng.standard_normal((rows, k) if rows > 1 else (k,), dtype=np.float32)
+    blocks = orc.quantize(qt, w, threads=THREADS)
+    want = orc.linear(qt, x, blocks, m, threads=THREADS)
+    say(f"case {fmt} M={m} K={k} rows={rows} kernel={hip.kernel_name(qt, rows, m, k)}")
+    wt = hip.Weight.upload(qt, blocks, m, k)
+    got = wt.linear_host(x)
+    wt.free()
+    return check_close(got, want, x, qt, blocks, f"{fmt} {m}x{k} rows={rows}")
+
+
+# BASELINE.json config 1 (Q8_0 4864x896), config 2 (every Qwen2-0.5B linear),
+# config 3 (LLaMA-7B shapes); all three formats at each shape.
+QWEN = [(896, 896), (128, 896), (4864, 896), (896, 4864), (151936, 896)]
+LLAMA = [(4096, 4096), (11008, 4096), (4096, 11008), (32000, 4096)]
+
+
+@pytest.mark.parametrize("shape", QWEN + LLAMA, ids=lambda s: f"{s[0]}x{s[1]}")
+def test_gemv_full_shapes(hip, orc, shape):
+    for fmt in FMTS:
+        run_case(hip, orc, fmt, *shape)
+
+
+@pytest.mark.parametrize("shape", [(5, 13), (32, 64), (17, 65), (86, 32), (32, 86), (128, 32),
+                                   (1, 32), (3, 4095), (7, 33), (64, 4160), (40, 20000)],
+                         ids=lambda s: f"{s[0]}x{s[1]}")
+def test_gemv_small_and_ragged(hip, orc, shape):
+    for fmt in FMTS:
+        run_case(hip, orc, fmt, *shape)
+
+
+@pytest.mark.parametrize("fmt", list(FMTS))
+@pytest.mark.parametrize("shape,rows", [((32, 64), 3), ((17, 65), 3), ((4096, 4096), 4),
+                                        ((896, 896), 16), ((300, 4096), 7)],
+                         ids=lambda v: str(v))
+def test_batched_rows(hip, orc, fmt, shape, rows):
+    run_case(hip, orc, fmt, *shape, rows=rows)
+
+
+def test_golden_vectors(hip, golden):
+    """The reference's own outputs (tests/golden) reproduced by the GPU path."""
+    for n in golden["names"]:
+        n = str(n)
+        w = golden[f"{n}__w"]
+        x = golden[f"{n}__x"]
+        for fmt, qt in FMTS.items():
+            blocks = golden[f"{n}__{fmt}__blocks"]
+            say(f"golden {n} {fmt}")
+            wt = hip.Weight.upload(qt, blocks, *w.shape)
+            got = wt.linear_host(x)
+            wt.free()
+            check_close(got, golden[f"{n}__{fmt}__y"], x, qt, blocks, f"golden {n} {fmt}")
+
+
+def test_tiny_model_linears(hip, tiny):
+    """All 15 linears of the reference's tiny model (hidden_dim 86 -> tail blocks)."""
+    for n in tiny["names"]:
+        key = str(n).replace(".", "_")
+        w = tiny[f"{key}__w"]
+        x = tiny[f"{key}__x"]
+        for fmt, qt in FMTS.items():
+            blocks = tiny[f"{key}__{fmt}__blocks"]
+            say(f"tiny {n} {fmt}")
+            wt = hip.Weight.upload(qt, blocks, *w.shape)
+            check_close(wt.linear_host(x), tiny[f"{key}__{fmt}__y"], x, qt, blocks, f"tiny {n} {fmt}")
+            wt.free()
+
+
+@pytest.mark.parametrize("fmt", list(FMTS))
+def test_call_forms_agree(hip, orc, fmt):
+    """Host-pointer, device-pointer, raw device form, batched-call form and a
+    captured graph (replayed with eager work in between) give the same bits."""
+    qt = FMTS[fmt]
+    m, k = 4096, 4096
+    w = weights(m, k)
+    blocks = orc.quantize(qt, w, threads=THREADS)
+    x = np.random.default_rng(3).standard_normal(k, dtype=np.float32)
+    want = orc.linear(qt, x, blocks, m, threads=THREADS)
+    say(f"forms {fmt}")
+    wt = hip.Weight.upload(qt, blocks, m, k)
+    y_host = wt.linear_host(x)
+    check_close(y_host, want, x, qt, blocks, "host form")
+    xd = hip.DeviceBuffer.from_array(x)
+    yd = hip.DeviceBuffer(4 * m)
+    wt.linear_device(xd, yd)
+    assert np.array_equal(yd.download(np.float32).view(np.uint32), y_host.view(np.uint32))
+    wb = hip.DeviceBuffer.from_array(blocks)
+    yd.fill(0)
+    hip.linear_device_raw(qt, wb, blocks.shape[0], m, k, xd, 1, yd)
+    hip.synchronize(hip.stream(0))
+    assert np.array_equal(yd.download(np.float32).view(np.uint32), y_host.view(np.uint32))
+    ys = [hip.DeviceBuffer(4 * m) for _ in range(3)]
+    calls = hip.make_calls([(wt, xd, yy, 1) for yy in ys])
+    hip.linear_many(calls)
+    hip.synchronize(hip.stream(0))
+    for yy in ys:
+        assert np.array_equal(yy.download(np.float32).view(np.uint32), y_host.view(np.uint32))
+    g = hip.Graph(calls)
+    for rep in range(4):
+        for yy in ys:
+            yy.fill(0xFF)
+        wt.linear_device(xd, yd)  # eager work between replays
+        g.launch()
+        hip.synchronize(hip.stream(0))
+        for yy in ys:
+            assert np.array_equal(yy.download(np.float32).view(np.uint32), y_host.view(np.uint32)), rep
+    g.destroy()
+    wt.free()
+
+
+def test_reference_error_messages(hip, orc):
+    """Validation mirrors src/cuda_quant.cu:214-243 and src/model.cpp:163-170."""
+    blocks = orc.quantize(oracle.Q4_0, np.ones((4, 64), np.float32))
+    with pytest.raises(hip.MlqError, match="HIP weight upload: Q4_0 block count mismatch, expected 8, got 7"):
+        hip.Weight.upload(oracle.Q4_0, blocks[:7], 4, 64)
+    wb = hip.DeviceBuffer.from_array(blocks)
+    xd = hip.DeviceBuffer(4 * 64)
+    yd = hip.DeviceBuffer(4 * 4)
+    with pytest.raises(hip.MlqError, match="hip_q4_0_linear: block count mismatch: expected 8, got 6"):
+        hip.linear_device_raw(oracle.Q4_0, wb, 6, 4, 64, xd, 1, yd)
+    with pytest.raises(hip.MlqError, match="hip_q4_0_linear: empty tensors are not supported"):
+        hip.linear_device_raw(oracle.Q4_0, wb, 8, 4, 64, xd, 0, yd)
+    # a host pointer passed as a device pointer is refused before any launch
+    host = np.zeros(64, np.float32)
+    lib = hip.load()
+    rc = lib.mlq_hip_quant_linear_device(0, oracle.Q4_0, wb.ptr, 8, 4, 64, host.ctypes.data, 1, yd.ptr, None)
+    assert rc == 3 and "not a HIP device pointer" in hip.last_error()
+    rc = lib.mlq_hip_quant_linear_device(0, oracle.Q4_0, None, 8, 4, 64, xd.ptr, 1, yd.ptr, None)
+    assert rc == 1 and hip.last_error() == "hip_q4_0_linear: device weight pointer is null"

@@ -1,0 +1,74 @@
+"""The device quantizer (mlq_hip_quantize) against the oracle / reference bytes.
+
+Bit-exact: the same f32 weights must give the same block bytes as
+quantize_to_q8_0 / quantize_to_q4_0 (src/quant.cpp:112-170, 207-270) and the
+Q4_1 test quantizer (tests/test_cuda_quant.cpp:129-180)."""
+
+import numpy as np
+import pytest
+
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+FMTS = {"q8_0": oracle.Q8_0, "q4_0": oracle.Q4_0, "q4_1": oracle.Q4_1}
+
+
+def device_quantize(hip, qt, w):
+    rows, k = w.shape
+    nb = (k + 31) // 32
+    src = hip.DeviceBuffer.from_array(np.ascontiguousarray(w, np.float32))
+    dst = hip.DeviceBuffer(rows * nb * oracle.BLOCK_BYTES[qt])
+    dst.fill(0xAB)
+    hip.quantize_device(qt, src, rows, k, dst)
+    hip.synchronize(hip.stream(0))
+    return dst.download(np.uint8).reshape(rows * nb, oracle.BLOCK_BYTES[qt])
+
+
+@pytest.mark.parametrize("fmt", list(FMTS))
+def test_device_quantizer_golden(hip, golden, fmt):
+    qt = FMTS[fmt]
+    for n in golden["names"]:
+        n = str(n)
+        w = golden[f"{n}__w"]
+        print(f"quantize golden {n} {fmt}", flush=True)
+        assert np.array_equal(device_quantize(hip, qt, w), golden[f"{n}__{fmt}__blocks"]), n
+
+
+@pytest.mark.parametrize("fmt", list(FMTS))
+def test_device_quantizer_random_and_special(hip, orc, fmt):
+    qt = FMTS[fmt]
+    rng = np.random.default_rng(21)
+    cases = []
+    cases.append((rng.standard_normal((64, 4096), dtype=np.float32) * np.float32(0.02)))
+    cases.append((rng.standard_normal((33, 86), dtype=np.float32)))
+    w = rng.standard_normal((16, 96), dtype=np.float32)
+    w[0] = 0.0                                  # all-zero blocks
+    w[1] = 3.0                                  # constant blocks
+    w[2, :32] = np.float32(1e-30)               # scale underflows fp16
+    w[3] *= np.float32(1e6)                     # scale overflows fp16 -> inf
+    w[4, 5] = np.float32(65519.996)             # near the fp16 top
+    w[5] = np.round(w[5] * 8) / 8               # exact ties in q
+    w[6, ::2] = -w[6, 1::2]
+    cases.append(w)
+    t = rng.standard_normal((8, 4095), dtype=np.float32)  # tail block of 31
+    cases.append(t)
+    for w in cases:
+        w = np.ascontiguousarray(w, np.float32)
+        print(f"quantize {fmt} {w.shape}", flush=True)
+        assert np.array_equal(device_quantize(hip, qt, w), orc.quantize(qt, w, threads=4)), w.shape
+
+
+def test_fill_normal_moments(hip):
+    n = 1 << 22
+    buf = hip.DeviceBuffer(4 * n)
+    hip.fill_normal(buf, n, seed=123, mean=0.0, std=0.02)
+    hip.synchronize(hip.stream(0))
+    v = buf.download(np.float32)
+    assert np.isfinite(v).all()
+    assert abs(float(v.mean())) < 1e-4
+    assert abs(float(v.std()) - 0.02) < 2e-4
+    buf2 = hip.DeviceBuffer(4 * n)
+    hip.fill_normal(buf2, n, seed=123, mean=0.0, std=0.02)
+    hip.synchronize(hip.stream(0))
+    assert np.array_equal(buf2.download(np.float32).view(np.uint32), v.view(np.uint32))
