@@ -84,7 +84,7 @@ LAYER = [("q", 4096, 4096, "x"), ("k", 4096, 4096, "x"), ("v", 4096, 4096, "x"),
 class Sweep:
     def __init__(self, layers=32, qt=hip.Q4_0, seed=7):
         self.qt = qt
-        tmp = hip.DeviceBuffer(4 * 11008 * 4096)
+        tmp = hip.DeviceBuffer(4 * 32000 * 4096)  # f32 scratch for the largest weight (lm_head)
         self.weights, self.calls_desc, self.ys, self.xs = [], [], [], []
         for l in range(layers):
             x = hip.DeviceBuffer(4 * 4096)

@@ -111,10 +111,12 @@ hipStream_t resolve_stream(int device, void* stream) {
     return stream != nullptr ? static_cast<hipStream_t>(stream) : g_dev[device].stream;
 }
 
-// Checks that `p` is device memory on `device` (device or managed allocation).
-// A host pointer handed over as a device pointer would fault the GPU, so this
-// runs before every launch that takes caller pointers.
-int check_device_ptr(const void* p, int device, const char* caller, const char* what) {
+// Checks that [p, p + bytes) lies inside one device allocation on `device`
+// (device or managed memory).  A host pointer handed over as a device pointer,
+// or a buffer shorter than the shape implies, would make a kernel fault, so
+// every entry point that takes caller pointers runs this before launching.
+int check_device_ptr(const void* p, int device, const char* caller, const char* what,
+                     size_t bytes) {
     if (p == nullptr) return fail(MLQ_ERR_INVALID, std::string(caller) + ": " + what + " pointer is null");
     hipPointerAttribute_t attr;
     std::memset(&attr, 0, sizeof attr);
@@ -129,6 +131,20 @@ int check_device_ptr(const void* p, int device, const char* caller, const char* 
     if (attr.device != device) {
         return fail(MLQ_ERR_DEVICE, std::string(caller) + ": " + what +
                                         " tensor is on a different HIP device");
+    }
+    hipDeviceptr_t base = nullptr;
+    size_t size = 0;
+    e = hipMemGetAddressRange(&base, &size, const_cast<void*>(p));
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return fail(MLQ_ERR_DEVICE, std::string(caller) + ": " + what + " allocation extent is unknown");
+    }
+    const uintptr_t start = reinterpret_cast<uintptr_t>(p);
+    const uintptr_t end = reinterpret_cast<uintptr_t>(base) + size;
+    if (start + bytes > end) {
+        return fail(MLQ_ERR_LIMIT, std::string(caller) + ": " + what + " buffer is too small: needs " +
+                                       std::to_string(bytes) + " bytes, the allocation holds " +
+                                       std::to_string(end - start) + " from this pointer");
     }
     return MLQ_OK;
 }
@@ -259,7 +275,8 @@ int mlq_hip_wrap_weight(int device, int qtype, const void* device_blocks, size_t
     if (rc != MLQ_OK) return rc;
     rc = ensure_device(device);
     if (rc != MLQ_OK) return rc;
-    rc = check_device_ptr(device_blocks, device, caller, "device weight");
+    rc = check_device_ptr(device_blocks, device, caller, "device weight",
+                          n_blocks * static_cast<size_t>(mlq::block_bytes(qtype)));
     if (rc != MLQ_OK) return rc;
     const int nb = (in_features + mlq::kQK - 1) / mlq::kQK;
     *out = new mlq_weight_s{device, qtype, out_features, in_features, nb, n_blocks,
@@ -303,9 +320,12 @@ int mlq_hip_quant_linear_device(int device, int qtype, const void* device_blocks
     if (rc != MLQ_OK) return rc;
     rc = ensure_device(device);
     if (rc != MLQ_OK) return rc;
-    if ((rc = check_device_ptr(device_blocks, device, caller, "device weight")) != MLQ_OK) return rc;
-    if ((rc = check_device_ptr(x, device, caller, "input")) != MLQ_OK) return rc;
-    if ((rc = check_device_ptr(y, device, caller, "output")) != MLQ_OK) return rc;
+    const size_t wbytes = n_blocks * static_cast<size_t>(mlq::block_bytes(qtype));
+    const size_t xbytes = static_cast<size_t>(rows) * in_features * sizeof(float);
+    const size_t ybytes = static_cast<size_t>(rows) * out_features * sizeof(float);
+    if ((rc = check_device_ptr(device_blocks, device, caller, "device weight", wbytes)) != MLQ_OK) return rc;
+    if ((rc = check_device_ptr(x, device, caller, "input", xbytes)) != MLQ_OK) return rc;
+    if ((rc = check_device_ptr(y, device, caller, "output", ybytes)) != MLQ_OK) return rc;
     mlq::LinearShape s{qtype, out_features, in_features, (in_features + 31) / 32, rows};
     hipError_t e = dispatch(s, device_blocks, x, y, resolve_stream(device, stream));
     if (e != hipSuccess) return hip_fail(e, caller);
@@ -333,8 +353,8 @@ int mlq_hip_quant_linear(mlq_weight_t w, const float* x, int rows, float* y, int
 
     const bool xd = flags & MLQ_X_ON_DEVICE;
     const bool yd = flags & MLQ_Y_ON_DEVICE;
-    if (xd && (rc = check_device_ptr(x, w->device, caller, "input")) != MLQ_OK) return rc;
-    if (yd && (rc = check_device_ptr(y, w->device, caller, "output")) != MLQ_OK) return rc;
+    if (xd && (rc = check_device_ptr(x, w->device, caller, "input", xb)) != MLQ_OK) return rc;
+    if (yd && (rc = check_device_ptr(y, w->device, caller, "output", yb)) != MLQ_OK) return rc;
     if (xd && yd) {
         hipError_t e = dispatch(shape, w->ptr, x, y, s);
         if (e != hipSuccess) return hip_fail(e, caller);
@@ -377,8 +397,11 @@ int mlq_hip_quant_linear_many(const mlq_linear_call* calls, int n, void* stream)
     if (rc != MLQ_OK) return rc;
     for (int i = 0; i < n; ++i) {
         const char* caller = caller_for(calls[i].w->qtype);
-        if ((rc = check_device_ptr(calls[i].x, device, caller, "input")) != MLQ_OK) return rc;
-        if ((rc = check_device_ptr(calls[i].y, device, caller, "output")) != MLQ_OK) return rc;
+        const mlq_weight_s* w = calls[i].w;
+        const size_t xb = static_cast<size_t>(calls[i].rows) * w->K * sizeof(float);
+        const size_t yb = static_cast<size_t>(calls[i].rows) * w->M * sizeof(float);
+        if ((rc = check_device_ptr(calls[i].x, device, caller, "input", xb)) != MLQ_OK) return rc;
+        if ((rc = check_device_ptr(calls[i].y, device, caller, "output", yb)) != MLQ_OK) return rc;
     }
     hipStream_t s = resolve_stream(device, stream);
     for (int i = 0; i < n; ++i) {
@@ -398,8 +421,11 @@ int mlq_hip_quantize(int device, int qtype, const float* src, int rows, int row_
     if (rows <= 0 || row_len <= 0) return fail(MLQ_ERR_SHAPE, "mlq_hip_quantize: empty tensors are not supported");
     int rc = ensure_device(device);
     if (rc != MLQ_OK) return rc;
-    if ((rc = check_device_ptr(src, device, "mlq_hip_quantize", "source")) != MLQ_OK) return rc;
-    if ((rc = check_device_ptr(device_blocks, device, "mlq_hip_quantize", "block")) != MLQ_OK) return rc;
+    const size_t nb = (static_cast<size_t>(row_len) + mlq::kQK - 1) / mlq::kQK;
+    const size_t sbytes = static_cast<size_t>(rows) * row_len * sizeof(float);
+    const size_t dbytes = static_cast<size_t>(rows) * nb * mlq::block_bytes(qtype);
+    if ((rc = check_device_ptr(src, device, "mlq_hip_quantize", "source", sbytes)) != MLQ_OK) return rc;
+    if ((rc = check_device_ptr(device_blocks, device, "mlq_hip_quantize", "block", dbytes)) != MLQ_OK) return rc;
     hipError_t e = mlq::launch_quantize(qtype, src, rows, row_len, device_blocks, resolve_stream(device, stream));
     if (e != hipSuccess) return hip_fail(e, "quantize_kernel");
     return MLQ_OK;
@@ -421,11 +447,19 @@ int mlq_hip_free(void* ptr) {
 }
 
 int mlq_hip_memcpy_htod(void* dst, const void* src, size_t bytes) {
+    int dev = 0;
+    MLQ_HIP_CHECK(hipGetDevice(&dev));
+    int rc = check_device_ptr(dst, dev, "mlq_hip_memcpy_htod", "destination", bytes);
+    if (rc != MLQ_OK) return rc;
     MLQ_HIP_CHECK(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
     return MLQ_OK;
 }
 
 int mlq_hip_memcpy_dtoh(void* dst, const void* src, size_t bytes) {
+    int dev = 0;
+    MLQ_HIP_CHECK(hipGetDevice(&dev));
+    int rc = check_device_ptr(src, dev, "mlq_hip_memcpy_dtoh", "source", bytes);
+    if (rc != MLQ_OK) return rc;
     MLQ_HIP_CHECK(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
     return MLQ_OK;
 }
@@ -433,12 +467,19 @@ int mlq_hip_memcpy_dtoh(void* dst, const void* src, size_t bytes) {
 int mlq_hip_memcpy_dtod(void* dst, const void* src, size_t bytes, void* stream) {
     int dev = 0;
     MLQ_HIP_CHECK(hipGetDevice(&dev));
+    int rc = check_device_ptr(dst, dev, "mlq_hip_memcpy_dtod", "destination", bytes);
+    if (rc == MLQ_OK) rc = check_device_ptr(src, dev, "mlq_hip_memcpy_dtod", "source", bytes);
+    if (rc != MLQ_OK) return rc;
     MLQ_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice,
                                  stream ? static_cast<hipStream_t>(stream) : g_dev[dev].stream));
     return MLQ_OK;
 }
 
 int mlq_hip_memset(void* ptr, int value, size_t bytes) {
+    int dev = 0;
+    MLQ_HIP_CHECK(hipGetDevice(&dev));
+    int rc = check_device_ptr(ptr, dev, "mlq_hip_memset", "destination", bytes);
+    if (rc != MLQ_OK) return rc;
     MLQ_HIP_CHECK(hipMemset(ptr, value, bytes));
     return MLQ_OK;
 }
@@ -506,8 +547,10 @@ int mlq_hip_graph_capture_many(const mlq_linear_call* calls, int n, void* stream
         }
         if ((rc = validate_linear(c.w->qtype, c.w->M, c.w->K, c.w->n_blocks, c.rows)) != MLQ_OK) return rc;
         const char* caller = caller_for(c.w->qtype);
-        if ((rc = check_device_ptr(c.x, device, caller, "input")) != MLQ_OK) return rc;
-        if ((rc = check_device_ptr(c.y, device, caller, "output")) != MLQ_OK) return rc;
+        const size_t xb = static_cast<size_t>(c.rows) * c.w->K * sizeof(float);
+        const size_t yb = static_cast<size_t>(c.rows) * c.w->M * sizeof(float);
+        if ((rc = check_device_ptr(c.x, device, caller, "input", xb)) != MLQ_OK) return rc;
+        if ((rc = check_device_ptr(c.y, device, caller, "output", yb)) != MLQ_OK) return rc;
     }
     hipStream_t s = resolve_stream(device, stream);
     MLQ_HIP_CHECK(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
@@ -557,7 +600,7 @@ int mlq_hip_fill_normal(float* device_dst, size_t n, uint64_t seed, float mean, 
     int rc = ensure_device(dev);
     if (rc != MLQ_OK) return rc;
     if (n == 0) return MLQ_OK;
-    if ((rc = check_device_ptr(device_dst, dev, "mlq_hip_fill_normal", "destination")) != MLQ_OK) return rc;
+    if ((rc = check_device_ptr(device_dst, dev, "mlq_hip_fill_normal", "destination", n * sizeof(float))) != MLQ_OK) return rc;
     hipError_t e = mlq::launch_fill_normal(device_dst, n, seed, mean, stddev, resolve_stream(dev, stream));
     if (e != hipSuccess) return hip_fail(e, "fill_normal_kernel");
     return MLQ_OK;

@@ -230,11 +230,14 @@ class Weight:
 
 def quantize_device(qtype: int, src: DeviceBuffer, rows: int, row_len: int, dst: DeviceBuffer,
                     device: int = 0, stream=None) -> None:
+    assert src.nbytes >= 4 * rows * row_len, "source buffer too small"
+    assert dst.nbytes >= rows * ((row_len + QK - 1) // QK) * BLOCK_BYTES[qtype], "block buffer too small"
     _check(load().mlq_hip_quantize(device, qtype, src.ptr, rows, row_len, dst.ptr, stream))
 
 
 def fill_normal(buf: DeviceBuffer, n: int, seed: int, mean: float = 0.0, std: float = 1.0,
                 stream=None) -> None:
+    assert buf.nbytes >= 4 * n, "destination buffer too small"
     _check(load().mlq_hip_fill_normal(buf.ptr, n, seed & (2 ** 64 - 1), mean, std, stream))
 
 

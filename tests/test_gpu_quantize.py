@@ -72,3 +72,23 @@ def test_fill_normal_moments(hip):
     hip.fill_normal(buf2, n, seed=123, mean=0.0, std=0.02)
     hip.synchronize(hip.stream(0))
     assert np.array_equal(buf2.download(np.float32).view(np.uint32), v.view(np.uint32))
+
+
+def test_extent_checks_refuse_short_buffers(hip):
+    """Buffers shorter than the shape implies are refused on the host, before
+    any launch (the C ABI checks every device pointer's allocation extent)."""
+    lib = hip.load()
+    buf = hip.DeviceBuffer(4 * 1000)
+    rc = lib.mlq_hip_fill_normal(buf.ptr, 1001, 1, 0.0, 1.0, None)
+    assert rc == 6 and "buffer is too small" in hip.last_error()
+    src = hip.DeviceBuffer(4 * 64 * 64)
+    dst = hip.DeviceBuffer(64 * 2 * 18 - 1)
+    rc = lib.mlq_hip_quantize(0, 2, src.ptr, 64, 64, dst.ptr, None)
+    assert rc == 6 and "block buffer is too small" in hip.last_error()
+    rc = lib.mlq_hip_quantize(0, 2, src.ptr + 4, 64, 64, dst.ptr, None)
+    assert rc == 6 and "source buffer is too small" in hip.last_error()
+    wb = hip.DeviceBuffer(8 * 18)
+    x = hip.DeviceBuffer(4 * 63)
+    y = hip.DeviceBuffer(4 * 4)
+    rc = lib.mlq_hip_quant_linear_device(0, 2, wb.ptr, 8, 4, 64, x.ptr, 1, y.ptr, None)
+    assert rc == 6 and "input buffer is too small" in hip.last_error()
