@@ -76,19 +76,25 @@ def test_fill_normal_moments(hip):
 
 def test_extent_checks_refuse_short_buffers(hip):
     """Buffers shorter than the shape implies are refused on the host, before
-    any launch (the C ABI checks every device pointer's allocation extent)."""
+    any launch (the C ABI checks every device pointer's allocation extent).
+    Buffers are 2 MiB so that allocation rounding cannot hide the overrun."""
     lib = hip.load()
-    buf = hip.DeviceBuffer(4 * 1000)
-    rc = lib.mlq_hip_fill_normal(buf.ptr, 1001, 1, 0.0, 1.0, None)
+    two_mib = 2 << 20
+    buf = hip.DeviceBuffer(two_mib)
+    rc = lib.mlq_hip_fill_normal(buf.ptr, two_mib // 4 + 1, 1, 0.0, 1.0, None)
     assert rc == 6 and "buffer is too small" in hip.last_error()
-    src = hip.DeviceBuffer(4 * 64 * 64)
-    dst = hip.DeviceBuffer(64 * 2 * 18 - 1)
-    rc = lib.mlq_hip_quantize(0, 2, src.ptr, 64, 64, dst.ptr, None)
-    assert rc == 6 and "block buffer is too small" in hip.last_error()
-    rc = lib.mlq_hip_quantize(0, 2, src.ptr + 4, 64, 64, dst.ptr, None)
+    rows, k = 2048, 1024                      # 8 MiB of f32, 2048*32*18 = 1.1 MiB of blocks
+    src = hip.DeviceBuffer(two_mib)           # too short for the source
+    dst = hip.DeviceBuffer(two_mib)
+    rc = lib.mlq_hip_quantize(0, 2, src.ptr, rows, k, dst.ptr, None)
     assert rc == 6 and "source buffer is too small" in hip.last_error()
-    wb = hip.DeviceBuffer(8 * 18)
-    x = hip.DeviceBuffer(4 * 63)
-    y = hip.DeviceBuffer(4 * 4)
-    rc = lib.mlq_hip_quant_linear_device(0, 2, wb.ptr, 8, 4, 64, x.ptr, 1, y.ptr, None)
+    src2 = hip.DeviceBuffer(8 << 20)
+    rc = lib.mlq_hip_quantize(0, 1, src2.ptr, rows, k, dst.ptr, None)  # Q8_0 needs 2.1 MiB
+    assert rc == 6 and "block buffer is too small" in hip.last_error()
+    k = two_mib // 4 + 32
+    nb = (k + 31) // 32
+    wb = hip.DeviceBuffer(4 * nb * 18)
+    x = hip.DeviceBuffer(two_mib)
+    y = hip.DeviceBuffer(16)
+    rc = lib.mlq_hip_quant_linear_device(0, 2, wb.ptr, 4 * nb, 4, k, x.ptr, 1, y.ptr, None)
     assert rc == 6 and "input buffer is too small" in hip.last_error()
