@@ -204,6 +204,48 @@ def gemv_shape_bench(name, qt, m, k, stream, reps_target=400):
     return res
 
 
+GEMM_CONFIGS = [(qt, m, 4096, n) for qt in (hip.Q8_0, hip.Q4_0) for m in (4096, 11008) for n in (16, 64, 512)]
+
+
+def gemm_shape_bench(qt, m, k, n, stream, reps_target=100):
+    """Y[N, M] = X[N, K] . W^T through the MFMA path, with
+    weight copies cycled so the working set exceeds the MALL."""
+    wbytes = m * ((k + 31) // 32) * BB[qt]
+    copies = max(8, math.ceil(1e9 / wbytes))
+    tmp = hip.DeviceBuffer(4 * m * k)
+    base = make_weight(qt, m, k, 777 + m + n + qt, tmp)
+    tmp.free()
+    bufs = [base._keep]
+    for _ in range(copies - 1):
+        b = hip.DeviceBuffer(wbytes)
+        hip.load().mlq_hip_memcpy_dtod(b.ptr, base._keep.ptr, wbytes, None)
+        bufs.append(b)
+    ws = [hip.Weight.wrap(qt, b, m * ((k + 31) // 32), m, k) for b in bufs]
+    x = hip.DeviceBuffer(4 * n * k)
+    hip.fill_normal(x, n * k, 31 + n, 0.0, 1.0)
+    y = hip.DeviceBuffer(4 * n * m)
+    calls = hip.make_calls([(w, x, y, n) for w in ws])
+    graph = hip.Graph(calls, stream)
+    hip.synchronize(stream)
+    loops = max(1, reps_target // copies)
+    graph.launch(stream)
+    ms = time_region(lambda: graph.launch(stream), loops, stream)
+    graph.destroy()
+    us = ms * 1e3 / (loops * copies)
+    flops = 2.0 * m * k * n
+    tflops = flops / (us * 1e-6) / 1e12
+    bytes_ = wbytes + 4.0 * n * k + 4.0 * n * m
+    res = {"fmt": FMT_NAME[qt], "M": m, "K": k, "N": n, "us_per_call": round(us, 2),
+           "tflops": round(tflops, 2), "frac_of_fp16_dense_peak": round(tflops / FP16_PEAK_TFLOPS, 4),
+           "gbs": round(bytes_ / (us * 1e-6) / 1e9, 1), "kernel": hip.kernel_name(qt, n, m, k),
+           "note": "useful flops 2*M*K*N; the kernel issues 2x that on MFMA (x split hi+lo fp16)"}
+    for w in ws:
+        w.free()
+    for b in bufs:
+        b.free()
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -211,7 +253,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--launch", choices=["graph", "plain"], default="graph")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline / parity leg")
-    ap.add_argument("--no-shapes", action="store_true", help="skip the per-shape GEMV table")
+    ap.add_argument("--no-shapes", action="store_true", help="skip the per-shape GEMV / GEMM tables")
     ap.add_argument("--layers", type=int, default=32)
     args = ap.parse_args()
 
@@ -256,6 +298,15 @@ def main():
                 f"{r['gbs']:8.1f} GB/s ({100 * r['frac_of_peak']:.1f}%) {r['kernel']}")
             shapes.append(r)
 
+    gemm = []
+    if not args.no_shapes:
+        for cfg in GEMM_CONFIGS:
+            r = gemm_shape_bench(*cfg, stream)
+            log(f"  gemm {r['fmt']} {r['M']:>6}x{r['K']:<5} N={r['N']:<4} {r['us_per_call']:9.2f} us "
+                f"{r['tflops']:8.1f} TFLOP/s ({100 * r['frac_of_fp16_dense_peak']:.1f}% of fp16 peak) "
+                f"{r['gbs']:8.1f} GB/s {r['kernel']}")
+            gemm.append(r)
+
     cpu = None
     parity = None
     if not args.no_cpu:
@@ -298,6 +349,7 @@ def main():
         "cpu_baseline": cpu,
         "parity": parity,
         "gemv": shapes,
+        "gemm": gemm,
     }
     print(json.dumps(out), flush=True)
 

@@ -12,6 +12,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdio>
 #include <cstring>
 #include <mutex>
@@ -56,6 +57,14 @@ int hip_fail(hipError_t e, const char* what) {
 
 constexpr int kMaxDevices = 64;
 
+// GEMM workspace, one per stream that ran a batched call (grow-only, kept
+// until the process ends).
+struct Workspace {
+    hipStream_t stream;
+    void* ptr;
+    size_t bytes;
+};
+
 struct DeviceState {
     std::once_flag once;
     hipError_t init_err = hipSuccess;
@@ -63,6 +72,8 @@ struct DeviceState {
     std::mutex mu;             // guards the host-pointer staging buffers
     void* stage = nullptr;     // x and y staging for host-pointer calls
     size_t stage_bytes = 0;
+    std::mutex ws_mu;          // guards the GEMM workspaces
+    std::vector<Workspace> ws;
 };
 
 DeviceState g_dev[kMaxDevices];
@@ -171,10 +182,45 @@ int validate_linear(int qtype, int M, int K, size_t n_blocks, int rows) {
     return MLQ_OK;
 }
 
-hipError_t dispatch(const mlq::LinearShape& s, const void* w, const float* x, float* y,
-                    hipStream_t stream) {
-    if (s.rows > 1 && mlq::gemm_supported(s)) return mlq::launch_gemm(s, w, x, y, stream);
-    return mlq::launch_gemv(s, w, x, y, stream);
+// Returns a workspace of at least `bytes` for `stream` on `device`.  Growing
+// waits for the stream first so a buffer is never freed under a running kernel.
+int stream_workspace(int device, hipStream_t stream, size_t bytes, void** out) {
+    DeviceState& st = g_dev[device];
+    std::lock_guard<std::mutex> lock(st.ws_mu);
+    for (Workspace& w : st.ws) {
+        if (w.stream != stream) continue;
+        if (w.bytes < bytes) {
+            MLQ_HIP_CHECK(hipStreamSynchronize(stream));
+            MLQ_HIP_CHECK(hipFree(w.ptr));
+            w.ptr = nullptr;
+            w.bytes = 0;
+            MLQ_HIP_CHECK(hipMalloc(&w.ptr, bytes));
+            w.bytes = bytes;
+        }
+        *out = w.ptr;
+        return MLQ_OK;
+    }
+    void* p = nullptr;
+    MLQ_HIP_CHECK(hipMalloc(&p, bytes));
+    st.ws.push_back(Workspace{stream, p, bytes});
+    *out = p;
+    return MLQ_OK;
+}
+
+int dispatch(int device, const mlq::LinearShape& s, const void* w, const float* x, float* y,
+             hipStream_t stream) {
+    hipError_t e;
+    if (s.rows > 1 && mlq::gemm_supported(s)) {
+        const size_t need = mlq::gemm_workspace_bytes(s);
+        void* ws = nullptr;
+        int rc = stream_workspace(device, stream, need, &ws);
+        if (rc != MLQ_OK) return rc;
+        e = mlq::launch_gemm(s, w, x, y, ws, need, stream);
+    } else {
+        e = mlq::launch_gemv(s, w, x, y, stream);
+    }
+    if (e != hipSuccess) return hip_fail(e, caller_for(s.qtype));
+    return MLQ_OK;
 }
 
 int grow_stage(DeviceState& st, size_t bytes) {
@@ -327,9 +373,7 @@ int mlq_hip_quant_linear_device(int device, int qtype, const void* device_blocks
     if ((rc = check_device_ptr(x, device, caller, "input", xbytes)) != MLQ_OK) return rc;
     if ((rc = check_device_ptr(y, device, caller, "output", ybytes)) != MLQ_OK) return rc;
     mlq::LinearShape s{qtype, out_features, in_features, (in_features + 31) / 32, rows};
-    hipError_t e = dispatch(s, device_blocks, x, y, resolve_stream(device, stream));
-    if (e != hipSuccess) return hip_fail(e, caller);
-    return MLQ_OK;
+    return dispatch(device, s, device_blocks, x, y, resolve_stream(device, stream));
 }
 
 int mlq_hip_quant_linear(mlq_weight_t w, const float* x, int rows, float* y, int flags,
@@ -356,8 +400,7 @@ int mlq_hip_quant_linear(mlq_weight_t w, const float* x, int rows, float* y, int
     if (xd && (rc = check_device_ptr(x, w->device, caller, "input", xb)) != MLQ_OK) return rc;
     if (yd && (rc = check_device_ptr(y, w->device, caller, "output", yb)) != MLQ_OK) return rc;
     if (xd && yd) {
-        hipError_t e = dispatch(shape, w->ptr, x, y, s);
-        if (e != hipSuccess) return hip_fail(e, caller);
+        if ((rc = dispatch(w->device, shape, w->ptr, x, y, s)) != MLQ_OK) return rc;
         if (!(flags & MLQ_ASYNC)) MLQ_HIP_CHECK(hipStreamSynchronize(s));
         return MLQ_OK;
     }
@@ -374,8 +417,7 @@ int mlq_hip_quant_linear(mlq_weight_t w, const float* x, int rows, float* y, int
         xdev = reinterpret_cast<const float*>(base + xoff);
     }
     if (!yd) ydev = reinterpret_cast<float*>(base + yoff);
-    hipError_t e = dispatch(shape, w->ptr, xdev, ydev, s);
-    if (e != hipSuccess) return hip_fail(e, caller);
+    if ((rc = dispatch(w->device, shape, w->ptr, xdev, ydev, s)) != MLQ_OK) return rc;
     if (!yd) MLQ_HIP_CHECK(hipMemcpyAsync(y, ydev, yb, hipMemcpyDeviceToHost, s));
     MLQ_HIP_CHECK(hipStreamSynchronize(s));
     return MLQ_OK;
@@ -407,8 +449,7 @@ int mlq_hip_quant_linear_many(const mlq_linear_call* calls, int n, void* stream)
     for (int i = 0; i < n; ++i) {
         const mlq_linear_call& c = calls[i];
         mlq::LinearShape shape{c.w->qtype, c.w->M, c.w->K, c.w->nb, c.rows};
-        hipError_t e = dispatch(shape, c.w->ptr, c.x, c.y, s);
-        if (e != hipSuccess) return hip_fail(e, caller_for(c.w->qtype));
+        if ((rc = dispatch(device, shape, c.w->ptr, c.x, c.y, s)) != MLQ_OK) return rc;
     }
     return MLQ_OK;
 }
@@ -446,41 +487,53 @@ int mlq_hip_free(void* ptr) {
     return MLQ_OK;
 }
 
+// Copies and fills run on the library's stream for the current device and
+// wait for it, so they are ordered after every launch the library made there
+// (that stream does not synchronize with the null stream).
 int mlq_hip_memcpy_htod(void* dst, const void* src, size_t bytes) {
     int dev = 0;
     MLQ_HIP_CHECK(hipGetDevice(&dev));
-    int rc = check_device_ptr(dst, dev, "mlq_hip_memcpy_htod", "destination", bytes);
+    int rc = ensure_device(dev);
+    if (rc == MLQ_OK) rc = check_device_ptr(dst, dev, "mlq_hip_memcpy_htod", "destination", bytes);
     if (rc != MLQ_OK) return rc;
-    MLQ_HIP_CHECK(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+    hipStream_t s = g_dev[dev].stream;
+    MLQ_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, s));
+    MLQ_HIP_CHECK(hipStreamSynchronize(s));
     return MLQ_OK;
 }
 
 int mlq_hip_memcpy_dtoh(void* dst, const void* src, size_t bytes) {
     int dev = 0;
     MLQ_HIP_CHECK(hipGetDevice(&dev));
-    int rc = check_device_ptr(src, dev, "mlq_hip_memcpy_dtoh", "source", bytes);
+    int rc = ensure_device(dev);
+    if (rc == MLQ_OK) rc = check_device_ptr(src, dev, "mlq_hip_memcpy_dtoh", "source", bytes);
     if (rc != MLQ_OK) return rc;
-    MLQ_HIP_CHECK(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
+    hipStream_t s = g_dev[dev].stream;
+    MLQ_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, s));
+    MLQ_HIP_CHECK(hipStreamSynchronize(s));
     return MLQ_OK;
 }
 
 int mlq_hip_memcpy_dtod(void* dst, const void* src, size_t bytes, void* stream) {
     int dev = 0;
     MLQ_HIP_CHECK(hipGetDevice(&dev));
-    int rc = check_device_ptr(dst, dev, "mlq_hip_memcpy_dtod", "destination", bytes);
+    int rc = ensure_device(dev);
+    if (rc == MLQ_OK) rc = check_device_ptr(dst, dev, "mlq_hip_memcpy_dtod", "destination", bytes);
     if (rc == MLQ_OK) rc = check_device_ptr(src, dev, "mlq_hip_memcpy_dtod", "source", bytes);
     if (rc != MLQ_OK) return rc;
-    MLQ_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice,
-                                 stream ? static_cast<hipStream_t>(stream) : g_dev[dev].stream));
+    MLQ_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, resolve_stream(dev, stream)));
     return MLQ_OK;
 }
 
 int mlq_hip_memset(void* ptr, int value, size_t bytes) {
     int dev = 0;
     MLQ_HIP_CHECK(hipGetDevice(&dev));
-    int rc = check_device_ptr(ptr, dev, "mlq_hip_memset", "destination", bytes);
+    int rc = ensure_device(dev);
+    if (rc == MLQ_OK) rc = check_device_ptr(ptr, dev, "mlq_hip_memset", "destination", bytes);
     if (rc != MLQ_OK) return rc;
-    MLQ_HIP_CHECK(hipMemset(ptr, value, bytes));
+    hipStream_t s = g_dev[dev].stream;
+    MLQ_HIP_CHECK(hipMemsetAsync(ptr, value, bytes, s));
+    MLQ_HIP_CHECK(hipStreamSynchronize(s));
     return MLQ_OK;
 }
 
@@ -553,18 +606,33 @@ int mlq_hip_graph_capture_many(const mlq_linear_call* calls, int n, void* stream
         if ((rc = check_device_ptr(c.y, device, caller, "output", yb)) != MLQ_OK) return rc;
     }
     hipStream_t s = resolve_stream(device, stream);
-    MLQ_HIP_CHECK(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
-    hipError_t launch_err = hipSuccess;
-    for (int i = 0; i < n && launch_err == hipSuccess; ++i) {
+    // Batched calls need the stream's GEMM workspace; size it for the largest
+    // before capture (no allocation may happen inside a capture).  All batched
+    // nodes of the graph run in stream order and share it.
+    size_t ws_need = 0;
+    for (int i = 0; i < n; ++i) {
         const mlq_linear_call& c = calls[i];
         mlq::LinearShape shape{c.w->qtype, c.w->M, c.w->K, c.w->nb, c.rows};
-        launch_err = dispatch(shape, c.w->ptr, c.x, c.y, s);
+        if (c.rows > 1 && mlq::gemm_supported(shape)) {
+            ws_need = std::max(ws_need, mlq::gemm_workspace_bytes(shape));
+        }
+    }
+    if (ws_need > 0) {
+        void* ws = nullptr;
+        if ((rc = stream_workspace(device, s, ws_need, &ws)) != MLQ_OK) return rc;
+    }
+    MLQ_HIP_CHECK(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+    int launch_rc = MLQ_OK;
+    for (int i = 0; i < n && launch_rc == MLQ_OK; ++i) {
+        const mlq_linear_call& c = calls[i];
+        mlq::LinearShape shape{c.w->qtype, c.w->M, c.w->K, c.w->nb, c.rows};
+        launch_rc = dispatch(device, shape, c.w->ptr, c.x, c.y, s);
     }
     hipGraph_t graph = nullptr;
     hipError_t end_err = hipStreamEndCapture(s, &graph);
-    if (launch_err != hipSuccess) {
+    if (launch_rc != MLQ_OK) {
         if (graph) (void)hipGraphDestroy(graph);
-        return hip_fail(launch_err, "graph capture launch");
+        return launch_rc;
     }
     if (end_err != hipSuccess) return hip_fail(end_err, "hipStreamEndCapture");
     hipGraphExec_t exec = nullptr;

@@ -35,12 +35,15 @@ hipError_t launch_gemv(const LinearShape& s, const void* w, const float* x, floa
                        hipStream_t stream);
 const char* gemv_kernel_name(const LinearShape& s);
 
-// Batched prefill GEMM for rows > 1: LDS-dequantised MFMA.  Returns
-// hipErrorNotSupported when the shape has no MFMA path (caller falls back).
-hipError_t launch_gemm(const LinearShape& s, const void* w, const float* x, float* y,
-                       hipStream_t stream);
-const char* gemm_kernel_name(const LinearShape& s);
+// Batched prefill GEMM for rows > 1 (MFMA).  Needs a device workspace of
+// gemm_workspace_bytes(s) bytes (split x, scales, split-K partials) that no
+// other launch uses concurrently.  Returns hipErrorNotSupported when the shape
+// has no MFMA path (the caller runs the GEMV kernels per row instead).
 bool gemm_supported(const LinearShape& s);
+size_t gemm_workspace_bytes(const LinearShape& s);
+hipError_t launch_gemm(const LinearShape& s, const void* w, const float* x, float* y, void* ws,
+                       size_t ws_bytes, hipStream_t stream);
+const char* gemm_kernel_name(const LinearShape& s);
 
 // Device quantizer and synthetic-data generator.
 hipError_t launch_quantize(int qtype, const float* src, int rows, int row_len, void* dst,

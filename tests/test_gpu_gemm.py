@@ -1,0 +1,66 @@
+"""GPU parity of the batched prefill GEMM (rows > 1, MFMA path) against the oracle.
+
+X f32 N(0,1) with N = 16 / 64 / 512 token rows, W Q8_0
+and Q4_0 at 4096x4096 and 11008x4096 (N(0,0.02), reference quantiser); Q4_1
+and ragged shapes in addition.  Bound: tests/tolerance.py (BASELINE and the
+reference's own criterion)."""
+
+import os
+import sys
+
+import numpy as np
+import pytest
+
+import oracle
+from tolerance import check_close
+
+pytestmark = pytest.mark.gpu
+
+FMTS = {"q8_0": oracle.Q8_0, "q4_0": oracle.Q4_0, "q4_1": oracle.Q4_1}
+THREADS = min(16, os.cpu_count() or 1)
+
+
+def run(hip, orc, qt, m, k, n, seed=0, scale_rows=None):
+    rng = np.random.default_rng(500 + m + k + n + seed)
+    w = (rng.standard_normal((m, k), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+    x = rng.standard_normal((n, k), dtype=np.float32)
+    if scale_rows is not None:
+        x *= np.asarray(scale_rows, np.float32)[:, None]
+    blocks = orc.quantize(qt, w, threads=THREADS)
+    want = orc.linear(qt, x, blocks, m, threads=THREADS)
+    name = hip.kernel_name(qt, n, m, k)
+    print(f"gemm qt={qt} M={m} K={k} N={n} kernel={name}", flush=True)
+    wt = hip.Weight.upload(qt, blocks, m, k)
+    got = wt.linear_host(x)
+    wt.free()
+    return name, check_close(got, want, x, qt, blocks, f"gemm qt={qt} {m}x{k} N={n}")
+
+
+@pytest.mark.parametrize("n", [16, 64, 512])
+@pytest.mark.parametrize("shape", [(4096, 4096), (11008, 4096)], ids=lambda s: f"{s[0]}x{s[1]}")
+def test_gemm_baseline_config4(hip, orc, shape, n):
+    for fmt in ("q8_0", "q4_0"):
+        name, _ = run(hip, orc, FMTS[fmt], *shape, n)
+        assert name.startswith("gemm_mfma"), name
+
+
+@pytest.mark.parametrize("m,k,n", [(4096, 4096, 16), (64, 64, 2), (33, 4096, 17), (300, 896, 40),
+                                   (4864, 896, 7), (17, 64, 100), (1000, 11008, 3)])
+def test_gemm_q4_1_and_ragged(hip, orc, m, k, n):
+    for fmt, qt in FMTS.items():
+        run(hip, orc, qt, m, k, n)
+
+
+def test_gemm_wide_dynamic_range(hip, orc):
+    """Per-token power-of-two scaling keeps the hi/lo split exact across token
+    magnitudes from 1e-6 to 1e4 (and an all-zero token)."""
+    scales = [1e-6, 1.0, 1e4, 0.0, 3.5, 1e-3, 250.0, 1.0]
+    for fmt, qt in FMTS.items():
+        run(hip, orc, qt, 512, 4096, len(scales), scale_rows=scales)
+
+
+def test_gemm_odd_block_count_uses_gemv_rows(hip, orc):
+    # K=4095 has an even block count (tail 31); K=100 has 4 blocks; K=4064+32 odd count -> GEMV per row
+    for m, k, n in [(64, 4095, 5), (64, 100, 3), (48, 4128, 4)]:
+        for fmt, qt in FMTS.items():
+            run(hip, orc, qt, m, k, n)
