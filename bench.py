@@ -255,6 +255,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline / parity leg")
     ap.add_argument("--no-shapes", action="store_true", help="skip the per-shape GEMV / GEMM tables")
     ap.add_argument("--layers", type=int, default=32)
+    ap.add_argument("--calibration-copy-mb", type=int, default=0,
+                    help="before timing, run one device-to-device copy of this many MiB: a kernel of "
+                         "known traffic that scales the rocprofv3 FETCH_SIZE / WRITE_SIZE counters")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -270,6 +273,15 @@ def main():
     t0 = time.time()
     sw = Sweep(layers=args.layers)
     log(f"sweep ready: {sw.n()} calls, {sw.bytes / 1e9:.3f} GB, setup {time.time() - t0:.1f}s")
+
+    if args.calibration_copy_mb > 0:
+        nbytes = args.calibration_copy_mb << 20
+        src, dst = hip.DeviceBuffer(nbytes), hip.DeviceBuffer(nbytes)
+        hip.load().mlq_hip_memcpy_dtod(dst.ptr, src.ptr, nbytes, stream)
+        hip.synchronize(stream)
+        log(f"calibration copy: {nbytes} bytes read and written")
+        src.free()
+        dst.free()
 
     if args.launch == "graph":
         graph = hip.Graph(sw.calls, stream)
