@@ -46,6 +46,21 @@ BB = {hip.Q8_0: 34, hip.Q4_0: 18, hip.Q4_1: 20}
 FMT_NAME = {hip.Q8_0: "q8_0", hip.Q4_0: "q4_0", hip.Q4_1: "q4_1"}
 
 
+TRAFFIC_PROFILE = os.path.join(REPO, "profiles", "gemv_q4_0_llama7b_sweep_hbm_traffic.md")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the sweep from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary (calibrated against a copy of known size), or None."""
+    try:
+        for line in open(TRAFFIC_PROFILE):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
@@ -357,7 +372,10 @@ def main():
                    "sweep_us": round(ms_step * 1e3, 1),
                    "sweep_us_other_launch_mode": round(alt * 1e3, 1)},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+                     "algorithmic_bytes_per_launch": round(sw.bytes / sw.n()),
+                     "avg_launch_us": round(ms_step * 1e3 / sw.n(), 3),
+                     "kernel": "Q4_0 GEMV family (gemv_single / gemv_multi), all launches of the step"},
         "cpu_baseline": cpu,
         "parity": parity,
         "gemv": shapes,
