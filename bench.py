@@ -129,6 +129,15 @@ class Sweep:
     def n(self):
         return len(self.calls_desc)
 
+    def stage_ids(self):
+        """Decode data flow per layer: q,k,v share x | o | gate,up share x | down;
+        lm_head last.  Every change of id is a dependency barrier."""
+        ids = []
+        for l in range(len(self.calls_desc) // len(LAYER)):
+            ids += [4 * l, 4 * l, 4 * l, 4 * l + 1, 4 * l + 2, 4 * l + 2, 4 * l + 3]
+        ids.append(ids[-1] + 1 if ids else 0)
+        return ids
+
 
 def cpu_sweep_check(sw: Sweep, threads: int):
     """Run the reference CPU linear over the whole sweep on the same blocks,
@@ -266,7 +275,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--launch", choices=["graph", "plain"], default="graph")
+    ap.add_argument("--launch", choices=["graph", "plain", "sequence", "per_stage", "independent"],
+                    default="sequence")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline / parity leg")
     ap.add_argument("--no-shapes", action="store_true", help="skip the per-shape GEMV / GEMM tables")
     ap.add_argument("--layers", type=int, default=32)
@@ -298,24 +308,48 @@ def main():
         src.free()
         dst.free()
 
-    if args.launch == "graph":
-        graph = hip.Graph(sw.calls, stream)
-        step = lambda: graph.launch(stream)  # noqa: E731
-    else:
-        step = lambda: hip.linear_many(sw.calls, stream)  # noqa: E731
+    # Every way of running the sweep; `--launch` picks the headline.
+    #   graph / plain: one launch per call (225), captured as a graph or issued from C;
+    #   sequence:  one persistent launch, barriers between the 129 dependent stages;
+    #   per_stage: one grouped launch per stage (129), captured as a graph;
+    #   independent: one persistent launch without barriers (the sweep's inputs are
+    #              all fresh, so nothing depends on anything; reported, not headline).
+    seqs = {m: hip.Sequence(sw.calls, sw.stage_ids(), mode)
+            for m, mode in (("sequence", hip.SEQ_PERSISTENT), ("per_stage", hip.SEQ_PER_STAGE),
+                            ("independent", hip.SEQ_INDEPENDENT))}
+    graph = hip.Graph(sw.calls, stream)
+    stage_graph = hip.Graph(sequence=seqs["per_stage"])
+    steps_by_mode = {
+        "graph": lambda: graph.launch(stream),
+        "plain": lambda: hip.linear_many(sw.calls, stream),
+        "sequence": lambda: seqs["sequence"].launch(stream),
+        "per_stage": lambda: stage_graph.launch(stream),
+        "independent": lambda: seqs["independent"].launch(stream),
+    }
+    variants = {}
+    for name, fn in steps_by_mode.items():
+        for _ in range(args.warmup):
+            fn()
+        hip.synchronize(stream)
+        variants[name] = time_region(fn, args.steps, stream) / args.steps
+        for sq in seqs.values():
+            if sq.status() != 0:
+                raise SystemExit(f"sweep {name}: a sequence barrier wait timed out")
+        log(f"sweep {name:12s}: {variants[name] * 1e3:8.1f} us/step, "
+            f"{sw.bytes / (variants[name] * 1e-3) / 1e9:8.1f} GB/s")
+    # The headline mode runs last before the parity check, so the outputs the
+    # CPU compares are the headline's.
+    step = steps_by_mode[args.launch]
     for _ in range(args.warmup):
         step()
     hip.synchronize(stream)
+    for y in sw.ys:
+        y.fill(0)
     ms = time_region(step, args.steps, stream)
     ms_step = ms / args.steps
     gbs = sw.bytes / (ms_step * 1e-3) / 1e9
-    # the other launch mode, for reference
-    if args.launch == "graph":
-        alt = time_region(lambda: hip.linear_many(sw.calls, stream), args.steps, stream) / args.steps
-    else:
-        g2 = hip.Graph(sw.calls, stream)
-        alt = time_region(lambda: g2.launch(stream), args.steps, stream) / args.steps
-    log(f"sweep: {ms_step * 1e3:.1f} us/step, {gbs:.1f} GB/s ({args.launch}); other mode {alt * 1e3:.1f} us")
+    seq_info = seqs["sequence"].info()
+    log(f"sweep: {ms_step * 1e3:.1f} us/step, {gbs:.1f} GB/s ({args.launch}); sequence {seq_info}")
 
     shapes = []
     if not args.no_shapes:
@@ -368,9 +402,10 @@ def main():
         "dtype": "f32",
         "data": "synthetic (device-generated N(0,0.02) weights quantized by the reference's Q4_0 rule, x~N(0,1))",
         "config": {"workload": "llama7b_q4_0_decode_linear_sweep", "layers": args.layers,
-                   "calls_per_step": sw.n(), "bytes_per_step": sw.bytes, "launch": args.launch,
+                   "calls_per_step": sw.n(), "stages_per_step": seq_info["stages"],
+                   "bytes_per_step": sw.bytes, "launch": args.launch,
                    "sweep_us": round(ms_step * 1e3, 1),
-                   "sweep_us_other_launch_mode": round(alt * 1e3, 1)},
+                   "sweep_us_by_launch": {k: round(v * 1e3, 1) for k, v in variants.items()}},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "algorithmic_bytes_per_launch": round(sw.bytes / sw.n()),

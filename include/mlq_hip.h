@@ -155,6 +155,44 @@ int mlq_hip_graph_capture_many(const mlq_linear_call* calls, int n, void* stream
 int mlq_hip_graph_launch(mlq_graph_t g, void* stream);
 int mlq_hip_graph_destroy(mlq_graph_t g);
 
+/* A decode step's chain of GEMVs run as one persistent launch (per run of
+ * same-format stages).  No counterpart in the reference, whose forward pass
+ * launches one kernel per linear (src/forward.cpp:172-227, through
+ * src/cuda_quant.cu:289-496); per call the results equal those of
+ * mlq_hip_quant_linear on the same inputs, bit for bit.
+ *
+ * calls[i] are GEMV calls (rows == 1) on one device, with an even number of
+ * blocks per row and at most 15 360 input features.  Consecutive calls with
+ * equal stage[i] form one stage (at most 4 calls): they read the same x, run
+ * concurrently, and no call of the stage writes where the stage reads or
+ * another of its calls writes.  stage == NULL puts every call in a stage of
+ * its own.  No y may overlap any weight of the sequence.
+ * Modes:
+ *   MLQ_SEQ_PERSISTENT   one launch; each stage starts after every earlier
+ *                        stage has written its outputs (device-wide barrier),
+ *                        so a call may read any earlier call's y;
+ *   MLQ_SEQ_PER_STAGE    one launch per stage, ordered by the stream (same
+ *                        semantics, no device-wide barrier);
+ *   MLQ_SEQ_INDEPENDENT  one launch without barriers: no call may read any
+ *                        call's output (checked when the sequence is created).
+ * The sequence keeps the pointers (buffers must outlive it and any graph
+ * captured from it); launches of one sequence must not overlap in time. */
+typedef struct mlq_sequence_s* mlq_sequence_t;
+#define MLQ_SEQ_PERSISTENT 0
+#define MLQ_SEQ_PER_STAGE 1
+#define MLQ_SEQ_INDEPENDENT 2
+int mlq_hip_sequence_create(const mlq_linear_call* calls, int n, const int* stage, int mode,
+                            mlq_sequence_t* out);
+int mlq_hip_sequence_launch(mlq_sequence_t seq, void* stream);
+/* After the launch's stream has been synchronized: the number of launches
+ * whose device-wide barrier wait gave up (outputs void), then cleared. */
+int mlq_hip_sequence_status(mlq_sequence_t seq, int* barrier_timeouts);
+/* Bound of each barrier wait in polls (default 1 << 20, about a second). */
+int mlq_hip_sequence_set_spin_limit(mlq_sequence_t seq, unsigned polls);
+int mlq_hip_sequence_info(mlq_sequence_t seq, int* stages, int* launches, int* grid);
+int mlq_hip_sequence_destroy(mlq_sequence_t seq);
+int mlq_hip_graph_capture_sequence(mlq_sequence_t seq, void* stream, mlq_graph_t* out);
+
 /* Fill an f32 device array with N(mean, std) from a counter-based generator
  * (splitmix64 + Box-Muller) -- synthetic weights and inputs for benchmarks. */
 int mlq_hip_fill_normal(float* device_dst, size_t n, uint64_t seed, float mean, float stddev,

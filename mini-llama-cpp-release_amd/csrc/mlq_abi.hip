@@ -36,6 +36,26 @@ struct mlq_graph_s {
     int device;
 };
 
+// A validated chain of GEMVs: stage descriptors and barrier words in device
+// memory, split into launches (segments) of one kernel variant each.
+struct mlq_sequence_s {
+    struct Segment {
+        int qtype;
+        int lpr;
+        int stage_begin;
+        int nstages;
+        int lds_bytes;
+        int grid;
+    };
+    int device;
+    int mode;
+    int nstages;
+    unsigned spin_limit;
+    std::vector<Segment> segs;
+    void* mem;               // [stage descriptors][SeqSync per segment]
+    size_t sync_offset;      // byte offset of the first SeqSync
+};
+
 namespace {
 
 thread_local std::string g_error;
@@ -681,6 +701,278 @@ int mlq_hip_kernel_name(int qtype, int rows, int out_features, int in_features, 
     const char* name = (rows > 1 && mlq::gemm_supported(s)) ? mlq::gemm_kernel_name(s)
                                                                : mlq::gemv_kernel_name(s);
     std::snprintf(buf, len, "%s", name);
+    return MLQ_OK;
+}
+
+}  // extern "C"
+
+// ---- sequences --------------------------------------------------------------
+
+namespace {
+
+struct Range {
+    uintptr_t lo;
+    uintptr_t hi;
+};
+
+bool overlaps(const Range& a, const Range& b) { return a.lo < b.hi && b.lo < a.hi; }
+
+Range range_of(const void* p, size_t bytes) {
+    const uintptr_t lo = reinterpret_cast<uintptr_t>(p);
+    return Range{lo, lo + bytes};
+}
+
+constexpr unsigned kDefaultSpinLimit = 1u << 20;
+
+}  // namespace
+
+extern "C" {
+
+int mlq_hip_sequence_create(const mlq_linear_call* calls, int n, const int* stage, int mode,
+                            mlq_sequence_t* out) {
+    static const char* caller = "mlq_hip_sequence_create";
+    if (out == nullptr) return fail(MLQ_ERR_INVALID, std::string(caller) + ": null output");
+    *out = nullptr;
+    if (calls == nullptr || n <= 0) return fail(MLQ_ERR_INVALID, std::string(caller) + ": no calls");
+    if (mode != MLQ_SEQ_PERSISTENT && mode != MLQ_SEQ_PER_STAGE && mode != MLQ_SEQ_INDEPENDENT) {
+        return fail(MLQ_ERR_INVALID, std::string(caller) + ": unknown mode " + std::to_string(mode));
+    }
+    if (calls[0].w == nullptr) return fail(MLQ_ERR_INVALID, std::string(caller) + ": null weight handle");
+    const int device = calls[0].w->device;
+    int rc = ensure_device(device);
+    if (rc != MLQ_OK) return rc;
+
+    std::vector<Range> wr(n), xr(n), yr(n);
+    for (int i = 0; i < n; ++i) {
+        const mlq_linear_call& c = calls[i];
+        const std::string at = std::string(caller) + ": call " + std::to_string(i);
+        if (c.w == nullptr) return fail(MLQ_ERR_INVALID, at + ": null weight handle");
+        if (c.w->device != device) return fail(MLQ_ERR_DEVICE, at + ": weight on a different device");
+        if (c.rows != 1) {
+            return fail(MLQ_ERR_INVALID, at + ": rows=" + std::to_string(c.rows) +
+                                             "; a sequence runs GEMV calls (rows == 1)");
+        }
+        if ((rc = validate_linear(c.w->qtype, c.w->M, c.w->K, c.w->n_blocks, 1)) != MLQ_OK) return rc;
+        if (!mlq::sequence_supported(c.w->qtype, c.w->K)) {
+            return fail(MLQ_ERR_LIMIT, at + ": in_features=" + std::to_string(c.w->K) +
+                                           " needs an even block count and at most 15360 elements");
+        }
+        const char* lin = caller_for(c.w->qtype);
+        const size_t xb = static_cast<size_t>(c.w->K) * sizeof(float);
+        const size_t yb = static_cast<size_t>(c.w->M) * sizeof(float);
+        if ((rc = check_device_ptr(c.x, device, lin, "input", xb)) != MLQ_OK) return rc;
+        if ((rc = check_device_ptr(c.y, device, lin, "output", yb)) != MLQ_OK) return rc;
+        wr[i] = range_of(c.w->ptr, c.w->n_blocks * static_cast<size_t>(mlq::block_bytes(c.w->qtype)));
+        xr[i] = range_of(c.x, xb);
+        yr[i] = range_of(c.y, yb);
+    }
+    // Outputs never overlap weights (the kernel requests weights of later
+    // stages before earlier outputs are written).
+    for (int i = 0; i < n; ++i) {
+        for (int j = 0; j < n; ++j) {
+            if (overlaps(yr[i], wr[j])) {
+                return fail(MLQ_ERR_INVALID, std::string(caller) + ": output of call " + std::to_string(i) +
+                                                 " overlaps the weight of call " + std::to_string(j));
+            }
+            if (mode == MLQ_SEQ_INDEPENDENT && overlaps(yr[i], xr[j])) {
+                return fail(MLQ_ERR_INVALID, std::string(caller) + ": output of call " + std::to_string(i) +
+                                                 " overlaps the input of call " + std::to_string(j) +
+                                                 "; MLQ_SEQ_INDEPENDENT needs independent calls");
+            }
+        }
+    }
+
+    // Stages: runs of equal stage ids (or single calls).
+    std::vector<mlq::SeqStageDesc> descs;
+    std::vector<int> stage_first;
+    for (int i = 0; i < n;) {
+        int j = i + 1;
+        if (stage != nullptr) {
+            while (j < n && stage[j] == stage[i]) ++j;
+        }
+        if (j - i > mlq::kSeqMaxCalls) {
+            return fail(MLQ_ERR_LIMIT, std::string(caller) + ": stage starting at call " + std::to_string(i) +
+                                           " has " + std::to_string(j - i) + " calls (at most " +
+                                           std::to_string(mlq::kSeqMaxCalls) + ")");
+        }
+        const mlq_weight_s* w0 = calls[i].w;
+        mlq::SeqStageDesc d;
+        std::memset(&d, 0, sizeof d);
+        d.x = calls[i].x;
+        d.K = w0->K;
+        d.nb = w0->nb;
+        d.np = w0->nb / 2;
+        const int lpr = mlq::sequence_lpr(w0->K);
+        d.nch = (d.np + lpr - 1) / lpr;
+        d.ncalls = j - i;
+        long long rows = 0;
+        for (int k = i; k < j; ++k) {
+            const mlq_linear_call& c = calls[k];
+            if (c.x != calls[i].x || c.w->K != w0->K || c.w->qtype != w0->qtype) {
+                return fail(MLQ_ERR_INVALID, std::string(caller) + ": call " + std::to_string(k) +
+                                                 " differs from call " + std::to_string(i) +
+                                                 " of its stage in input, in_features or quant type");
+            }
+            if (overlaps(yr[k], xr[k])) {
+                return fail(MLQ_ERR_INVALID, std::string(caller) + ": output of call " + std::to_string(k) +
+                                                 " overlaps its stage's input");
+            }
+            for (int m = i; m < k; ++m) {
+                if (overlaps(yr[k], yr[m])) {
+                    return fail(MLQ_ERR_INVALID, std::string(caller) + ": outputs of calls " + std::to_string(m) +
+                                                     " and " + std::to_string(k) + " of one stage overlap");
+                }
+            }
+            d.call[k - i] = mlq::SeqCallDesc{c.w->ptr, c.y, c.w->M, static_cast<int>(rows)};
+            rows += c.w->M;
+        }
+        if (rows > (1ll << 30)) return fail(MLQ_ERR_LIMIT, std::string(caller) + ": stage has too many rows");
+        d.rows = static_cast<int>(rows);
+        const int sub = 64 / lpr;
+        d.items = (d.rows + sub - 1) / sub;
+        descs.push_back(d);
+        stage_first.push_back(i);
+        i = j;
+    }
+
+    // Segments: runs of stages with one kernel variant; one per stage in
+    // per-stage mode.
+    auto seq = new mlq_sequence_s;
+    seq->device = device;
+    seq->mode = mode;
+    seq->nstages = static_cast<int>(descs.size());
+    seq->spin_limit = kDefaultSpinLimit;
+    seq->mem = nullptr;
+    for (int s = 0; s < seq->nstages; ++s) {
+        const mlq_weight_s* w0 = calls[stage_first[s]].w;
+        const int lpr = mlq::sequence_lpr(w0->K);
+        const int lds = mlq::sequence_stage_lds_bytes(w0->K);
+        bool extend = !seq->segs.empty() && mode != MLQ_SEQ_PER_STAGE;
+        if (extend) {
+            const auto& last = seq->segs.back();
+            extend = last.qtype == w0->qtype && last.lpr == lpr;
+        }
+        if (extend) {
+            auto& last = seq->segs.back();
+            last.nstages += 1;
+            last.lds_bytes = std::max(last.lds_bytes, lds);
+            descs[s].barrier = mode == MLQ_SEQ_PERSISTENT ? 1 : 0;
+        } else {
+            seq->segs.push_back(mlq_sequence_s::Segment{w0->qtype, lpr, s, 1, lds, 0});
+            descs[s].barrier = 0;
+        }
+    }
+    for (auto& g : seq->segs) {
+        hipError_t e = mlq::sequence_grid(g.qtype, g.lpr, g.lds_bytes, device, &g.grid);
+        if (e != hipSuccess) {
+            delete seq;
+            return hip_fail(e, "sequence occupancy");
+        }
+    }
+    const size_t table_bytes = descs.size() * sizeof(mlq::SeqStageDesc);
+    seq->sync_offset = (table_bytes + 255) & ~static_cast<size_t>(255);
+    const size_t total = seq->sync_offset + seq->segs.size() * sizeof(mlq::SeqSync);
+    hipError_t e = hipMalloc(&seq->mem, total);
+    if (e == hipSuccess) e = hipMemset(seq->mem, 0, total);
+    if (e == hipSuccess) e = hipMemcpy(seq->mem, descs.data(), table_bytes, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+        if (seq->mem) (void)hipFree(seq->mem);
+        delete seq;
+        return hip_fail(e, "sequence upload");
+    }
+    *out = seq;
+    return MLQ_OK;
+}
+
+int mlq_hip_sequence_launch(mlq_sequence_t seq, void* stream) {
+    if (seq == nullptr) return fail(MLQ_ERR_INVALID, "mlq_hip_sequence_launch: null sequence");
+    int rc = ensure_device(seq->device);
+    if (rc != MLQ_OK) return rc;
+    hipStream_t s = resolve_stream(seq->device, stream);
+    auto* table = static_cast<const mlq::SeqStageDesc*>(seq->mem);
+    auto* syncs = reinterpret_cast<mlq::SeqSync*>(static_cast<char*>(seq->mem) + seq->sync_offset);
+    for (size_t i = 0; i < seq->segs.size(); ++i) {
+        const auto& g = seq->segs[i];
+        const bool coherent = seq->mode == MLQ_SEQ_PERSISTENT && g.nstages > 1;
+        hipError_t e = mlq::launch_sequence(g.qtype, g.lpr, table + g.stage_begin, g.nstages, syncs + i, g.grid,
+                                            g.lds_bytes, seq->spin_limit, coherent, s);
+        if (e != hipSuccess) return hip_fail(e, mlq::sequence_kernel_name(g.qtype, g.lpr));
+    }
+    return MLQ_OK;
+}
+
+int mlq_hip_sequence_status(mlq_sequence_t seq, int* barrier_timeouts) {
+    if (seq == nullptr || barrier_timeouts == nullptr) {
+        return fail(MLQ_ERR_INVALID, "mlq_hip_sequence_status: null argument");
+    }
+    int rc = ensure_device(seq->device);
+    if (rc != MLQ_OK) return rc;
+    *barrier_timeouts = 0;
+    auto* syncs = reinterpret_cast<mlq::SeqSync*>(static_cast<char*>(seq->mem) + seq->sync_offset);
+    for (size_t i = 0; i < seq->segs.size(); ++i) {
+        unsigned err = 0;
+        MLQ_HIP_CHECK(hipMemcpy(&err, &syncs[i].error[0], sizeof err, hipMemcpyDeviceToHost));
+        if (err != 0) {
+            ++*barrier_timeouts;
+            MLQ_HIP_CHECK(hipMemset(&syncs[i].error[0], 0, sizeof(unsigned)));
+        }
+    }
+    MLQ_HIP_CHECK(hipDeviceSynchronize());
+    return MLQ_OK;
+}
+
+int mlq_hip_sequence_set_spin_limit(mlq_sequence_t seq, unsigned polls) {
+    if (seq == nullptr) return fail(MLQ_ERR_INVALID, "mlq_hip_sequence_set_spin_limit: null sequence");
+    seq->spin_limit = polls;
+    return MLQ_OK;
+}
+
+int mlq_hip_sequence_info(mlq_sequence_t seq, int* stages, int* launches, int* grid) {
+    if (seq == nullptr) return fail(MLQ_ERR_INVALID, "mlq_hip_sequence_info: null sequence");
+    if (stages) *stages = seq->nstages;
+    if (launches) *launches = static_cast<int>(seq->segs.size());
+    if (grid) *grid = seq->segs.empty() ? 0 : seq->segs[0].grid;
+    return MLQ_OK;
+}
+
+int mlq_hip_sequence_destroy(mlq_sequence_t seq) {
+    if (seq == nullptr) return MLQ_OK;
+    (void)hipSetDevice(seq->device);
+    hipError_t e = hipSuccess;
+    if (seq->mem) {
+        e = hipDeviceSynchronize();
+        hipError_t f = hipFree(seq->mem);
+        if (e == hipSuccess) e = f;
+    }
+    delete seq;
+    if (e != hipSuccess) return hip_fail(e, "mlq_hip_sequence_destroy");
+    return MLQ_OK;
+}
+
+int mlq_hip_graph_capture_sequence(mlq_sequence_t seq, void* stream, mlq_graph_t* out) {
+    if (out == nullptr) return fail(MLQ_ERR_INVALID, "mlq_hip_graph_capture_sequence: null output");
+    *out = nullptr;
+    if (seq == nullptr) return fail(MLQ_ERR_INVALID, "mlq_hip_graph_capture_sequence: null sequence");
+    int rc = ensure_device(seq->device);
+    if (rc != MLQ_OK) return rc;
+    hipStream_t s = resolve_stream(seq->device, stream);
+    MLQ_HIP_CHECK(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+    const int launch_rc = mlq_hip_sequence_launch(seq, s);
+    hipGraph_t graph = nullptr;
+    hipError_t end_err = hipStreamEndCapture(s, &graph);
+    if (launch_rc != MLQ_OK) {
+        if (graph) (void)hipGraphDestroy(graph);
+        return launch_rc;
+    }
+    if (end_err != hipSuccess) return hip_fail(end_err, "hipStreamEndCapture");
+    hipGraphExec_t exec = nullptr;
+    hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        (void)hipGraphDestroy(graph);
+        return hip_fail(e, "hipGraphInstantiate");
+    }
+    *out = new mlq_graph_s{graph, exec, seq->device};
     return MLQ_OK;
 }
 

@@ -45,6 +45,55 @@ hipError_t launch_gemm(const LinearShape& s, const void* w, const float* x, floa
                        size_t ws_bytes, hipStream_t stream);
 const char* gemm_kernel_name(const LinearShape& s);
 
+// Persistent GEMV over a chain of linears (sequence.hip).  A stage is up to
+// kSeqMaxCalls GEMVs reading the same x; their rows are concatenated in call
+// order (call j owns rows [row_begin, row_begin + M)).  Descriptors live in
+// device memory for as long as any launch that uses them.
+constexpr int kSeqMaxCalls = 4;
+
+struct SeqCallDesc {
+    const void* W;   // [M][nb] blocks
+    float* y;        // [M]
+    int M;
+    int row_begin;
+};
+
+struct SeqStageDesc {
+    const float* x;  // [K]
+    int K;
+    int nb;          // blocks per row (even)
+    int np;          // pairs per row
+    int nch;         // chunks per row: ceil(np / lane-group width)
+    int rows;        // sum of M over the stage's calls
+    int items;       // row items: ceil(rows / (64 / lane-group width))
+    int ncalls;
+    int barrier;     // 1: wait for every earlier stage of the launch first
+    SeqCallDesc call[kSeqMaxCalls];
+};
+
+// Barrier words of one launch (each on its own 128-byte line); zero before
+// the first launch and left at zero by every launch that completes.
+// Workgroup b arrives on sub[b % kSeqGroups]; the last arrival of a group
+// bumps `top`, which every workgroup polls.
+constexpr int kSeqGroups = 8;
+
+struct SeqSync {
+    unsigned sub[kSeqGroups][32];
+    unsigned top[32];
+    unsigned exit[32];
+    unsigned error[32];  // error[0] set when a barrier wait gave up (the launch's outputs are void)
+};
+
+bool sequence_supported(int qtype, int K);
+int sequence_lpr(int K);                 // lane-group width for rows of K elements: 16 or 64
+int sequence_stage_lds_bytes(int K);
+hipError_t sequence_grid(int qtype, int lpr, int lds_bytes, int device, int* grid);
+// coherent_x: stage x with agent-scope loads (needed when an earlier stage of
+// the same launch wrote it; plain cached loads otherwise).
+hipError_t launch_sequence(int qtype, int lpr, const SeqStageDesc* stages, int nstages, SeqSync* sync,
+                           int grid, int lds_bytes, unsigned spin_limit, bool coherent_x, hipStream_t stream);
+const char* sequence_kernel_name(int qtype, int lpr);
+
 // Device quantizer and synthetic-data generator.
 hipError_t launch_quantize(int qtype, const float* src, int rows, int row_len, void* dst,
                            hipStream_t stream);

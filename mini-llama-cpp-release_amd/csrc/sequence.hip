@@ -1,0 +1,349 @@
+// Persistent decode GEMV over a whole sequence of linears (one launch).
+//
+// A decode step issues a fixed chain of GEMVs (LLaMA: q, k, v -> o ->
+// gate, up -> down per layer, then lm_head).  Launched one kernel at a time,
+// every call pays the launch, the first-byte latency of its weights and the
+// drain of its last wave; at 4096x4096 Q4_0 (9.4 MB, ~1.5 us of HBM time)
+// those cost more than the transfer itself.  This kernel runs the chain in one
+// launch:
+//  * The chain is split into *stages*: up to kSeqMaxCalls GEMVs that read the
+//    same x (q, k, v or gate, up) and write disjoint outputs.  A stage's rows
+//    are concatenated and dealt to all waves of the grid (wave w takes row
+//    items w, w + GW, ...), so a fused q/k/v stage is one balanced pass.
+//  * Between stages a grid-wide barrier makes every output of the earlier
+//    stages visible before any wave stages the next x, so a call may consume
+//    any earlier call's y, exactly as with one launch per call in stream order.
+//  * Weights never depend on earlier outputs, so each wave requests the next
+//    chunk of W (one pair per lane) before computing the current one - also
+//    across the stage boundary: the next stage's first weights are in flight
+//    while the grid waits at the barrier and stages x.
+//  * Per row the arithmetic is that of the GEMV kernels in gemv.hip (same pair
+//    dot, same lane-group width and chunk order, same DPP reduction), so
+//    outputs are bit-identical to one launch per call.
+//
+// Barrier protocol (device memory, agent scope, no cache-maintenance fences):
+//  * outputs are written with agent-scope stores (write-through to the point
+//    of coherence) and the next stage reads x with agent-scope loads, so no L2
+//    writeback or invalidate is needed - those cost ~20-40 us per grid
+//    barrier on MI355X when every workgroup issues them;
+//  * arrival: each wave waits for its stores to complete, the workgroup
+//    synchronises, and thread 0 adds 1 to sub[b % 8]; the last arrival of a
+//    group adds 1 to `top` (a two-level tree: one hot address would serialise
+//    all arrivals, ~90 ns each);
+//  * the next stage's first weights are requested right after arriving, then
+//    thread 0 polls `top`; the poll is bounded by `spin_limit`: a workgroup
+//    that gives up sets `error` and stops waiting, so every wave always reaches
+//    the end of the kernel (the launch's outputs are then void and the host
+//    reports it);
+//  * the workgroups count themselves out through `exit`; the last one resets
+//    all counters, so the next launch starts from zero without a host reset.
+// All workgroups must be resident together: the host sizes the grid from the
+// occupancy of this kernel (at most two workgroups per CU).
+
+#include "gemv_device.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+
+namespace mlq {
+namespace {
+
+template <int QT, int LPR>
+__device__ __forceinline__ void seq_load_chunk(const SeqStageDesc& S, int it, int c, int slot, int pl,
+                                               uint32_t (&w)[Fmt<QT>::DW]) {
+    constexpr int DW = Fmt<QT>::DW;
+    constexpr int SUB = 64 / LPR;
+    // Rows / pairs past the end re-read the last one; their results are dropped.
+    const int row = min(it * SUB + slot, S.rows - 1);
+    const int p = min(c * LPR + pl, S.np - 1);
+    const void* W = S.call[0].W;
+    int rb = 0;
+#pragma unroll
+    for (int j = 1; j < kSeqMaxCalls; ++j) {
+        if (j < S.ncalls && row >= S.call[j].row_begin) {
+            W = S.call[j].W;
+            rb = S.call[j].row_begin;
+        }
+    }
+    const uint32_t* src = static_cast<const uint32_t*>(W) + static_cast<size_t>(row - rb) * (static_cast<size_t>(S.np) * DW) +
+                          static_cast<size_t>(p) * DW;
+#pragma unroll
+    for (int i = 0; i < DW; ++i) w[i] = src[i];
+}
+
+__device__ __forceinline__ void seq_store_row(const SeqStageDesc& S, int row, float v) {
+    float* y = S.call[0].y;
+    int rb = 0;
+#pragma unroll
+    for (int j = 1; j < kSeqMaxCalls; ++j) {
+        if (j < S.ncalls && row >= S.call[j].row_begin) {
+            y = S.call[j].y;
+            rb = S.call[j].row_begin;
+        }
+    }
+    __hip_atomic_store(y + (row - rb), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// First stage at or after `s` in which wave `gw` has a row item.
+__device__ __forceinline__ int seq_next_stage(const SeqStageDesc* __restrict__ st, int nstages, int s, int gw) {
+    while (s < nstages && gw >= st[s].items) ++s;
+    return s;
+}
+
+__device__ __forceinline__ unsigned seq_load(const unsigned* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ void seq_store(unsigned* p, unsigned v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ unsigned seq_groups() { return gridDim.x < kSeqGroups ? gridDim.x : kSeqGroups; }
+
+// Barrier number n (1-based within the launch), arrival half.
+__device__ __forceinline__ void seq_arrive(SeqSync* sync, unsigned n) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's y stores have completed
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const unsigned C = seq_groups();
+        const unsigned g = blockIdx.x % C;
+        const unsigned members = (gridDim.x - g + C - 1) / C;
+        const unsigned old = __hip_atomic_fetch_add(&sync->sub[g][0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (old == n * members - 1) {
+            __hip_atomic_fetch_add(&sync->top[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+}
+
+// Barrier number n, waiting half (thread 0 polls, then the workgroup syncs).
+__device__ __forceinline__ void seq_wait(SeqSync* sync, unsigned n, unsigned spin_limit, bool& gave_up) {
+    if (threadIdx.x == 0 && !gave_up) {
+        const unsigned target = n * seq_groups();
+        unsigned polls = 0;
+        while (seq_load(&sync->top[0]) < target) {
+            if (++polls > spin_limit) {
+                seq_store(&sync->error[0], 1u);
+                gave_up = true;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+    }
+    __syncthreads();
+}
+
+// Waves per SIMD the register budget is sized for: two workgroups per CU for
+// the 4-bit formats; Q8_0's 17-dword pairs fit one (same bytes in flight).
+template <int QT> struct SeqOcc { static constexpr int waves_per_simd = QT == 1 ? 2 : 4; };
+
+template <int QT, int LPR>
+__global__ __launch_bounds__(kWaves * 64, SeqOcc<QT>::waves_per_simd) void gemv_sequence_kernel(const SeqStageDesc* __restrict__ st,
+                                                                       int nstages, SeqSync* __restrict__ sync,
+                                                                       unsigned spin_limit, int coherent_x) {
+    constexpr int DW = Fmt<QT>::DW;
+    constexpr int SUB = 64 / LPR;
+    extern __shared__ float4 lds4[];
+    const int lane = threadIdx.x & 63;
+    const int slot = lane / LPR;
+    const int pl = lane % LPR;
+    const int gw = blockIdx.x * kWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int GW = gridDim.x * kWaves;
+    const NibConsts nk = NibConsts::make();
+    bool gave_up = false;
+
+    // Cursor of this wave: stage cs, row item cit, chunk cc (pairs cc*LPR + pl);
+    // wc holds that chunk's weights (or their request in flight).
+    int cs = seq_next_stage(st, nstages, 0, gw);
+    int cit = gw;
+    int cc = 0;
+    uint32_t wc[DW];
+    if (cs < nstages) seq_load_chunk<QT, LPR>(st[cs], cit, cc, slot, pl, wc);
+
+    unsigned barriers = 0;
+    for (int s = 0; s < nstages; ++s) {
+        const SeqStageDesc& S = st[s];
+        if (s > 0) {
+            if (S.barrier) {
+                seq_wait(sync, barriers, spin_limit, gave_up);
+            } else {
+                __syncthreads();  // LDS of the previous stage is no longer read
+            }
+        }
+        const int np = S.np;
+        float4* xs4 = lds4;
+        float2* cb = reinterpret_cast<float2*>(lds4 + np * 16);
+        if (coherent_x) {
+            stage_x<QT, true>(S.x, S.K, S.nb, xs4, cb);
+        } else {
+            stage_x<QT, false>(S.x, S.K, S.nb, xs4, cb);
+        }
+        __syncthreads();
+
+        bool pending = false;  // successor lies in a later stage, not yet requested
+        if (S.nch == 1) {
+            // Rows of one chunk: every item of the stage uses the same x pair.
+            const int pp = min(pl, np - 1);
+            float xv[64];
+            load_xv(xs4, pp, xv);
+            const float2 c0 = cb[2 * pp];
+            const float2 c1 = cb[2 * pp + 1];
+            const bool active = pl < np;
+            while (cs == s) {
+                int ns = cs;
+                int nit = cit + GW;
+                if (nit >= S.items) {
+                    ns = seq_next_stage(st, nstages, s + 1, gw);
+                    nit = gw;
+                }
+                uint32_t wn[DW];
+                const bool same_stage = ns == s;
+                if (same_stage) seq_load_chunk<QT, LPR>(S, nit, 0, slot, pl, wn);
+                float acc = active ? PairDot<QT>::run(wc, xv, c0, c1, 0.0f, nk) : 0.0f;
+                acc = group_sum<LPR>(acc);
+                const int row = cit * SUB + slot;
+                if (pl == LPR - 1 && row < S.rows) seq_store_row(S, row, acc);
+                if (same_stage) {
+#pragma unroll
+                    for (int i = 0; i < DW; ++i) wc[i] = wn[i];
+                } else {
+                    pending = ns < nstages;
+                }
+                cs = ns;
+                cit = nit;
+            }
+        } else {
+            float acc = 0.0f;
+            while (cs == s) {
+                int ns = cs;
+                int nit = cit;
+                int nc = cc + 1;
+                if (nc >= S.nch) {
+                    nc = 0;
+                    nit = cit + GW;
+                    if (nit >= S.items) {
+                        ns = seq_next_stage(st, nstages, s + 1, gw);
+                        nit = gw;
+                    }
+                }
+                uint32_t wn[DW];
+                const bool same_stage = ns == s;
+                if (same_stage) seq_load_chunk<QT, LPR>(S, nit, nc, slot, pl, wn);
+                const int p = cc * LPR + pl;
+                {
+                    const int pp = min(p, np - 1);
+                    float xv[64];
+                    load_xv(xs4, pp, xv);
+                    const float2 c0 = cb[2 * pp];
+                    const float2 c1 = cb[2 * pp + 1];
+                    if (p < np) acc = PairDot<QT>::run(wc, xv, c0, c1, acc, nk);
+                }
+                if (cc == S.nch - 1) {
+                    const float r = group_sum<LPR>(acc);
+                    acc = 0.0f;
+                    const int row = cit * SUB + slot;
+                    if (pl == LPR - 1 && row < S.rows) seq_store_row(S, row, r);
+                }
+                if (same_stage) {
+#pragma unroll
+                    for (int i = 0; i < DW; ++i) wc[i] = wn[i];
+                } else {
+                    pending = ns < nstages;
+                }
+                cs = ns;
+                cit = nit;
+                cc = nc;
+            }
+        }
+        // Arrive before requesting the next stage's weights, so the arrival
+        // does not wait for them.
+        if (s + 1 < nstages && st[s + 1].barrier) seq_arrive(sync, ++barriers);
+        if (pending) seq_load_chunk<QT, LPR>(st[cs], cit, cc, slot, pl, wc);
+    }
+
+    // Count out; the last workgroup resets the counters for the next launch.
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const unsigned done = __hip_atomic_fetch_add(&sync->exit[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (done == gridDim.x - 1) {
+            for (int g = 0; g < kSeqGroups; ++g) seq_store(&sync->sub[g][0], 0u);
+            seq_store(&sync->top[0], 0u);
+            seq_store(&sync->exit[0], 0u);
+        }
+    }
+}
+
+template <int QT, int LPR>
+const void* seq_kernel_ptr() {
+    return reinterpret_cast<const void*>(&gemv_sequence_kernel<QT, LPR>);
+}
+
+const void* seq_kernel(int qtype, int lpr) {
+    switch (qtype * 100 + lpr) {
+        case 116: return seq_kernel_ptr<1, 16>();
+        case 132: return seq_kernel_ptr<1, 32>();
+        case 164: return seq_kernel_ptr<1, 64>();
+        case 216: return seq_kernel_ptr<2, 16>();
+        case 232: return seq_kernel_ptr<2, 32>();
+        case 264: return seq_kernel_ptr<2, 64>();
+        case 316: return seq_kernel_ptr<3, 16>();
+        case 332: return seq_kernel_ptr<3, 32>();
+        case 364: return seq_kernel_ptr<3, 64>();
+        default: return nullptr;
+    }
+}
+
+}  // namespace
+
+bool sequence_supported(int qtype, int K) {
+    const int nb = (K + kQK - 1) / kQK;
+    return (qtype >= 1 && qtype <= 3) && nb % 2 == 0 && pair_lds_bytes(nb) <= kMaxPairLdsBytes;
+}
+
+int sequence_lpr(int K) {
+    // The lane-group width gemv.hip picks for a single launch of this shape,
+    // so a row is summed in the same order either way.
+    const int np = (K + kQK - 1) / kQK / 2;
+    if (np <= 16) return 16;
+    if (np <= 64) return 64;
+    for (int lpr : {64, 32, 16}) {
+        const int iters = (np + lpr - 1) / lpr;
+        if (static_cast<double>(np) / (static_cast<double>(lpr) * iters) >= 0.875) return lpr;
+    }
+    return 16;
+}
+
+int sequence_stage_lds_bytes(int K) { return pair_lds_bytes((K + kQK - 1) / kQK); }
+
+hipError_t sequence_grid(int qtype, int lpr, int lds_bytes, int device, int* grid) {
+    const void* k = seq_kernel(qtype, lpr);
+    if (k == nullptr) return hipErrorInvalidValue;
+    int per_cu = 0;
+    hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, kWaves * 64, lds_bytes);
+    if (e != hipSuccess) return e;
+    int cus = 0;
+    e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
+    if (e != hipSuccess) return e;
+    if (per_cu < 1 || cus < 1) return hipErrorInvalidConfiguration;
+    *grid = cus * (per_cu < 2 ? per_cu : 2);
+    return hipSuccess;
+}
+
+hipError_t launch_sequence(int qtype, int lpr, const SeqStageDesc* stages, int nstages, SeqSync* sync,
+                           int grid, int lds_bytes, unsigned spin_limit, bool coherent_x, hipStream_t stream) {
+    const void* k = seq_kernel(qtype, lpr);
+    if (k == nullptr || nstages <= 0 || grid <= 0) return hipErrorInvalidValue;
+    int coh = coherent_x ? 1 : 0;
+    void* args[] = {&stages, &nstages, &sync, &spin_limit, &coh};
+    return hipLaunchKernel(k, dim3(grid), dim3(kWaves * 64), args, static_cast<size_t>(lds_bytes), stream);
+}
+
+const char* sequence_kernel_name(int qtype, int lpr) {
+    static thread_local char buf[64];
+    const char* fmt = qtype == 1 ? "q8_0" : qtype == 2 ? "q4_0" : "q4_1";
+    snprintf(buf, sizeof buf, "gemv_sequence_%s_lpr%d", fmt, lpr);
+    return buf;
+}
+
+}  // namespace mlq

@@ -23,6 +23,7 @@ F32, Q8_0, Q4_0, Q4_1 = 0, 1, 2, 3
 BLOCK_BYTES = {Q8_0: 34, Q4_0: 18, Q4_1: 20}
 QK = 32
 X_ON_DEVICE, Y_ON_DEVICE, ASYNC = 1, 2, 4
+SEQ_PERSISTENT, SEQ_PER_STAGE, SEQ_INDEPENDENT = 0, 1, 2
 
 _vp = ctypes.c_void_p
 
@@ -75,6 +76,15 @@ _SIGS = {
                                                    ctypes.POINTER(_vp)]),
     "mlq_hip_graph_launch": (ctypes.c_int, [_vp, _vp]),
     "mlq_hip_graph_destroy": (ctypes.c_int, [_vp]),
+    "mlq_hip_sequence_create": (ctypes.c_int, [ctypes.POINTER(LinearCall), ctypes.c_int,
+                                                ctypes.POINTER(ctypes.c_int), ctypes.c_int, ctypes.POINTER(_vp)]),
+    "mlq_hip_sequence_launch": (ctypes.c_int, [_vp, _vp]),
+    "mlq_hip_sequence_status": (ctypes.c_int, [_vp, ctypes.POINTER(ctypes.c_int)]),
+    "mlq_hip_sequence_set_spin_limit": (ctypes.c_int, [_vp, ctypes.c_uint]),
+    "mlq_hip_sequence_info": (ctypes.c_int, [_vp, ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int),
+                                              ctypes.POINTER(ctypes.c_int)]),
+    "mlq_hip_sequence_destroy": (ctypes.c_int, [_vp]),
+    "mlq_hip_graph_capture_sequence": (ctypes.c_int, [_vp, _vp, ctypes.POINTER(_vp)]),
     "mlq_hip_fill_normal": (ctypes.c_int, [_vp, ctypes.c_size_t, ctypes.c_uint64, ctypes.c_float,
                                             ctypes.c_float, _vp]),
     "mlq_hip_kernel_name": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
@@ -263,12 +273,63 @@ def linear_many(arr: ctypes.Array, stream=None) -> None:
     _check(load().mlq_hip_quant_linear_many(arr, len(arr), stream))
 
 
-class Graph:
-    def __init__(self, arr: ctypes.Array, stream=None):
+class Sequence:
+    """A chain of GEMV calls run as persistent launches (mlq_hip_sequence_*).
+
+    ``stages`` gives one stage id per call (consecutive equal ids form a stage of
+    calls that share x); None puts every call in a stage of its own."""
+
+    def __init__(self, arr: ctypes.Array, stages=None, mode: int = SEQ_PERSISTENT):
         h = _vp()
-        _check(load().mlq_hip_graph_capture_many(arr, len(arr), stream, ctypes.byref(h)))
+        ids = None
+        if stages is not None:
+            assert len(stages) == len(arr), "one stage id per call"
+            ids = (ctypes.c_int * len(stages))(*stages)
+        _check(load().mlq_hip_sequence_create(arr, len(arr), ids, mode, ctypes.byref(h)))
+        self.h = h.value
+        self._keep = (arr, ids)
+
+    def launch(self, stream=None) -> None:
+        _check(_LIB.mlq_hip_sequence_launch(self.h, stream))
+
+    def status(self) -> int:
+        n = ctypes.c_int(0)
+        _check(_LIB.mlq_hip_sequence_status(self.h, ctypes.byref(n)))
+        return n.value
+
+    def set_spin_limit(self, polls: int) -> None:
+        _check(_LIB.mlq_hip_sequence_set_spin_limit(self.h, polls))
+
+    def info(self) -> dict:
+        st, ln, gr = ctypes.c_int(0), ctypes.c_int(0), ctypes.c_int(0)
+        _check(_LIB.mlq_hip_sequence_info(self.h, ctypes.byref(st), ctypes.byref(ln), ctypes.byref(gr)))
+        return {"stages": st.value, "launches": ln.value, "grid": gr.value}
+
+    def destroy(self) -> None:
+        if getattr(self, "h", None):
+            _LIB.mlq_hip_sequence_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.destroy()
+        except Exception:
+            pass
+
+
+class Graph:
+    """A captured and instantiated graph of ``linear_many(arr)`` or of one
+    sequence launch (``Graph(sequence=seq)``; the sequence must outlive it)."""
+
+    def __init__(self, arr: ctypes.Array | None = None, stream=None, sequence: "Sequence | None" = None):
+        h = _vp()
+        if sequence is not None:
+            _check(load().mlq_hip_graph_capture_sequence(sequence.h, stream, ctypes.byref(h)))
+        else:
+            _check(load().mlq_hip_graph_capture_many(arr, len(arr), stream, ctypes.byref(h)))
         self.h = h.value
         self._arr = arr
+        self._seq = sequence
 
     def launch(self, stream=None) -> None:
         _check(_LIB.mlq_hip_graph_launch(self.h, stream))

@@ -1,0 +1,257 @@
+"""GPU tests of the persistent GEMV sequence (mlq_hip_sequence_*).
+
+A sequence runs a chain of GEMVs in one launch with device-wide barriers
+between stages.  Per call its outputs must equal one mlq_hip_quant_linear
+launch per call bit for bit (same lane-group width, same summation order), in
+all three modes, for chained calls whose x is an earlier call's y (what the
+barriers are for), for fused stages (q/k/v, gate/up) and across graph replays
+with eager work in between.  One chain is also checked against the CPU oracle
+to the parity bound, and the host-side validation and the bounded barrier wait
+are exercised.
+"""
+
+import sys
+
+import numpy as np
+import pytest
+
+import oracle
+from tolerance import check_close
+
+pytestmark = pytest.mark.gpu
+
+FMTS = {"q8_0": oracle.Q8_0, "q4_0": oracle.Q4_0, "q4_1": oracle.Q4_1}
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+class Lin:
+    """A device weight N(0, 0.02) quantized on the device, plus its blocks."""
+
+    def __init__(self, hip, qt, m, k, seed):
+        self.qt, self.m, self.k = qt, m, k
+        nb = (k + 31) // 32
+        f = hip.DeviceBuffer(4 * m * k)
+        hip.fill_normal(f, m * k, seed, 0.0, 0.02)
+        self.buf = hip.DeviceBuffer(m * nb * hip.BLOCK_BYTES[qt])
+        hip.quantize_device(qt, f, m, k, self.buf)
+        f.free()
+        self.w = hip.Weight.wrap(qt, self.buf, m * nb, m, k)
+
+    def blocks(self):
+        bb = {oracle.Q8_0: 34, oracle.Q4_0: 18, oracle.Q4_1: 20}[self.qt]
+        return self.buf.download(np.uint8).reshape(-1, bb)
+
+
+def vec(hip, n, seed):
+    b = hip.DeviceBuffer(4 * n)
+    hip.fill_normal(b, n, seed, 0.0, 1.0)
+    return b
+
+
+def per_call(hip, calls):
+    """Reference: one launch per call, in order, on the library stream."""
+    for w, x, y in calls:
+        w.w.linear_device(x, y)
+
+
+def snapshot(bufs):
+    return [b.download(np.float32) for b in bufs]
+
+
+def llama_layer(hip, qt, seed, hidden=4096, ffn=11008):
+    """q,k,v | o | gate,up | down with the real data flow: o reads v's output
+    (a stand-in for attention), down reads up's output (for silu(gate)*up)."""
+    lq, lk, lv = (Lin(hip, qt, hidden, hidden, seed + i) for i in range(3))
+    lo = Lin(hip, qt, hidden, hidden, seed + 3)
+    lg, lu = Lin(hip, qt, ffn, hidden, seed + 4), Lin(hip, qt, ffn, hidden, seed + 5)
+    ld = Lin(hip, qt, hidden, ffn, seed + 6)
+    x = vec(hip, hidden, seed + 100)
+    yq, yk, yv, yo = (hip.DeviceBuffer(4 * hidden) for _ in range(4))
+    yg, yu = hip.DeviceBuffer(4 * ffn), hip.DeviceBuffer(4 * ffn)
+    yd = hip.DeviceBuffer(4 * hidden)
+    calls = [(lq, x, yq), (lk, x, yk), (lv, x, yv), (lo, yv, yo), (lg, yo, yg), (lu, yo, yu), (ld, yu, yd)]
+    stages = [0, 0, 0, 1, 2, 2, 3]
+    keep = [lq, lk, lv, lo, lg, lu, ld, x]
+    return calls, stages, [yq, yk, yv, yo, yg, yu, yd], keep
+
+
+def run_sequence(hip, calls, stages, mode):
+    arr = hip.make_calls([(w.w, x, y, 1) for w, x, y in calls])
+    seq = hip.Sequence(arr, stages, mode)
+    seq.launch()
+    hip.synchronize()
+    assert seq.status() == 0, "a barrier wait timed out"
+    return seq
+
+
+@pytest.mark.parametrize("fmt", list(FMTS))
+def test_chain_matches_per_call_launches(hip, fmt):
+    qt = FMTS[fmt]
+    calls, stages, outs, keep = llama_layer(hip, qt, seed=11)
+    say(f"sequence chain {fmt}: per-call reference")
+    per_call(hip, calls)
+    want = snapshot(outs)
+    for b in outs:
+        b.fill(0)
+    for mode in (hip.SEQ_PERSISTENT, hip.SEQ_PER_STAGE):
+        say(f"sequence chain {fmt} mode={mode}")
+        seq = run_sequence(hip, calls, stages, mode)
+        got = snapshot(outs)
+        for i, (g, w) in enumerate(zip(got, want)):
+            assert np.array_equal(g.view(np.uint32), w.view(np.uint32)), f"{fmt} mode {mode} call {i} differs"
+        info = seq.info()
+        assert info["stages"] == 4
+        seq.destroy()
+        for b in outs:
+            b.fill(0)
+
+
+def test_chain_against_oracle(hip, orc):
+    """A dependent Q4_0 chain 4096 -> 11008 -> 4096 checked call by call against
+    the CPU oracle on the inputs each call actually saw."""
+    qt = oracle.Q4_0
+    l1, l2, l3 = Lin(hip, qt, 11008, 4096, 5), Lin(hip, qt, 4096, 11008, 6), Lin(hip, qt, 4096, 4096, 7)
+    x = vec(hip, 4096, 8)
+    y1, y2, y3 = hip.DeviceBuffer(4 * 11008), hip.DeviceBuffer(4 * 4096), hip.DeviceBuffer(4 * 4096)
+    calls = [(l1, x, y1), (l2, y1, y2), (l3, y2, y3)]
+    say("sequence chain vs oracle")
+    run_sequence(hip, calls, None, hip.SEQ_PERSISTENT)
+    ins = [x.download(np.float32), y1.download(np.float32), y2.download(np.float32)]
+    for (lin, _, yb), xin in zip(calls, ins):
+        blocks = lin.blocks()
+        want = orc.linear(qt, xin, blocks, lin.m, threads=16)
+        check_close(yb.download(np.float32), want, xin, qt, blocks, f"chain {lin.m}x{lin.k}")
+
+
+@pytest.mark.parametrize("shape", [(896, 896), (128, 896), (4864, 896), (896, 4864), (300, 2048),
+                                   (37, 64), (1000, 3072), (77, 15360)],
+                         ids=lambda s: f"{s[0]}x{s[1]}")
+def test_independent_shapes_all_modes(hip, shape):
+    """Every lane-group width (16 / 32 / 64), ragged row counts, a 4-call stage
+    and the largest supported K, in all three modes, against per-call launches."""
+    m, k = shape
+    for fmt, qt in FMTS.items():
+        lins = [Lin(hip, qt, m + 3 * i, k, 40 + i) for i in range(4)]
+        x = vec(hip, k, 99)
+        outs = [hip.DeviceBuffer(4 * (m + 3 * i)) for i in range(4)]
+        calls = [(lins[i], x, outs[i]) for i in range(4)]
+        per_call(hip, calls)
+        want = snapshot(outs)
+        for mode in (hip.SEQ_PERSISTENT, hip.SEQ_PER_STAGE, hip.SEQ_INDEPENDENT):
+            for stages in ([0, 0, 0, 0], [0, 1, 1, 2], None):
+                for b in outs:
+                    b.fill(0)
+                say(f"sequence {fmt} {m}x{k} mode={mode} stages={stages}")
+                run_sequence(hip, calls, stages, mode)
+                for i, (g, w) in enumerate(zip(snapshot(outs), want)):
+                    assert np.array_equal(g.view(np.uint32), w.view(np.uint32)), \
+                        f"{fmt} {m}x{k} mode {mode} stages {stages} call {i}"
+
+
+def test_mixed_formats_split_launches(hip):
+    """Formats and widths change along the chain: one launch per run, same bits."""
+    a = Lin(hip, oracle.Q8_0, 896, 4096, 1)
+    b = Lin(hip, oracle.Q4_0, 4096, 896, 2)
+    c = Lin(hip, oracle.Q4_1, 4096, 4096, 3)
+    d = Lin(hip, oracle.Q4_0, 4096, 4096, 4)
+    x = vec(hip, 4096, 5)
+    ya, yb, yc, yd = (hip.DeviceBuffer(4 * n) for n in (896, 4096, 4096, 4096))
+    calls = [(a, x, ya), (b, ya, yb), (c, yb, yc), (d, yc, yd)]
+    per_call(hip, calls)
+    want = snapshot([ya, yb, yc, yd])
+    for buf in (ya, yb, yc, yd):
+        buf.fill(0)
+    seq = run_sequence(hip, calls, None, hip.SEQ_PERSISTENT)
+    assert seq.info()["launches"] == 4
+    for i, (g, w) in enumerate(zip(snapshot([ya, yb, yc, yd]), want)):
+        assert np.array_equal(g.view(np.uint32), w.view(np.uint32)), f"call {i}"
+
+
+def test_graph_replays(hip):
+    """A captured sequence replayed with new x contents and eager work between
+    replays: every replay equals per-call launches on the same x."""
+    calls, stages, outs, keep = llama_layer(hip, oracle.Q4_0, seed=21)
+    x = keep[-1]
+    arr = hip.make_calls([(w.w, xx, y, 1) for w, xx, y in calls])
+    seq = hip.Sequence(arr, stages, hip.SEQ_PERSISTENT)
+    g = hip.Graph(sequence=seq)
+    scratch = hip.DeviceBuffer(4 * 4096)
+    for rep in range(4):
+        hip.fill_normal(x, 4096, 500 + rep, 0.0, 1.0)
+        hip.synchronize()
+        say(f"sequence graph replay {rep}")
+        g.launch()
+        hip.synchronize()
+        assert seq.status() == 0
+        got = snapshot(outs)
+        hip.fill_normal(scratch, 4096, 9, 0.0, 1.0)  # eager work between replays
+        per_call(hip, calls)
+        want = snapshot(outs)
+        for i, (a, b) in enumerate(zip(got, want)):
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"replay {rep} call {i}"
+    g.destroy()
+    seq.destroy()
+
+
+def test_validation_messages(hip):
+    l1 = Lin(hip, oracle.Q4_0, 64, 128, 1)
+    l2 = Lin(hip, oracle.Q4_0, 64, 256, 2)
+    odd = Lin(hip, oracle.Q4_0, 64, 96, 3)  # 3 blocks per row
+    l64 = Lin(hip, oracle.Q4_0, 64, 64, 5)
+    x = vec(hip, 256, 4)
+    y = hip.DeviceBuffer(4 * 64)
+    y2 = hip.DeviceBuffer(4 * 64)
+
+    def create(calls, stages=None, mode=hip.SEQ_PERSISTENT):
+        return hip.Sequence(hip.make_calls(calls), stages, mode)
+
+    with pytest.raises(hip.MlqError, match="a sequence runs GEMV calls"):
+        create([(l1.w, x, y, 2)])
+    with pytest.raises(hip.MlqError, match="even block count"):
+        create([(odd.w, x, y, 1)])
+    with pytest.raises(hip.MlqError, match="differs from call 0 of its stage"):
+        create([(l1.w, x, y, 1), (l2.w, x, y2, 1)], [0, 0])
+    with pytest.raises(hip.MlqError, match="of one stage overlap"):
+        create([(l1.w, x, y, 1), (l1.w, x, y, 1)], [0, 0])
+    with pytest.raises(hip.MlqError, match="overlaps its stage's input"):
+        create([(l1.w, x, x, 1)])
+    with pytest.raises(hip.MlqError, match="overlaps the weight of call"):
+        create([(l1.w, x, l1.buf.ptr, 1)])
+    with pytest.raises(hip.MlqError, match="MLQ_SEQ_INDEPENDENT needs independent calls"):
+        create([(l1.w, x, y, 1), (l64.w, y, y2, 1)], None, hip.SEQ_INDEPENDENT)
+    with pytest.raises(hip.MlqError, match="at most 4"):
+        ys = [hip.DeviceBuffer(4 * 64) for _ in range(5)]
+        create([(l1.w, x, ys[i], 1) for i in range(5)], [0] * 5)
+    with pytest.raises(hip.MlqError, match="unknown mode"):
+        create([(l1.w, x, y, 1)], None, 7)
+    # a dependent chain is fine in the barrier modes
+    create([(l1.w, x, y, 1), (l64.w, y, y2, 1)]).destroy()
+
+
+def test_barrier_wait_bound_recovers(hip):
+    """With a one-poll bound the barrier waits give up instead of spinning; the
+    launch still ends, the status reports it, and the next launch with the
+    default bound is correct again (the barrier words reset themselves)."""
+    calls, stages, outs, keep = llama_layer(hip, oracle.Q4_0, seed=31)
+    per_call(hip, calls)
+    want = snapshot(outs)
+    arr = hip.make_calls([(w.w, x, y, 1) for w, x, y in calls])
+    seq = hip.Sequence(arr, stages, hip.SEQ_PERSISTENT)
+    seq.set_spin_limit(1)
+    say("sequence with a one-poll barrier bound")
+    seq.launch()
+    hip.synchronize()
+    timeouts = seq.status()
+    say(f"  timeouts reported: {timeouts}")
+    assert timeouts in (0, 1)
+    assert seq.status() == 0, "status must clear"
+    seq.set_spin_limit(1 << 20)
+    seq.launch()
+    hip.synchronize()
+    assert seq.status() == 0
+    for i, (g, w) in enumerate(zip(snapshot(outs), want)):
+        assert np.array_equal(g.view(np.uint32), w.view(np.uint32)), f"call {i} after recovery"
