@@ -8,6 +8,16 @@ fresh x ~ N(0, 1) per layer (x for q..up, h for down), all generated on the
 device before timing.  `value` is algorithmic bytes (weight blocks + 4K + 4M
 per call) per second over the timed steps.
 
+Headline launch mode (`--launch per_stage`): the decode step's data flow, in
+stream order -- per layer the q/k/v calls (same x) as one fused launch, then
+o, then gate/up (same x) fused, then down; 129 launches per step captured as
+one graph.  Every launch may depend on the previous one, as in a real decode
+step.  The other modes are timed too and reported in config.sweep_us_by_launch:
+one launch per call (graph / plain), the persistent sequence kernel with grid
+barriers between the same 129 stages (sequence), and the persistent kernel
+without barriers (independent: valid only because this sweep's inputs are all
+fresh; not a decode step).
+
 Also reported (not the headline value):
   * gemv[]: per-shape GEMV time / GB/s for BASELINE configs 1-3, each cycling
     max(32, ceil(1 GB / W bytes)) distinct weight copies so the 256 MB MALL
@@ -19,7 +29,8 @@ Also reported (not the headline value):
     compiled from the reference sources; the restated oracle if absent) over
     the whole sweep on all host cores.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--launch graph|plain]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+                       [--launch per_stage|graph|plain|sequence|independent]
 """
 
 from __future__ import annotations
@@ -48,13 +59,22 @@ FMT_NAME = {hip.Q8_0: "q8_0", hip.Q4_0: "q4_0", hip.Q4_1: "q4_1"}
 
 TRAFFIC_PROFILE = os.path.join(REPO, "profiles", "gemv_q4_0_llama7b_sweep_hbm_traffic.md")
 
+KERNEL_BY_LAUNCH = {
+    "graph": "Q4_0 GEMV family (gemv_single / gemv_multi), one launch per call",
+    "plain": "Q4_0 GEMV family (gemv_single / gemv_multi), one launch per call",
+    "per_stage": "Q4_0 GEMV family (gemv_single / gemv_multi), one fused launch per stage (q,k,v | o | gate,up | down)",
+    "sequence": "gemv_sequence (persistent, grid barriers between stages)",
+    "independent": "gemv_sequence (persistent, no barriers)",
+}
 
-def measured_traffic():
-    """HBM bytes per launch of the sweep from the committed rocprofv3 FETCH_SIZE /
-    WRITE_SIZE summary (calibrated against a copy of known size), or None."""
+
+def measured_traffic(launch):
+    """HBM bytes per launch of the sweep in this launch mode from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (calibrated against a copy of
+    known size), or None when that mode has not been profiled."""
     try:
         for line in open(TRAFFIC_PROFILE):
-            if line.startswith("traffic_bytes_per_launch:"):
+            if line.startswith(f"traffic_bytes_per_launch[{launch}]:"):
                 return int(line.split(":", 1)[1])
     except OSError:
         pass
@@ -276,7 +296,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--launch", choices=["graph", "plain", "sequence", "per_stage", "independent"],
-                    default="sequence")
+                    default="per_stage")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline / parity leg")
     ap.add_argument("--no-shapes", action="store_true", help="skip the per-shape GEMV / GEMM tables")
     ap.add_argument("--layers", type=int, default=32)
@@ -349,6 +369,8 @@ def main():
     ms_step = ms / args.steps
     gbs = sw.bytes / (ms_step * 1e-3) / 1e9
     seq_info = seqs["sequence"].info()
+    launches = {"graph": sw.n(), "plain": sw.n(), "per_stage": seqs["per_stage"].info()["launches"],
+                "sequence": seq_info["launches"], "independent": seqs["independent"].info()["launches"]}[args.launch]
     log(f"sweep: {ms_step * 1e3:.1f} us/step, {gbs:.1f} GB/s ({args.launch}); sequence {seq_info}")
 
     shapes = []
@@ -407,10 +429,11 @@ def main():
                    "sweep_us": round(ms_step * 1e3, 1),
                    "sweep_us_by_launch": {k: round(v * 1e3, 1) for k, v in variants.items()}},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
-                     "algorithmic_bytes_per_launch": round(sw.bytes / sw.n()),
-                     "avg_launch_us": round(ms_step * 1e3 / sw.n(), 3),
-                     "kernel": "Q4_0 GEMV family (gemv_single / gemv_multi), all launches of the step"},
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(args.launch),
+                     "algorithmic_bytes_per_launch": round(sw.bytes / launches),
+                     "launches_per_step": launches,
+                     "avg_launch_us": round(ms_step * 1e3 / launches, 3),
+                     "kernel": KERNEL_BY_LAUNCH[args.launch]},
         "cpu_baseline": cpu,
         "parity": parity,
         "gemv": shapes,

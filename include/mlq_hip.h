@@ -125,6 +125,14 @@ typedef struct mlq_linear_call {
 } mlq_linear_call;
 int mlq_hip_quant_linear_many(const mlq_linear_call* calls, int n, void* stream);
 
+/* Up to 4 GEMVs (rows == 1) that read the same x, in one launch: the fused
+ * q/k/v or gate/up projection of a decode step.  Same x, in_features and
+ * quant type for every call; outputs disjoint from each other and from x.
+ * Per call the result equals mlq_hip_quant_linear bit for bit.  No
+ * counterpart in the reference (its forward issues one linear per projection,
+ * src/forward.cpp:172-227).  Asynchronous on `stream`. */
+int mlq_hip_quant_linear_fused(const mlq_linear_call* calls, int n, void* stream);
+
 /* Quantize an f32 [rows, row_len] matrix that is already on `device` into
  * blocks on the same device, bit-identical to the reference quantizers:
  * quantize_to_q8_0 / quantize_to_q4_0 (src/quant.cpp:112-170, 207-270) and

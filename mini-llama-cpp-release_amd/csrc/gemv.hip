@@ -56,23 +56,64 @@
 namespace mlq {
 namespace {
 
+// Call of a group that owns launch row `row` (calls are in row order).
+__device__ __forceinline__ int group_call(const GemvGroup& g, int row) {
+    int k = 0;
+#pragma unroll
+    for (int j = 1; j < kGroupMaxCalls; ++j) k = (j < g.ncalls && row >= g.row_begin[j]) ? j : k;
+    return k;
+}
+
+__device__ __forceinline__ const uint32_t* group_row(const GemvGroup& g, int row, size_t row_dw) {
+    const void* w = g.W[0];
+    int rb = 0;
+#pragma unroll
+    for (int j = 1; j < kGroupMaxCalls; ++j) {
+        if (j < g.ncalls && row >= g.row_begin[j]) {
+            w = g.W[j];
+            rb = g.row_begin[j];
+        }
+    }
+    return static_cast<const uint32_t*>(w) + static_cast<size_t>(row - rb) * row_dw;
+}
+
+// y of launch row `row` for batch row `b` (each call's y is [rows][M_j]).
+__device__ __forceinline__ float* group_y(const GemvGroup& g, int row, int M, int b) {
+    float* y = g.y[0];
+    int rb = 0;
+    int re = g.ncalls > 1 ? g.row_begin[1] : M;
+#pragma unroll
+    for (int j = 1; j < kGroupMaxCalls; ++j) {
+        if (j < g.ncalls && row >= g.row_begin[j]) {
+            y = g.y[j];
+            rb = g.row_begin[j];
+            re = j + 1 < g.ncalls ? g.row_begin[j + 1] : M;
+        }
+    }
+    return y + static_cast<size_t>(b) * (re - rb) + (row - rb);
+}
+
 template <int R, int DW>
-__device__ __forceinline__ void load_rows(const uint32_t* __restrict__ W, size_t row_dw, int row0, int M,
-                                          int p, uint32_t (&w)[R][DW]) {
+__device__ __forceinline__ void load_rows(const GemvGroup& g, size_t row_dw, int row0, int M, int p,
+                                          uint32_t (&w)[R][DW]) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const int row = min(row0 + r, M - 1);  // rows past M compute on row M-1 and are dropped
-        const uint32_t* src = W + static_cast<size_t>(row) * row_dw + static_cast<size_t>(p) * DW;
+        const uint32_t* src = group_row(g, row, row_dw) + static_cast<size_t>(p) * DW;
 #pragma unroll
         for (int i = 0; i < DW; ++i) w[r][i] = src[i];
     }
 }
 
+// Waves per SIMD the single kernel's registers are bounded for: four (two
+// workgroups per CU) except Q8_0 with two rows per slot, whose 2 x 17 pair
+// dwords in flight do not fit 128 VGPRs without spilling.
+template <int QT, int R> struct SingleOcc { static constexpr int waves_per_simd = (QT == 1 && R == 2) ? 2 : 4; };
+
 // Rows of at most LPR pairs: x in VGPRs, persistent over row groups.
 template <int QT, int LPR, int R, int WAVES>
-__global__ __launch_bounds__(WAVES * 64) void gemv_single_kernel(
-    const uint8_t* __restrict__ Wb, const float* __restrict__ x, float* __restrict__ y, int M, int K,
-    int nb, int groups) {
+__global__ __launch_bounds__(WAVES * 64, (SingleOcc<QT, R>::waves_per_simd)) void gemv_single_kernel(
+    const GemvGroup g, const float* __restrict__ x, int M, int K, int nb, int groups) {
     constexpr int DW = Fmt<QT>::DW;
     constexpr int SUB = 64 / LPR;
     extern __shared__ float4 lds4[];
@@ -80,8 +121,6 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_single_kernel(
     float4* xs4 = lds4;
     float2* cb = reinterpret_cast<float2*>(lds4 + np * 16);
     x += static_cast<size_t>(blockIdx.y) * K;
-    y += static_cast<size_t>(blockIdx.y) * M;
-    const uint32_t* W = reinterpret_cast<const uint32_t*>(Wb);
 
     const int lane = threadIdx.x & 63;
     const int slot = lane / LPR;
@@ -90,10 +129,10 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_single_kernel(
     const int p = active ? pl : 0;
     const size_t row_dw = static_cast<size_t>(np) * DW;
     const int gstride = gridDim.x * WAVES;
-    int gi = blockIdx.x * WAVES + (threadIdx.x >> 6);
+    int gi = blockIdx.x * WAVES + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 
     uint32_t wc[R][DW];
-    if (gi < groups) load_rows<R, DW>(W, row_dw, gi * (SUB * R) + slot * R, M, p, wc);
+    if (gi < groups) load_rows<R, DW>(g, row_dw, gi * (SUB * R) + slot * R, M, p, wc);
     stage_x<QT>(x, K, nb, xs4, cb);
     __syncthreads();
     float xv[64];
@@ -105,7 +144,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_single_kernel(
     for (; gi < groups; gi += gstride) {
         uint32_t wn[R][DW];
         const int gn = gi + gstride;
-        if (gn < groups) load_rows<R, DW>(W, row_dw, gn * (SUB * R) + slot * R, M, p, wn);
+        if (gn < groups) load_rows<R, DW>(g, row_dw, gn * (SUB * R) + slot * R, M, p, wn);
         float acc[R];
 #pragma unroll
         for (int r = 0; r < R; ++r) {
@@ -116,7 +155,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_single_kernel(
             const int row0 = gi * (SUB * R) + slot * R;
 #pragma unroll
             for (int r = 0; r < R; ++r) {
-                if (row0 + r < M) y[row0 + r] = acc[r];
+                if (row0 + r < M) *group_y(g, row0 + r, M, blockIdx.y) = acc[r];
             }
         }
 #pragma unroll
@@ -129,8 +168,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_single_kernel(
 // Rows of more than LPR pairs: one row group per wave, x from LDS per pair.
 template <int QT, int LPR, int R, int WAVES>
 __global__ __launch_bounds__(WAVES * 64) void gemv_multi_kernel(
-    const uint8_t* __restrict__ Wb, const float* __restrict__ x, float* __restrict__ y, int M, int K,
-    int nb) {
+    const GemvGroup g, const float* __restrict__ x, int M, int K, int nb) {
     constexpr int DW = Fmt<QT>::DW;
     constexpr int SUB = 64 / LPR;
     extern __shared__ float4 lds4[];
@@ -138,17 +176,15 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_multi_kernel(
     float4* xs4 = lds4;
     float2* cb = reinterpret_cast<float2*>(lds4 + np * 16);
     x += static_cast<size_t>(blockIdx.y) * K;
-    y += static_cast<size_t>(blockIdx.y) * M;
-    const uint32_t* W = reinterpret_cast<const uint32_t*>(Wb);
 
     const int lane = threadIdx.x & 63;
     const int slot = lane / LPR;
     const int pl = lane % LPR;
-    const int row0 = (blockIdx.x * WAVES + (threadIdx.x >> 6)) * (SUB * R) + slot * R;
+    const int row0 = (blockIdx.x * WAVES + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) * (SUB * R) + slot * R;
     const size_t row_dw = static_cast<size_t>(np) * DW;
 
     uint32_t wc[R][DW];
-    if (pl < np) load_rows<R, DW>(W, row_dw, row0, M, pl, wc);
+    if (pl < np) load_rows<R, DW>(g, row_dw, row0, M, pl, wc);
     stage_x<QT>(x, K, nb, xs4, cb);
     __syncthreads();
     const NibConsts nk = NibConsts::make();
@@ -157,7 +193,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_multi_kernel(
     for (int r = 0; r < R; ++r) acc[r] = 0.0f;
     for (int p = pl; p < np; p += LPR) {
         uint32_t wn[R][DW];
-        if (p + LPR < np) load_rows<R, DW>(W, row_dw, row0, M, p + LPR, wn);
+        if (p + LPR < np) load_rows<R, DW>(g, row_dw, row0, M, p + LPR, wn);
         float xv[64];
         load_xv(xs4, p, xv);
         const float2 c0 = cb[2 * p];
@@ -174,7 +210,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_multi_kernel(
     if (pl == LPR - 1) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            if (row0 + r < M) y[row0 + r] = acc[r];
+            if (row0 + r < M) *group_y(g, row0 + r, M, blockIdx.y) = acc[r];
         }
     }
 }
@@ -183,19 +219,19 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_multi_kernel(
 // Generic kernel: one wave per output row, lanes over blocks, byte loads.
 // Handles every shape (odd block counts, K beyond the LDS budget).
 template <int QT>
-__global__ __launch_bounds__(256) void gemv_generic_kernel(const uint8_t* __restrict__ W,
-                                                           const float* __restrict__ x,
-                                                           float* __restrict__ y, int M, int K,
-                                                           int nb) {
+__global__ __launch_bounds__(256) void gemv_generic_kernel(const GemvGroup g, const float* __restrict__ x,
+                                                           int M, int K, int nb) {
     constexpr int BB = Fmt<QT>::BB;
     const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int row = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if (row >= M) return;
     x += static_cast<size_t>(blockIdx.y) * K;
-    y += static_cast<size_t>(blockIdx.y) * M;
+    const int k = group_call(g, row);
+    const uint8_t* W = static_cast<const uint8_t*>(g.W[k]) +
+                       static_cast<size_t>(row - g.row_begin[k]) * nb * BB;
     float acc = 0.0f;
     for (int b = lane; b < nb; b += 64) {
-        const uint8_t* blk = W + (static_cast<size_t>(row) * nb + b) * BB;
+        const uint8_t* blk = W + static_cast<size_t>(b) * BB;
         const uint16_t dbits = static_cast<uint16_t>(blk[0] | (blk[1] << 8));
         const float d = (float)__builtin_bit_cast(_Float16, dbits);
         const int k0 = b * kQK;
@@ -223,7 +259,7 @@ __global__ __launch_bounds__(256) void gemv_generic_kernel(const uint8_t* __rest
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
-    if (lane == 0) y[row] = acc;
+    if (lane == 0) *group_y(g, row, M, blockIdx.y) = acc;
 }
 
 // ---------------------------------------------------------------------------
@@ -252,58 +288,63 @@ PairCfg choose_pair(const LinearShape& s) {
 }
 
 template <int QT, int LPR, int R>
-hipError_t launch_single_t(const LinearShape& s, const void* w, const float* x, float* y,
-                           hipStream_t stream) {
+hipError_t launch_single_t(const LinearShape& s, const GemvGroup& g, const float* x, hipStream_t stream) {
     constexpr int rows_per_group = (64 / LPR) * R;
     const int groups = (s.M + rows_per_group - 1) / rows_per_group;
     int grid = (groups + kWaves - 1) / kWaves;
     if (grid > kPersistentWgs) grid = kPersistentWgs;
     hipLaunchKernelGGL((gemv_single_kernel<QT, LPR, R, kWaves>), dim3(grid, s.rows), dim3(kWaves * 64),
-                       pair_lds_bytes(s.nb), stream, static_cast<const uint8_t*>(w), x, y, s.M, s.K, s.nb,
-                       groups);
+                       pair_lds_bytes(s.nb), stream, g, x, s.M, s.K, s.nb, groups);
     return hipGetLastError();
 }
 
 template <int QT, int LPR>
-hipError_t launch_multi_t(const LinearShape& s, const void* w, const float* x, float* y,
-                          hipStream_t stream) {
+hipError_t launch_multi_t(const LinearShape& s, const GemvGroup& g, const float* x, hipStream_t stream) {
     constexpr int rows_per_wg = kWaves * (64 / LPR);
     dim3 grid((s.M + rows_per_wg - 1) / rows_per_wg, s.rows);
     hipLaunchKernelGGL((gemv_multi_kernel<QT, LPR, 1, kWaves>), grid, dim3(kWaves * 64), pair_lds_bytes(s.nb),
-                       stream, static_cast<const uint8_t*>(w), x, y, s.M, s.K, s.nb);
+                       stream, g, x, s.M, s.K, s.nb);
     return hipGetLastError();
 }
 
 template <int QT>
-hipError_t launch_q(const LinearShape& s, const PairCfg& c, const void* w, const float* x, float* y,
+hipError_t launch_q(const LinearShape& s, const PairCfg& c, const GemvGroup& g, const float* x,
                     hipStream_t stream) {
     if (c.kind == Kind::Single) {
-        if (c.lpr == 16) return launch_single_t<QT, 16, 1>(s, w, x, y, stream);
-        if (c.r == 2) return launch_single_t<QT, 64, 2>(s, w, x, y, stream);
-        return launch_single_t<QT, 64, 1>(s, w, x, y, stream);
+        if (c.lpr == 16) return launch_single_t<QT, 16, 1>(s, g, x, stream);
+        if (c.r == 2) return launch_single_t<QT, 64, 2>(s, g, x, stream);
+        return launch_single_t<QT, 64, 1>(s, g, x, stream);
     }
     if (c.kind == Kind::Multi) {
-        if (c.lpr == 64) return launch_multi_t<QT, 64>(s, w, x, y, stream);
-        if (c.lpr == 32) return launch_multi_t<QT, 32>(s, w, x, y, stream);
-        return launch_multi_t<QT, 16>(s, w, x, y, stream);
+        if (c.lpr == 64) return launch_multi_t<QT, 64>(s, g, x, stream);
+        if (c.lpr == 32) return launch_multi_t<QT, 32>(s, g, x, stream);
+        return launch_multi_t<QT, 16>(s, g, x, stream);
     }
     dim3 grid((s.M + 3) / 4, s.rows);
-    hipLaunchKernelGGL((gemv_generic_kernel<QT>), grid, dim3(256), 0, stream, static_cast<const uint8_t*>(w), x,
-                       y, s.M, s.K, s.nb);
+    hipLaunchKernelGGL((gemv_generic_kernel<QT>), grid, dim3(256), 0, stream, g, x, s.M, s.K, s.nb);
     return hipGetLastError();
 }
 
 }  // namespace
 
-hipError_t launch_gemv(const LinearShape& s, const void* w, const float* x, float* y,
-                       hipStream_t stream) {
+hipError_t launch_gemv_group(const LinearShape& s, const GemvGroup& g, const float* x, hipStream_t stream) {
+    if (g.ncalls < 1 || g.ncalls > kGroupMaxCalls) return hipErrorInvalidValue;
     const PairCfg c = choose_pair(s);
     switch (s.qtype) {
-        case 1: return launch_q<1>(s, c, w, x, y, stream);
-        case 2: return launch_q<2>(s, c, w, x, y, stream);
-        case 3: return launch_q<3>(s, c, w, x, y, stream);
+        case 1: return launch_q<1>(s, c, g, x, stream);
+        case 2: return launch_q<2>(s, c, g, x, stream);
+        case 3: return launch_q<3>(s, c, g, x, stream);
         default: return hipErrorInvalidValue;
     }
+}
+
+hipError_t launch_gemv(const LinearShape& s, const void* w, const float* x, float* y,
+                       hipStream_t stream) {
+    GemvGroup g{};
+    g.W[0] = w;
+    g.y[0] = y;
+    g.ncalls = 1;
+    return launch_gemv_group(s, g, x, stream);
 }
 
 const char* gemv_kernel_name(const LinearShape& s) {

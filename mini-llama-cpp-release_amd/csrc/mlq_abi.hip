@@ -52,6 +52,13 @@ struct mlq_sequence_s {
     int nstages;
     unsigned spin_limit;
     std::vector<Segment> segs;
+    // Per-stage mode: one grouped GEMV launch per stage.
+    struct HostStage {
+        mlq::LinearShape shape;  // M = rows of all calls of the stage
+        mlq::GemvGroup group;
+        const float* x;
+    };
+    std::vector<HostStage> host_stages;
     void* mem;               // [stage descriptors][SeqSync per segment]
     size_t sync_offset;      // byte offset of the first SeqSync
 };
@@ -474,6 +481,58 @@ int mlq_hip_quant_linear_many(const mlq_linear_call* calls, int n, void* stream)
     return MLQ_OK;
 }
 
+int mlq_hip_quant_linear_fused(const mlq_linear_call* calls, int n, void* stream) {
+    static const char* caller = "mlq_hip_quant_linear_fused";
+    if (calls == nullptr || n <= 0) return fail(MLQ_ERR_INVALID, std::string(caller) + ": no calls");
+    if (n > mlq::kGroupMaxCalls) {
+        return fail(MLQ_ERR_LIMIT, std::string(caller) + ": " + std::to_string(n) + " calls (at most " +
+                                       std::to_string(mlq::kGroupMaxCalls) + ")");
+    }
+    if (calls[0].w == nullptr) return fail(MLQ_ERR_INVALID, std::string(caller) + ": null weight handle");
+    const mlq_weight_s* w0 = calls[0].w;
+    const int device = w0->device;
+    int rc = ensure_device(device);
+    if (rc != MLQ_OK) return rc;
+    mlq::GemvGroup g{};
+    long long rows = 0;
+    for (int i = 0; i < n; ++i) {
+        const mlq_linear_call& c = calls[i];
+        const std::string at = std::string(caller) + ": call " + std::to_string(i);
+        if (c.w == nullptr) return fail(MLQ_ERR_INVALID, at + ": null weight handle");
+        if (c.w->device != device) return fail(MLQ_ERR_DEVICE, at + ": weight on a different device");
+        if (c.rows != 1) return fail(MLQ_ERR_INVALID, at + ": rows must be 1 (a fused launch is a GEMV)");
+        if (c.x != calls[0].x || c.w->K != w0->K || c.w->qtype != w0->qtype) {
+            return fail(MLQ_ERR_INVALID, at + ": differs from call 0 in input, in_features or quant type");
+        }
+        if ((rc = validate_linear(c.w->qtype, c.w->M, c.w->K, c.w->n_blocks, 1)) != MLQ_OK) return rc;
+        const char* lin = caller_for(c.w->qtype);
+        const size_t xb = static_cast<size_t>(c.w->K) * sizeof(float);
+        const size_t yb = static_cast<size_t>(c.w->M) * sizeof(float);
+        if ((rc = check_device_ptr(c.x, device, lin, "input", xb)) != MLQ_OK) return rc;
+        if ((rc = check_device_ptr(c.y, device, lin, "output", yb)) != MLQ_OK) return rc;
+        const uintptr_t ylo = reinterpret_cast<uintptr_t>(c.y), yhi = ylo + yb;
+        const uintptr_t xlo = reinterpret_cast<uintptr_t>(c.x), xhi = xlo + xb;
+        if (ylo < xhi && xlo < yhi) return fail(MLQ_ERR_INVALID, at + ": output overlaps the input");
+        for (int j = 0; j < i; ++j) {
+            const uintptr_t olo = reinterpret_cast<uintptr_t>(calls[j].y);
+            const uintptr_t ohi = olo + static_cast<size_t>(calls[j].w->M) * sizeof(float);
+            if (ylo < ohi && olo < yhi) {
+                return fail(MLQ_ERR_INVALID, at + ": output overlaps the output of call " + std::to_string(j));
+            }
+        }
+        g.W[i] = c.w->ptr;
+        g.y[i] = c.y;
+        g.row_begin[i] = static_cast<int>(rows);
+        rows += c.w->M;
+    }
+    if (rows > (1ll << 30)) return fail(MLQ_ERR_LIMIT, std::string(caller) + ": too many rows");
+    g.ncalls = n;
+    mlq::LinearShape shape{w0->qtype, static_cast<int>(rows), w0->K, w0->nb, 1};
+    hipError_t e = mlq::launch_gemv_group(shape, g, calls[0].x, resolve_stream(device, stream));
+    if (e != hipSuccess) return hip_fail(e, caller);
+    return MLQ_OK;
+}
+
 int mlq_hip_quantize(int device, int qtype, const float* src, int rows, int row_len,
                      void* device_blocks, void* stream) {
     if (qtype != MLQ_Q8_0 && qtype != MLQ_Q4_0 && qtype != MLQ_Q4_1) {
@@ -834,6 +893,21 @@ int mlq_hip_sequence_create(const mlq_linear_call* calls, int n, const int* stag
         stage_first.push_back(i);
         i = j;
     }
+    std::vector<mlq_sequence_s::HostStage> host_stages;
+    for (size_t k = 0; k < descs.size(); ++k) {
+        const mlq::SeqStageDesc& d = descs[k];
+        mlq_sequence_s::HostStage hs;
+        hs.shape = mlq::LinearShape{calls[stage_first[k]].w->qtype, d.rows, d.K, d.nb, 1};
+        hs.group = mlq::GemvGroup{};
+        for (int c = 0; c < d.ncalls; ++c) {
+            hs.group.W[c] = d.call[c].W;
+            hs.group.y[c] = d.call[c].y;
+            hs.group.row_begin[c] = d.call[c].row_begin;
+        }
+        hs.group.ncalls = d.ncalls;
+        hs.x = d.x;
+        host_stages.push_back(hs);
+    }
 
     // Segments: runs of stages with one kernel variant; one per stage in
     // per-stage mode.
@@ -843,6 +917,7 @@ int mlq_hip_sequence_create(const mlq_linear_call* calls, int n, const int* stag
     seq->nstages = static_cast<int>(descs.size());
     seq->spin_limit = kDefaultSpinLimit;
     seq->mem = nullptr;
+    seq->host_stages = std::move(host_stages);
     for (int s = 0; s < seq->nstages; ++s) {
         const mlq_weight_s* w0 = calls[stage_first[s]].w;
         const int lpr = mlq::sequence_lpr(w0->K);
@@ -890,6 +965,13 @@ int mlq_hip_sequence_launch(mlq_sequence_t seq, void* stream) {
     int rc = ensure_device(seq->device);
     if (rc != MLQ_OK) return rc;
     hipStream_t s = resolve_stream(seq->device, stream);
+    if (seq->mode == MLQ_SEQ_PER_STAGE) {
+        for (const auto& hs : seq->host_stages) {
+            hipError_t e = mlq::launch_gemv_group(hs.shape, hs.group, hs.x, s);
+            if (e != hipSuccess) return hip_fail(e, mlq::gemv_kernel_name(hs.shape));
+        }
+        return MLQ_OK;
+    }
     auto* table = static_cast<const mlq::SeqStageDesc*>(seq->mem);
     auto* syncs = reinterpret_cast<mlq::SeqSync*>(static_cast<char*>(seq->mem) + seq->sync_offset);
     for (size_t i = 0; i < seq->segs.size(); ++i) {
@@ -931,7 +1013,9 @@ int mlq_hip_sequence_set_spin_limit(mlq_sequence_t seq, unsigned polls) {
 int mlq_hip_sequence_info(mlq_sequence_t seq, int* stages, int* launches, int* grid) {
     if (seq == nullptr) return fail(MLQ_ERR_INVALID, "mlq_hip_sequence_info: null sequence");
     if (stages) *stages = seq->nstages;
-    if (launches) *launches = static_cast<int>(seq->segs.size());
+    if (launches) {
+        *launches = seq->mode == MLQ_SEQ_PER_STAGE ? seq->nstages : static_cast<int>(seq->segs.size());
+    }
     if (grid) *grid = seq->segs.empty() ? 0 : seq->segs[0].grid;
     return MLQ_OK;
 }

@@ -35,6 +35,21 @@ hipError_t launch_gemv(const LinearShape& s, const void* w, const float* x, floa
                        hipStream_t stream);
 const char* gemv_kernel_name(const LinearShape& s);
 
+// Up to kGroupMaxCalls GEMVs that read the same x (a fused q/k/v or gate/up
+// launch): their rows are concatenated in call order, call j owning rows
+// [row_begin[j], row_begin[j] + M_j) of the launch's s.M rows.  Each row is
+// computed exactly as by a launch of its own call.
+constexpr int kGroupMaxCalls = 4;
+
+struct GemvGroup {
+    const void* W[kGroupMaxCalls];
+    float* y[kGroupMaxCalls];
+    int row_begin[kGroupMaxCalls];
+    int ncalls;
+};
+
+hipError_t launch_gemv_group(const LinearShape& s, const GemvGroup& g, const float* x, hipStream_t stream);
+
 // Batched prefill GEMM for rows > 1 (MFMA).  Needs a device workspace of
 // gemm_workspace_bytes(s) bytes (split x, scales, split-K partials) that no
 // other launch uses concurrently.  Returns hipErrorNotSupported when the shape
@@ -49,7 +64,7 @@ const char* gemm_kernel_name(const LinearShape& s);
 // kSeqMaxCalls GEMVs reading the same x; their rows are concatenated in call
 // order (call j owns rows [row_begin, row_begin + M)).  Descriptors live in
 // device memory for as long as any launch that uses them.
-constexpr int kSeqMaxCalls = 4;
+constexpr int kSeqMaxCalls = kGroupMaxCalls;
 
 struct SeqCallDesc {
     const void* W;   // [M][nb] blocks

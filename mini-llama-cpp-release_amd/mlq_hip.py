@@ -59,6 +59,7 @@ _SIGS = {
     "mlq_hip_quant_linear_device": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, _vp, ctypes.c_size_t,
                                                     ctypes.c_int, ctypes.c_int, _vp, ctypes.c_int, _vp, _vp]),
     "mlq_hip_quant_linear_many": (ctypes.c_int, [ctypes.POINTER(LinearCall), ctypes.c_int, _vp]),
+    "mlq_hip_quant_linear_fused": (ctypes.c_int, [ctypes.POINTER(LinearCall), ctypes.c_int, _vp]),
     "mlq_hip_quantize": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, _vp, ctypes.c_int, ctypes.c_int, _vp, _vp]),
     "mlq_hip_malloc": (ctypes.c_int, [ctypes.c_int, ctypes.c_size_t, ctypes.POINTER(_vp)]),
     "mlq_hip_free": (ctypes.c_int, [_vp]),
@@ -271,6 +272,11 @@ def make_calls(calls) -> ctypes.Array:
 
 def linear_many(arr: ctypes.Array, stream=None) -> None:
     _check(load().mlq_hip_quant_linear_many(arr, len(arr), stream))
+
+
+def linear_fused(arr: ctypes.Array, stream=None) -> None:
+    """One launch for up to 4 GEMVs that share x (asynchronous on `stream`)."""
+    _check(load().mlq_hip_quant_linear_fused(arr, len(arr), stream))
 
 
 class Sequence:

@@ -255,3 +255,49 @@ def test_barrier_wait_bound_recovers(hip):
     assert seq.status() == 0
     for i, (g, w) in enumerate(zip(snapshot(outs), want)):
         assert np.array_equal(g.view(np.uint32), w.view(np.uint32)), f"call {i} after recovery"
+
+
+@pytest.mark.parametrize("shape", [(4096, 4096), (11008, 4096), (896, 896), (128, 896), (33, 4864),
+                                   (64, 96), (40, 20000), (7, 33)],
+                         ids=lambda s: f"{s[0]}x{s[1]}")
+def test_fused_launch_matches_per_call(hip, shape):
+    """mlq_hip_quant_linear_fused: 1-4 calls sharing x in one launch (pair
+    kernels, odd block counts and K past the pair-kernel limit, which take the
+    byte-load kernel), bit-identical to one launch per call."""
+    m, k = shape
+    for fmt, qt in FMTS.items():
+        lins = [Lin(hip, qt, m + 5 * i, k, 60 + i) for i in range(4)]
+        x = vec(hip, k, 61)
+        outs = [hip.DeviceBuffer(4 * (m + 5 * i)) for i in range(4)]
+        calls = [(lins[i], x, outs[i]) for i in range(4)]
+        per_call(hip, calls)
+        want = snapshot(outs)
+        for n in (1, 2, 3, 4):
+            for b in outs:
+                b.fill(0)
+            say(f"fused {fmt} {m}x{k} n={n}")
+            hip.linear_fused(hip.make_calls([(c[0].w, c[1], c[2], 1) for c in calls[:n]]))
+            hip.synchronize()
+            for i, (g, w) in enumerate(zip(snapshot(outs[:n]), want[:n])):
+                assert np.array_equal(g.view(np.uint32), w.view(np.uint32)), f"fused {fmt} {m}x{k} n={n} call {i}"
+
+
+def test_fused_validation(hip):
+    l1 = Lin(hip, oracle.Q4_0, 64, 128, 1)
+    l2 = Lin(hip, oracle.Q8_0, 64, 128, 2)
+    x = vec(hip, 256, 3)
+    y = [hip.DeviceBuffer(4 * 64) for _ in range(5)]
+
+    def fused(calls):
+        hip.linear_fused(hip.make_calls(calls))
+
+    with pytest.raises(hip.MlqError, match="differs from call 0"):
+        fused([(l1.w, x, y[0], 1), (l2.w, x, y[1], 1)])
+    with pytest.raises(hip.MlqError, match="at most 4"):
+        fused([(l1.w, x, y[i], 1) for i in range(5)])
+    with pytest.raises(hip.MlqError, match="overlaps the output of call 0"):
+        fused([(l1.w, x, y[0], 1), (l1.w, x, y[0], 1)])
+    with pytest.raises(hip.MlqError, match="overlaps the input"):
+        fused([(l1.w, x, x, 1)])
+    with pytest.raises(hip.MlqError, match="rows must be 1"):
+        fused([(l1.w, x, y[0], 2)])
