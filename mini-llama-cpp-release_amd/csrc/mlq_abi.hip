@@ -222,6 +222,9 @@ int stream_workspace(int device, hipStream_t stream, size_t bytes, void** out) {
             w.ptr = nullptr;
             w.bytes = 0;
             MLQ_HIP_CHECK(hipMalloc(&w.ptr, bytes));
+            // The split-K arrival counters start at zero; every launch leaves
+            // them so.  Cleared on the workspace's own stream, ahead of its kernels.
+            MLQ_HIP_CHECK(hipMemsetAsync(w.ptr, 0, bytes, stream));
             w.bytes = bytes;
         }
         *out = w.ptr;
@@ -229,6 +232,7 @@ int stream_workspace(int device, hipStream_t stream, size_t bytes, void** out) {
     }
     void* p = nullptr;
     MLQ_HIP_CHECK(hipMalloc(&p, bytes));
+    MLQ_HIP_CHECK(hipMemsetAsync(p, 0, bytes, stream));
     st.ws.push_back(Workspace{stream, p, bytes});
     *out = p;
     return MLQ_OK;
