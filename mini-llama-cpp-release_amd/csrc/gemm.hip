@@ -279,151 +279,42 @@ __device__ __forceinline__ void decode_pair(const uint32_t (&r)[7], WFrag& f0, W
     }
 }
 
-// Tiled MFMA kernel: a workgroup of four waves owns BM weight rows x BN tokens
-// and the pairs [p0, p1) of K.  Per pair, the workgroup copies the raw weight
-// dwords (BM rows x one pair) and the split x fragments (2 blocks x BN tokens x
-// 32 hi + 32 lo halves) from global memory into LDS, double-buffered, so every
-// weight byte is read once per token tile and every x fragment once per row
-// tile.  The waves are arranged WM x WN over the tile; a wave decodes the codes
-// of its own row tiles from LDS and multiplies them with every token tile it
-// owns.
+// Streaming MFMA kernel.  A workgroup of four waves owns BM = 64 * RT weight
+// rows x BN = 16 * TT tokens and the pairs [p0, p1) of K.  Wave w owns rows
+// [16 * RT * w, 16 * RT * (w + 1)) of the tile and reads their weight pairs
+// straight from global memory into registers in fragment layout (nobody else
+// needs them); the x fragments of a pair (2 blocks x BN tokens x 32 hi + 32 lo
+// halves) are shared by the four waves, so the workgroup copies them into LDS,
+// double-buffered, one barrier per pair.  Both are requested one pair ahead;
+// latency is hidden by several workgroups per CU.  Per block each wave decodes
+// RT weight fragments and issues 2 * RT * TT MFMAs (x hi, x lo).
 constexpr int kGemmThreads = 256;
 constexpr int kGemmMaxTiles = 65536;  // split-K arrival counters in the workspace
-constexpr int kXRowHalves = 72;  // 64 halves of one token's block + 8 of padding (bank spread)
+constexpr int kXRowHalves = 72;       // 64 halves of one token's block + 8 of padding (bank spread)
 
-template <int QT, int BM, int BN>
-struct TileLds {
-    static constexpr int DW = GFmt<QT>::DW;
-    static constexpr int w_dwords = BM * DW;                 // raw pair dwords, row-major
-    static constexpr int x_halves = 2 * BN * kXRowHalves;    // [block][token][72]
-    static constexpr int s_floats = QT == 3 ? 2 * BN : 0;    // Q4_1 block sums [block][token]
-    static constexpr int stage_bytes = w_dwords * 4 + x_halves * 2 + s_floats * 4;
+template <int TT>
+struct StreamLds {
+    static constexpr int BN = 16 * TT;
+    static constexpr int x_halves = 2 * BN * kXRowHalves;  // [block h][token][72]
+    static constexpr int stage_bytes = x_halves * 2 + 2 * BN * 4;  // + Q4_1 block sums [h][token]
     static constexpr int bytes = 2 * stage_bytes;
 };
 
-template <int QT, int BM, int BN>
-__device__ __forceinline__ void tile_load_global(const uint32_t* const (&wrow)[(BM * GFmt<QT>::DW + kGemmThreads - 1) / kGemmThreads],
-                                                 const _Float16* __restrict__ xs, const float* __restrict__ bsum,
-                                                 int npad, int n_base, int p,
-                                                 uint32_t (&wr)[(BM * GFmt<QT>::DW + kGemmThreads - 1) / kGemmThreads],
-                                                 u32x4 (&xr)[(2 * BN * 8 + kGemmThreads - 1) / kGemmThreads],
-                                                 float (&sr)[QT == 3 ? (2 * BN + kGemmThreads - 1) / kGemmThreads : 1]) {
-    constexpr int DW = GFmt<QT>::DW;
-    constexpr int WN_ = (BM * DW + kGemmThreads - 1) / kGemmThreads;
-    constexpr int XN = (2 * BN * 8 + kGemmThreads - 1) / kGemmThreads;
-    // Unconditional loads (indices clamped where the tile is not a multiple of
-    // the thread count; the copies past the end are never stored), so the
-    // compiler can count them in order instead of waiting for all of them.
-#pragma unroll
-    for (int j = 0; j < WN_; ++j) wr[j] = wrow[j][static_cast<size_t>(p) * DW];
-#pragma unroll
-    for (int j = 0; j < XN; ++j) {
-        const int idx = min(static_cast<int>(threadIdx.x) + j * kGemmThreads, 2 * BN * 8 - 1);  // [h][t][c]
-        const int c = idx & 7;
-        const int t = (idx >> 3) % BN;
-        const int h = (idx >> 3) / BN;
-        const size_t off = (static_cast<size_t>(2 * p + h) * npad + n_base + t) * 64 + 8 * c;
-        xr[j] = *reinterpret_cast<const u32x4*>(xs + off);
-    }
-    if (QT == 3) {
-#pragma unroll
-        for (int j = 0; j < (2 * BN + kGemmThreads - 1) / kGemmThreads; ++j) {
-            const int idx = min(static_cast<int>(threadIdx.x) + j * kGemmThreads, 2 * BN - 1);
-            const int t = idx % BN;
-            const int h = idx / BN;
-            sr[j] = bsum[static_cast<size_t>(2 * p + h) * npad + n_base + t];
-        }
-    }
-}
-
-template <int QT, int BM, int BN>
-__device__ __forceinline__ void tile_store_lds(char* stage,
-                                               const uint32_t (&wr)[(BM * GFmt<QT>::DW + kGemmThreads - 1) / kGemmThreads],
-                                               const u32x4 (&xr)[(2 * BN * 8 + kGemmThreads - 1) / kGemmThreads],
-                                               const float (&sr)[QT == 3 ? (2 * BN + kGemmThreads - 1) / kGemmThreads : 1]) {
-    using L = TileLds<QT, BM, BN>;
-    constexpr int DW = GFmt<QT>::DW;
-    uint32_t* wl = reinterpret_cast<uint32_t*>(stage);
-    _Float16* xl = reinterpret_cast<_Float16*>(stage + L::w_dwords * 4);
-    float* sl = reinterpret_cast<float*>(stage + L::w_dwords * 4 + L::x_halves * 2);
-#pragma unroll
-    for (int j = 0; j < (BM * DW + kGemmThreads - 1) / kGemmThreads; ++j) {
-        const int idx = threadIdx.x + j * kGemmThreads;
-        if (idx < BM * DW) wl[idx] = wr[j];
-    }
-#pragma unroll
-    for (int j = 0; j < (2 * BN * 8 + kGemmThreads - 1) / kGemmThreads; ++j) {
-        const int idx = threadIdx.x + j * kGemmThreads;
-        if (idx < 2 * BN * 8) {
-            const int c = idx & 7;
-            const int row = idx >> 3;  // h * BN + t
-            *reinterpret_cast<u32x4*>(xl + row * kXRowHalves + 8 * c) = xr[j];
-        }
-    }
-    if (QT == 3) {
-#pragma unroll
-        for (int j = 0; j < (2 * BN + kGemmThreads - 1) / kGemmThreads; ++j) {
-            const int idx = threadIdx.x + j * kGemmThreads;
-            if (idx < 2 * BN) sl[idx] = sr[j];
-        }
-    }
-}
-
-// Weight fragment of block h (0/1) of the pair for row `row` of the tile, from
-// the raw pair dwords in LDS.
-template <int QT>
-__device__ __forceinline__ void lds_wfrag(const uint32_t* wl, int row, int g, int h, WFrag& f, uint32_t mask,
-                                          uint32_t magic) {
-    constexpr int DW = GFmt<QT>::DW;
-    const uint32_t* pw = wl + row * DW;
-    if (QT == 2) {
-        const uint32_t nb2 = 0xE408E408u;  // {-1032.0h, -1032.0h}
-        if (h == 0) {
-            f.b = nibbles_to_f16(__builtin_amdgcn_alignbit(pw[g + 1], pw[g], 16), nb2, mask, magic);
-            f.d = h_lo(pw[0]);
-        } else {
-            f.b = nibbles_to_f16(pw[5 + g], nb2, mask, magic);
-            f.d = h_hi(pw[4]);
-        }
-        f.m = 0.0f;
-    } else if (QT == 1) {
-        const uint32_t nb2 = 0xE480E480u;  // {-1152.0h, -1152.0h}
-        if (h == 0) {
-            f.b = bytes_to_f16(__builtin_amdgcn_alignbit(pw[2 * g + 1], pw[2 * g], 16),
-                               __builtin_amdgcn_alignbit(pw[2 * g + 2], pw[2 * g + 1], 16), nb2);
-            f.d = h_lo(pw[0]);
-        } else {
-            f.b = bytes_to_f16(pw[9 + 2 * g], pw[10 + 2 * g], nb2);
-            f.d = h_hi(pw[8]);
-        }
-        f.m = 0.0f;
-    } else {
-        const uint32_t nb2 = 0xE400E400u;  // {-1024.0h, -1024.0h}
-        const int o = 5 * h;
-        f.b = nibbles_to_f16(pw[o + 1 + g], nb2, mask, magic);
-        f.d = h_lo(pw[o]);
-        f.m = h_hi(pw[o]);
-    }
-}
-
-template <int QT, int BM, int BN, int WM, int WN, int D>
-__global__ __launch_bounds__(kGemmThreads) void gemm_tile_kernel(
+template <int QT, int RT, int TT, int D>
+__global__ __launch_bounds__(kGemmThreads) void gemm_stream_kernel(
     const uint8_t* __restrict__ W, const _Float16* __restrict__ xs, const float* __restrict__ bsum,
     const float* __restrict__ scale, float* __restrict__ y, float* __restrict__ part,
     unsigned* __restrict__ tile_count, int M, int N, int npad, int nb, int pairs_per_split) {
-    using L = TileLds<QT, BM, BN>;
+    using L = StreamLds<TT>;
     constexpr int DW = GFmt<QT>::DW;
-    constexpr int RT = BM / (16 * WM);  // row tiles per wave
-    constexpr int TT = BN / (16 * WN);  // token tiles per wave
-    constexpr int WLD = (BM * DW + kGemmThreads - 1) / kGemmThreads;
-    constexpr int XLD = (2 * BN * 8 + kGemmThreads - 1) / kGemmThreads;
-    constexpr int SLD = QT == 3 ? (2 * BN + kGemmThreads - 1) / kGemmThreads : 1;
+    constexpr int BM = 64 * RT;
+    constexpr int BN = 16 * TT;
+    constexpr int XC = (16 * BN) / kGemmThreads;  // 16-byte x chunks per thread per pair
+    static_assert((16 * BN) % kGemmThreads == 0, "x chunks must divide evenly");
     extern __shared__ __attribute__((aligned(16))) char smem[];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int wm = wave / WN;
-    const int wn = wave % WN;
     const int i16 = lane & 15;
     const int g = lane >> 4;
     const int m_base = blockIdx.x * BM;
@@ -435,15 +326,30 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_tile_kernel(
     uint32_t mask = 0x000F000Fu, magic = 0x64006400u;
     asm volatile("" : "+v"(mask), "+v"(magic));
 
-    // Global row pointers of the raw-weight dwords this thread copies.
-    const uint32_t* wrow[WLD];
+    // Weight rows of this lane (rows past M re-read row M-1; results dropped).
+    const uint32_t* wrow[RT];
 #pragma unroll
-    for (int j = 0; j < WLD; ++j) {
-        const int idx = min(static_cast<int>(threadIdx.x) + j * kGemmThreads, BM * DW - 1);
-        const int r = idx / DW;
-        const int m = min(m_base + r, M - 1);  // rows past M copy row M-1; results dropped
-        wrow[j] = reinterpret_cast<const uint32_t*>(W) + static_cast<size_t>(m) * np * DW + (idx - r * DW);
+    for (int r = 0; r < RT; ++r) {
+        const int m = min(m_base + (wave * RT + r) * 16 + i16, M - 1);
+        wrow[r] = reinterpret_cast<const uint32_t*>(W) + static_cast<size_t>(m) * np * DW;
     }
+    // x chunks this thread copies: global offset = p * xstride + xoff[j],
+    // LDS offset = loff[j] (both in halves).
+    const size_t xstride = static_cast<size_t>(2) * npad * 64;
+    size_t xoff[XC];
+    int loff[XC];
+#pragma unroll
+    for (int j = 0; j < XC; ++j) {
+        const int c = threadIdx.x + j * kGemmThreads;  // [h][token][chunk of 8]
+        const int h = c / (8 * BN);
+        const int rem = c % (8 * BN);
+        const int t = rem >> 3;
+        const int q = rem & 7;
+        xoff[j] = (static_cast<size_t>(h) * npad + n_base + t) * 64 + 8 * q;
+        loff[j] = (h * BN + t) * kXRowHalves + 8 * q;
+    }
+    const bool sum_lane = QT == 3 && threadIdx.x < 2 * BN;
+    const size_t soff = QT == 3 ? static_cast<size_t>(threadIdx.x / BN) * npad + n_base + threadIdx.x % BN : 0;
 
     f32x4 acc[RT][TT];
 #pragma unroll
@@ -452,73 +358,90 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_tile_kernel(
         for (int t = 0; t < TT; ++t) acc[r][t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     const f32x4 zero{0.0f, 0.0f, 0.0f, 0.0f};
 
-    // Pipeline: pair q's global loads are issued D pairs ahead into register
-    // set q % D; at step q they go to LDS buffer q & 1, the workgroup syncs, the
-    // loads for pair q + D are issued into the freed set, and the waves compute
-    // pair q from LDS.  One barrier per pair: the buffer written at step q was
-    // last read at step q - 2, before the barrier of step q - 1.
-    uint32_t wr[D][WLD];
-    u32x4 xr[D][XLD];
-    float sr[D][SLD];
+    // Load pipeline, D pairs deep: register set d holds pair q = q0 + d (weights
+    // in fragment layout, x chunks).  Step q: x chunks of set d -> LDS buffer
+    // q & 1; barrier; compute pair q (weights of set d, x from LDS); request
+    // pair q + D into set d.  The buffer written at step q was last read at step
+    // q - 2, before the barrier of step q - 1.  Requests past the split's last
+    // pair re-read that pair, so every load is unconditional.
+    uint32_t wr[D][RT][7];
+    u32x4 xr[D][XC];
+    float sr[D];
+    auto request = [&](int p, uint32_t (&w)[RT][7], u32x4 (&x)[XC], float& sv) {
 #pragma unroll
-    for (int d = 0; d < D; ++d) {
-        if (p0 + d < p1) tile_load_global<QT, BM, BN>(wrow, xs, bsum, npad, n_base, p0 + d, wr[d], xr[d], sr[d]);
-    }
+        for (int r = 0; r < RT; ++r) load_pair<QT>(wrow[r] + static_cast<size_t>(p) * DW, g, w[r]);
+#pragma unroll
+        for (int j = 0; j < XC; ++j) x[j] = *reinterpret_cast<const u32x4*>(xs + p * xstride + xoff[j]);
+        if (QT == 3) sv = bsum[static_cast<size_t>(2 * p) * npad + soff];
+    };
+    const int plast = max(p0, p1 - 1);
+#pragma unroll
+    for (int d = 0; d < D; ++d) request(min(p0 + d, plast), wr[d], xr[d], sr[d]);
 
-    // Step q: LDS buffer (q - p0) & 1 <- register set d; barrier; optionally
-    // request pair q + D into set d; compute pair q.
-    auto step = [&](int q, auto& wrd, auto& xrd, auto& srd, bool refill) {
-        char* cur = smem + ((q - p0) & 1) * L::stage_bytes;
-        tile_store_lds<QT, BM, BN>(cur, wrd, xrd, srd);
+    auto step = [&](int q, uint32_t (&wrd)[RT][7], u32x4 (&xrd)[XC], float& srd) {
+            char* cur = smem + ((q - p0) & 1) * L::stage_bytes;
+        {
+            _Float16* xl = reinterpret_cast<_Float16*>(cur);
+#pragma unroll
+            for (int j = 0; j < XC; ++j) *reinterpret_cast<u32x4*>(xl + loff[j]) = xrd[j];
+            if (sum_lane) reinterpret_cast<float*>(cur + L::x_halves * 2)[threadIdx.x] = srd;
+        }
         __syncthreads();
-        if (refill) tile_load_global<QT, BM, BN>(wrow, xs, bsum, npad, n_base, q + D, wrd, xrd, srd);
-        const uint32_t* wl = reinterpret_cast<const uint32_t*>(cur);
-        const _Float16* xl = reinterpret_cast<const _Float16*>(cur + L::w_dwords * 4);
-        const float* sl = reinterpret_cast<const float*>(cur + L::w_dwords * 4 + L::x_halves * 2);
+        const _Float16* xl = reinterpret_cast<const _Float16*>(cur);
+        const float* sl = reinterpret_cast<const float*>(cur + L::x_halves * 2);
+        // Per block: all x fragments, all weight fragments, then every MFMA of
+        // the block (independent accumulator tiles, so they pipeline), then
+        // the scale epilogue.
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             f16x8 ahi[TT], alo[TT];
             f32x4 sv[TT];
 #pragma unroll
             for (int t = 0; t < TT; ++t) {
-                const int tok = (wn * TT + t) * 16 + i16;
-                const _Float16* src = xl + (h * BN + tok) * kXRowHalves + 8 * g;
+                const _Float16* src = xl + (h * BN + t * 16 + i16) * kXRowHalves + 8 * g;
                 ahi[t] = *reinterpret_cast<const f16x8*>(src);
                 alo[t] = *reinterpret_cast<const f16x8*>(src + 32);
-                if (QT == 3) sv[t] = *reinterpret_cast<const f32x4*>(sl + h * BN + (wn * TT + t) * 16 + 4 * g);
+                if (QT == 3) sv[t] = *reinterpret_cast<const f32x4*>(sl + h * BN + t * 16 + 4 * g);
             }
+            WFrag f[RT];
 #pragma unroll
             for (int r = 0; r < RT; ++r) {
-                WFrag f;
-                lds_wfrag<QT>(wl, (wm * RT + r) * 16 + i16, g, h, f, mask, magic);
+                WFrag f0, f1;
+                decode_pair<QT>(wrd[r], f0, f1, mask, magic);
+                f[r] = h ? f1 : f0;
+            }
+            f32x4 blk[RT][TT];
 #pragma unroll
-                for (int t = 0; t < TT; ++t) {
-                    f32x4 blk = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[t], f.b, zero, 0, 0, 0);
-                    blk = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[t], f.b, blk, 0, 0, 0);
+            for (int r = 0; r < RT; ++r)
+#pragma unroll
+                for (int t = 0; t < TT; ++t) blk[r][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[t], f[r].b, zero, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < RT; ++r)
+#pragma unroll
+                for (int t = 0; t < TT; ++t)
+                    blk[r][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[t], f[r].b, blk[r][t], 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < RT; ++r)
+#pragma unroll
+                for (int t = 0; t < TT; ++t)
 #pragma unroll
                     for (int qq = 0; qq < 4; ++qq) {
-                        acc[r][t][qq] = __builtin_fmaf(f.d, blk[qq], acc[r][t][qq]);
-                        if (QT == 3) acc[r][t][qq] = __builtin_fmaf(f.m, sv[t][qq], acc[r][t][qq]);
+                        acc[r][t][qq] = __builtin_fmaf(f[r].d, blk[r][t][qq], acc[r][t][qq]);
+                        if (QT == 3) acc[r][t][qq] = __builtin_fmaf(f[r].m, sv[t][qq], acc[r][t][qq]);
                     }
-                }
-            }
         }
+        request(min(q + D, plast), wrd, xrd, srd);
     };
-
-    // Steady state: every step refills its set (no conditional loads).
-    int q = p0;
-    for (; q + 2 * D <= p1; q += D) {
+    // Full groups of D pairs without branches (so the compiler counts the
+    // in-flight loads exactly), then the remaining pairs.
+    int q0 = p0;
+    for (; q0 + D <= p1; q0 += D) {
 #pragma unroll
-        for (int d = 0; d < D; ++d) step(q + d, wr[d], xr[d], sr[d], true);
-    }
-    // Drain: the remaining pairs (at most 2D - 1) refill only while pairs remain.
-#pragma unroll
-    for (int d = 0; d < D; ++d) {
-        if (q + d < p1) step(q + d, wr[d], xr[d], sr[d], q + d + D < p1);
+        for (int d = 0; d < D; ++d) step(q0 + d, wr[d], xr[d], sr[d]);
     }
 #pragma unroll
     for (int d = 0; d < D; ++d) {
-        if (q + D + d < p1) step(q + D + d, wr[d], xr[d], sr[d], false);
+        if (q0 + d < p1) step(q0 + d, wr[d], xr[d], sr[d]);
     }
     __syncthreads();
 
@@ -527,12 +450,12 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_tile_kernel(
         for (int t = 0; t < TT; ++t) {
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                const int n = n_base + (wn * TT + t) * 16 + 4 * g + q;
+                const int n = n_base + t * 16 + 4 * g + q;
                 if (n >= N) continue;
                 const float sn = scale[n];
 #pragma unroll
                 for (int r = 0; r < RT; ++r) {
-                    const int m = m_base + (wm * RT + r) * 16 + i16;
+                    const int m = m_base + (wave * RT + r) * 16 + i16;
                     if (m < M) y[static_cast<size_t>(n) * M + m] = acc[r][t][q] * sn;
                 }
             }
@@ -547,10 +470,10 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_tile_kernel(
     for (int t = 0; t < TT; ++t) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            const int n = n_base + (wn * TT + t) * 16 + 4 * g + q;
+            const int n = n_base + t * 16 + 4 * g + q;
 #pragma unroll
             for (int r = 0; r < RT; ++r) {
-                const int m = m_base + (wm * RT + r) * 16 + i16;
+                const int m = m_base + (wave * RT + r) * 16 + i16;
                 if (n < N && m < M) {
                     __hip_atomic_store(part + (static_cast<size_t>(blockIdx.z) * npad + n) * M + m, acc[r][t][q],
                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -568,102 +491,83 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_tile_kernel(
     }
     __syncthreads();
     if (last == 0u) return;
-    // Every thread sums E tile elements over the splits in split order, with
-    // all loads of four splits in flight at once (the loads bypass stale
-    // caches, so each is a memory round trip).
+    // Every thread sums its tile elements over the splits in split order, eight
+    // elements at a time with the loads of four splits in flight (each load is
+    // a round trip to the point of coherence).
     constexpr int E = (BM * BN) / kGemmThreads;
-    static_assert((BM * BN) % kGemmThreads == 0, "tile must be a multiple of the workgroup");
-    float sum[E];
-    size_t off[E];
-#pragma unroll
-    for (int i = 0; i < E; ++i) {
-        const int e = threadIdx.x + i * kGemmThreads;
-        const int n = min(n_base + e / BM, N - 1);  // clamped; out-of-range results are not stored
-        const int m = min(m_base + e % BM, M - 1);
-        off[i] = static_cast<size_t>(n) * M + m;
-        sum[i] = 0.0f;
-    }
+    constexpr int EC = E < 8 ? E : 8;
+    static_assert((BM * BN) % kGemmThreads == 0 && E % EC == 0, "tile must divide the workgroup");
     const size_t zstride = static_cast<size_t>(npad) * M;
     const unsigned S = gridDim.z;
-    unsigned k = 0;
-    for (; k + 4 <= S; k += 4) {
-        float v[4][E];
+    for (int i0 = 0; i0 < E; i0 += EC) {
+        float sum[EC];
+        size_t off[EC];
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
+        for (int i = 0; i < EC; ++i) {
+            const int e = threadIdx.x + (i0 + i) * kGemmThreads;
+            const int n = min(n_base + e / BM, N - 1);  // clamped; out-of-range results are not stored
+            const int m = min(m_base + e % BM, M - 1);
+            off[i] = static_cast<size_t>(n) * M + m;
+            sum[i] = 0.0f;
+        }
+        unsigned k = 0;
+        for (; k + 4 <= S; k += 4) {
+            float v[4][EC];
 #pragma unroll
-            for (int i = 0; i < E; ++i)
-                v[u][i] = __hip_atomic_load(part + (k + u) * zstride + off[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            for (int u = 0; u < 4; ++u)
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
+                for (int i = 0; i < EC; ++i)
+                    v[u][i] = __hip_atomic_load(part + (k + u) * zstride + off[i], __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
 #pragma unroll
-            for (int i = 0; i < E; ++i) sum[i] += v[u][i];
-    }
-    for (; k < S; ++k) {
+            for (int u = 0; u < 4; ++u)
 #pragma unroll
-        for (int i = 0; i < E; ++i)
-            sum[i] += __hip_atomic_load(part + k * zstride + off[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+                for (int i = 0; i < EC; ++i) sum[i] += v[u][i];
+        }
+        for (; k < S; ++k) {
 #pragma unroll
-    for (int i = 0; i < E; ++i) {
-        const int e = threadIdx.x + i * kGemmThreads;
-        const int n = n_base + e / BM;
-        const int m = m_base + e % BM;
-        if (n < N && m < M) y[static_cast<size_t>(n) * M + m] = sum[i] * scale[n];
+            for (int i = 0; i < EC; ++i)
+                sum[i] += __hip_atomic_load(part + k * zstride + off[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+#pragma unroll
+        for (int i = 0; i < EC; ++i) {
+            const int e = threadIdx.x + (i0 + i) * kGemmThreads;
+            const int n = n_base + e / BM;
+            const int m = m_base + e % BM;
+            if (n < N && m < M) y[static_cast<size_t>(n) * M + m] = sum[i] * scale[n];
+        }
     }
     if (threadIdx.x == 0) __hip_atomic_store(tile_count + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---------------------------------------------------------------------------
-// Tile configurations: skinny N (decode-like batches) streams each weight
-// byte once with one 16-row tile per wave; wide N (prefill) gives each wave
-// 64 rows x 32 tokens so decoded weight fragments and x fragments are reused
-// across several MFMAs.  K is split across workgroups until the grid covers
-// the CUs (partials reduced in a fixed order).
-enum class Tile { N16, N32, N64, Wide };
-
-// Pairs in flight per workgroup (register sets of the load pipeline).
-constexpr int kDepthN16 = 4;
-constexpr int kDepthN32 = 4;
-constexpr int kDepthN64 = 4;
-constexpr int kDepthWide = 2;
-
+// Configurations: rows per wave (RT) and token tiles (TT) by batch size.  K is
+// split across workgroups until the grid gives every CU a few workgroups,
+// keeping at least eight pairs per split.
 struct GemmCfg {
-    Tile tile;
-    int bm, bn, splits, pairs_per_split, npad, lds;
+    int rt, tt, bm, bn, splits, pairs_per_split, npad, lds;
 };
-
-template <int QT>
-int tile_lds(Tile t) {
-    switch (t) {
-        case Tile::N16: return TileLds<QT, 64, 16>::bytes;
-        case Tile::N32: return TileLds<QT, 64, 32>::bytes;
-        case Tile::N64: return TileLds<QT, 64, 64>::bytes;
-        default: return TileLds<QT, 128, 64>::bytes;
-    }
-}
 
 GemmCfg choose(const LinearShape& s) {
     GemmCfg c;
     if (s.rows <= 16) {
-        c.tile = Tile::N16, c.bm = 64, c.bn = 16;
+        c.rt = 1, c.tt = 1;
     } else if (s.rows <= 32) {
-        c.tile = Tile::N32, c.bm = 64, c.bn = 32;
+        c.rt = 1, c.tt = 2;
     } else if (s.rows <= 64) {
-        c.tile = Tile::N64, c.bm = 64, c.bn = 64;
+        c.rt = 1, c.tt = 4;
     } else {
-        c.tile = Tile::Wide, c.bm = 128, c.bn = 64;
+        c.rt = 2, c.tt = 4;
     }
-    c.lds = s.qtype == 1 ? tile_lds<1>(c.tile) : s.qtype == 2 ? tile_lds<2>(c.tile) : tile_lds<3>(c.tile);
+    c.bm = 64 * c.rt;
+    c.bn = 16 * c.tt;
+    c.lds = c.tt == 1 ? StreamLds<1>::bytes : c.tt == 2 ? StreamLds<2>::bytes : StreamLds<4>::bytes;
     c.npad = (s.rows + c.bn - 1) / c.bn * c.bn;
     const int np = s.nb / 2;
     const long long tiles = static_cast<long long>((s.M + c.bm - 1) / c.bm) * (c.npad / c.bn);
-    // About one workgroup per CU (two for the narrow tiles), and at least two
-    // prefetch depths of pairs per split so each workgroup's pipeline fills.
-    const int depth = c.tile == Tile::N16 ? kDepthN16 : c.tile == Tile::N32 ? kDepthN32
-                    : c.tile == Tile::N64 ? kDepthN64 : kDepthWide;
-    const long long target = c.tile == Tile::Wide ? 256 : 512;
+    const long long target = c.rt == 1 ? 1024 : 512;
     int splits = static_cast<int>((target + tiles - 1) / tiles);
-    splits = max(1, min(splits, np / (2 * depth)));
+    splits = max(1, min(splits, np / 8));
     if (tiles > kGemmMaxTiles) splits = 1;
     c.pairs_per_split = (np + splits - 1) / splits;
     c.splits = (np + c.pairs_per_split - 1) / c.pairs_per_split;
@@ -671,7 +575,7 @@ GemmCfg choose(const LinearShape& s) {
 }
 
 struct WsLayout {
-    size_t xs, bsum, scale, count, part, total;
+    size_t count, xs, bsum, scale, part, total;
 };
 
 // The split-K arrival counters sit at the start of every layout: all shapes
@@ -688,7 +592,7 @@ WsLayout layout(const LinearShape& s, const GemmCfg& c) {
     return l;
 }
 
-template <int QT, int BM, int BN, int WM, int WN, int D>
+template <int QT, int RT, int TT>
 hipError_t launch_t(const LinearShape& s, const GemmCfg& c, const WsLayout& l, const void* w,
                     const float* x, float* y, char* ws, hipStream_t stream) {
     _Float16* xs = reinterpret_cast<_Float16*>(ws + l.xs);
@@ -698,9 +602,9 @@ hipError_t launch_t(const LinearShape& s, const GemmCfg& c, const WsLayout& l, c
     unsigned* count = reinterpret_cast<unsigned*>(ws + l.count);
     hipLaunchKernelGGL((xsplit_kernel<QT>), dim3(c.npad), dim3(256), 0, stream, x, s.rows, s.K, s.nb,
                        c.npad, xs, bsum, scale);
-    dim3 grid((s.M + BM - 1) / BM, c.npad / BN, c.splits);
-    constexpr int lds = TileLds<QT, BM, BN>::bytes;
-    hipLaunchKernelGGL((gemm_tile_kernel<QT, BM, BN, WM, WN, D>), grid, dim3(kGemmThreads), lds, stream,
+    dim3 grid((s.M + 64 * RT - 1) / (64 * RT), c.npad / (16 * TT), c.splits);
+    constexpr int lds = StreamLds<TT>::bytes;
+    hipLaunchKernelGGL((gemm_stream_kernel<QT, RT, TT, (RT == 1 ? 4 : 2)>), grid, dim3(kGemmThreads), lds, stream,
                        static_cast<const uint8_t*>(w), xs, bsum, scale, y, part, count, s.M, s.rows, c.npad,
                        s.nb, c.pairs_per_split);
     return hipGetLastError();
@@ -709,11 +613,11 @@ hipError_t launch_t(const LinearShape& s, const GemmCfg& c, const WsLayout& l, c
 template <int QT>
 hipError_t launch_q(const LinearShape& s, const GemmCfg& c, const WsLayout& l, const void* w,
                     const float* x, float* y, char* ws, hipStream_t stream) {
-    switch (c.tile) {
-        case Tile::N16: return launch_t<QT, 64, 16, 4, 1, kDepthN16>(s, c, l, w, x, y, ws, stream);
-        case Tile::N32: return launch_t<QT, 64, 32, 4, 1, kDepthN32>(s, c, l, w, x, y, ws, stream);
-        case Tile::N64: return launch_t<QT, 64, 64, 4, 1, kDepthN64>(s, c, l, w, x, y, ws, stream);
-        default: return launch_t<QT, 128, 64, 2, 2, kDepthWide>(s, c, l, w, x, y, ws, stream);
+    if (c.rt == 2) return launch_t<QT, 2, 4>(s, c, l, w, x, y, ws, stream);
+    switch (c.tt) {
+        case 1: return launch_t<QT, 1, 1>(s, c, l, w, x, y, ws, stream);
+        case 2: return launch_t<QT, 1, 2>(s, c, l, w, x, y, ws, stream);
+        default: return launch_t<QT, 1, 4>(s, c, l, w, x, y, ws, stream);
     }
 }
 
@@ -746,7 +650,7 @@ const char* gemm_kernel_name(const LinearShape& s) {
     static thread_local char buf[96];
     const GemmCfg c = choose(s);
     const char* fmt = s.qtype == 1 ? "q8_0" : s.qtype == 2 ? "q4_0" : "q4_1";
-    snprintf(buf, sizeof buf, "gemm_tile_%s_bm%d_bn%d_splitk%d", fmt, c.bm, c.bn, c.splits);
+    snprintf(buf, sizeof buf, "gemm_mfma_%s_bm%d_bn%d_splitk%d", fmt, c.bm, c.bn, c.splits);
     return buf;
 }
 

@@ -68,4 +68,4 @@ def test_kernel_selection_names():
     assert mlq_hip.kernel_name(mlq_hip.Q4_0, 1, 896, 4864) == "gemv_multi_q4_0_lpr16"
     assert mlq_hip.kernel_name(mlq_hip.Q4_1, 1, 151936, 896) == "gemv_single_q4_1_lpr16_r1"
     assert mlq_hip.kernel_name(mlq_hip.Q4_0, 1, 5, 13) == "gemv_generic_q4_0"
-    assert mlq_hip.kernel_name(mlq_hip.Q4_0, 64, 4096, 4096).startswith("gemm_tile_q4_0")
+    assert mlq_hip.kernel_name(mlq_hip.Q4_0, 64, 4096, 4096).startswith("gemm_mfma_q4_0")

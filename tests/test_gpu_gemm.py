@@ -41,7 +41,7 @@ def run(hip, orc, qt, m, k, n, seed=0, scale_rows=None):
 def test_gemm_baseline_config4(hip, orc, shape, n):
     for fmt in ("q8_0", "q4_0"):
         name, _ = run(hip, orc, FMTS[fmt], *shape, n)
-        assert name.startswith("gemm_tile"), name
+        assert name.startswith("gemm_mfma"), name
 
 
 @pytest.mark.parametrize("m,k,n", [(4096, 4096, 16), (64, 64, 2), (33, 4096, 17), (300, 896, 40),
