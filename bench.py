@@ -300,6 +300,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline / parity leg")
     ap.add_argument("--no-shapes", action="store_true", help="skip the per-shape GEMV / GEMM tables")
     ap.add_argument("--layers", type=int, default=32)
+    ap.add_argument("--no-variants", action="store_true",
+                    help="time only the --launch mode (for profiling one mode's kernels)")
     ap.add_argument("--calibration-copy-mb", type=int, default=0,
                     help="before timing, run one device-to-device copy of this many MiB: a kernel of "
                          "known traffic that scales the rocprofv3 FETCH_SIZE / WRITE_SIZE counters")
@@ -348,6 +350,8 @@ def main():
     }
     variants = {}
     for name, fn in steps_by_mode.items():
+        if args.no_variants and name != args.launch:
+            continue
         for _ in range(args.warmup):
             fn()
         hip.synchronize(stream)
