@@ -36,6 +36,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdint>
 #include <cstdio>
 
@@ -541,6 +542,476 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_stream_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// Chunked MFMA kernel.
+//
+// A workgroup of four waves owns BM = 64 * RW weight rows x BN = 16 * TT
+// tokens and a contiguous range of K chunks (4 blocks = 128 k each); the grid
+// is about one wave of workgroups (two per CU), so each workgroup streams a
+// long run of chunks through a pipeline instead of paying a memory latency per
+// step.  Per chunk:
+//  * weights: each wave reads its own rows' chunk (RW * 16 rows x 4 blocks)
+//    with coalesced 8-byte loads, P chunks ahead, into registers, and parks it
+//    in a wave-private LDS buffer; MFMA B fragments are read back from there.
+//  * x, one chunk ahead, into a shared LDS buffer of A fragments (slot order
+//    of the weight codes), from one of two sources:
+//    XS: the x split by xsplit_kernel (per-token power-of-two scale, fp16 hi +
+//        lo in fragment order, Q4_1 block sums): a plain copy;
+//    !XS: the f32 x itself (small batches, where a second launch would cost
+//        more than the split): the workgroup picks a power-of-two scale per
+//        (token, chunk) that puts the chunk's max|x| in [2^13, 2^14) and
+//        splits every scaled element into fp16 hi + lo.
+//  * MFMAs: per block, hi then lo into a zeroed tile, then the block scale
+//    d (+ m * sum(x') for Q4_1) times the tile into the accumulator (!XS: into
+//    a chunk accumulator that is scaled back by the chunk's inverse scale).
+// K is split across workgroups only when the tiles alone would not fill the
+// CUs; the splits of a tile are adjacent in launch order.  Each split stores
+// its partial tile with write-through stores and counts in; the workgroup
+// that completes the count adds the partials in split order (deterministic),
+// applies the token scale and writes y.  Needs nb % 4 == 0 (8-byte aligned
+// chunk rows), K == 32 nb and (!XS) a 16-byte aligned x.
+constexpr int kChunkBlocks = 4;
+
+template <int QT> struct ChunkFmt;
+template <> struct ChunkFmt<1> { static constexpr int BB = 34, U = 17, WROW = 136; };  // U: 8-byte units per row
+template <> struct ChunkFmt<2> { static constexpr int BB = 18, U = 9, WROW = 72; };
+template <> struct ChunkFmt<3> { static constexpr int BB = 20, U = 10, WROW = 80; };
+
+template <int QT, int RW, int TT, bool XS>
+struct ChunkLds {
+    static constexpr int BN = 16 * TT;
+    static constexpr int w_wave = RW * 16 * ChunkFmt<QT>::WROW;  // one buffer of one wave
+    static constexpr int w_bytes = 2 * 4 * w_wave;                 // [buffer][wave][row][WROW]
+    static constexpr int x_halves = kChunkBlocks * BN * kXRowHalves;  // [block][token][72]
+    // + (!XS) inverse scales [BN] + (Q4_1) block sums [block][BN]
+    static constexpr int sums_off = x_halves * 2 + (XS ? 0 : BN * 4);
+    static constexpr int x_buf = sums_off + (QT == 3 ? kChunkBlocks * BN * 4 : 0);
+    static constexpr int bytes = w_bytes + 2 * x_buf;
+};
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), static_cast<int>(bytes),
+                                             0x00020000);
+}
+constexpr int kCoherent = 16;  // sc1: write through / read from the point of coherence (agent scope)
+
+struct ChunkArgs {
+    const uint8_t* W;
+    const float* x;         // !XS: f32 x [N][K]
+    const _Float16* xs;     // XS: split x [nb][npad][64]
+    const float* bsum;      // XS, Q4_1: [nb][npad]
+    const float* xscale;    // XS: [npad]
+    float* y;
+    float* part;
+    uint32_t part_bytes;
+    unsigned* tile_count;
+    int M, N, K, nb, npad, row_tiles, splits, chunks_per_split;
+};
+
+template <int QT, int RW, int TT, int P, bool XS>
+__global__ __launch_bounds__(kGemmThreads) void gemm_chunk_kernel(const ChunkArgs a) {
+    using L = ChunkLds<QT, RW, TT, XS>;
+    using F = ChunkFmt<QT>;
+    constexpr int BN = L::BN;
+    constexpr int TPT = kGemmThreads / BN;  // !XS: x-split threads per token
+    constexpr int EPT = 128 / TPT;          // !XS: elements per thread per chunk (8, 16 or 32)
+    constexpr int XU = kChunkBlocks * BN * 8 / kGemmThreads;  // XS: 16-byte x units per thread per chunk
+    constexpr int XR = XS ? XU : EPT / 4;   // x registers (float4 / 16-byte units) per thread
+    constexpr int WU = RW * 16 * F::U;      // weight units per wave per chunk
+    constexpr int NWL = (WU + 63) / 64;     // weight loads per lane per chunk
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int i16 = lane & 15;
+    const int g = lane >> 4;
+    const int wg = blockIdx.x;
+    const int split = wg % a.splits;
+    const int tile = wg / a.splits;
+    const int m_base = (tile % a.row_tiles) * (64 * RW);
+    const int n_base = (tile / a.row_tiles) * BN;
+    const int M = a.M, N = a.N, nb = a.nb;
+    const int nchunk_all = nb / kChunkBlocks;
+    const int c0 = split * a.chunks_per_split;
+    const int nchunk = min(nchunk_all, c0 + a.chunks_per_split) - c0;
+
+    uint32_t mask = 0x000F000Fu, magic = 0x64006400u;
+    asm volatile("" : "+v"(mask), "+v"(magic));
+
+    // Weight units of this lane: unit u = lane + 64 i -> (row u / U, 8-byte
+    // column u % U); 32-bit offsets from the split's first chunk (the host
+    // keeps a weight below 4 GiB on this path).  Loads are unconditional
+    // (lanes past the wave's units re-read its last unit, tokens past N read
+    // token 0 and are zeroed) so that no branch forces an early wait; only
+    // the LDS store is predicated.
+    const uint8_t* wsplit = a.W + static_cast<size_t>(c0) * kChunkBlocks * F::BB;
+    uint32_t goff[NWL];
+    int loff[NWL];
+#pragma unroll
+    for (int i = 0; i < NWL; ++i) {
+        const int u = min(lane + 64 * i, WU - 1);
+        const int rl = u / F::U;
+        const int col = u % F::U;
+        const int row = min(m_base + wave * RW * 16 + rl, M - 1);
+        goff[i] = static_cast<uint32_t>(row) * static_cast<uint32_t>(nb * F::BB) + col * 8;
+        loff[i] = rl * F::WROW + col * 8;
+    }
+    const bool last_ok = lane + 64 * (NWL - 1) < WU;  // the last load is partial when 64 does not divide WU
+    constexpr size_t kChunkBytes = static_cast<size_t>(kChunkBlocks) * F::BB;
+
+    // !XS: x slice of this thread: token tok, elements e0 .. e0 + EPT - 1 of the chunk.
+    const int tok = tid / TPT;
+    const int e0 = (tid % TPT) * EPT;
+    const bool tok_ok = n_base + tok < N;
+    const float* xrow = XS ? nullptr
+                           : a.x + static_cast<size_t>(tok_ok ? n_base + tok : 0) * a.K +
+                                 static_cast<size_t>(c0) * 128 + e0;
+    // XS: unit v = tid + 256 i -> (block j, token, 16-byte column q) of the chunk.
+    uint32_t xoff[XS ? XU : 1];
+    int xl_off[XS ? XU : 1];
+    if (XS) {
+#pragma unroll
+        for (int i = 0; i < XU; ++i) {
+            const int v = tid + kGemmThreads * i;
+            const int j = v / (BN * 8);
+            const int tk = (v / 8) % BN;
+            const int q = v % 8;
+            xoff[i] = (static_cast<uint32_t>(j) * a.npad + n_base + tk) * 64 + 8 * q;  // halves, from the chunk's block 0
+            xl_off[i] = ((j * BN + tk) * kXRowHalves + 8 * q) * 2;                      // bytes
+        }
+    }
+    const bool sum_lane = XS && QT == 3 && tid < kChunkBlocks * BN;
+
+    uint2 wreg[P][NWL];
+    u32x4 xreg[XR];
+    float sreg = 0.0f;
+    auto load_w = [&](int c, uint2 (&wr)[NWL]) {
+        const uint8_t* wc = wsplit + static_cast<size_t>(c) * kChunkBytes;
+#pragma unroll
+        for (int i = 0; i < NWL; ++i) wr[i] = *reinterpret_cast<const uint2*>(wc + goff[i]);
+    };
+    auto store_w = [&](const uint2 (&wr)[NWL], int buf) {
+        char* base = smem + (buf * 4 + wave) * L::w_wave;
+#pragma unroll
+        for (int i = 0; i < NWL; ++i) {
+            if (i < NWL - 1 || last_ok) *reinterpret_cast<uint2*>(base + loff[i]) = wr[i];
+        }
+    };
+    auto load_x = [&](int c) {
+        if (XS) {
+            const int b = (c0 + c) * kChunkBlocks;
+            const _Float16* src = a.xs + static_cast<size_t>(b) * a.npad * 64;
+#pragma unroll
+            for (int i = 0; i < XU; ++i) xreg[i] = *reinterpret_cast<const u32x4*>(src + xoff[i]);
+            if (QT == 3) {
+                const int t = sum_lane ? tid : 0;
+                sreg = a.bsum[static_cast<size_t>(b + t / BN) * a.npad + n_base + t % BN];
+            }
+        } else {
+            const u32x4* src = reinterpret_cast<const u32x4*>(xrow + static_cast<size_t>(c) * 128);
+#pragma unroll
+            for (int i = 0; i < XR; ++i) xreg[i] = src[i];
+        }
+    };
+    auto put_x = [&](int buf) {
+        char* xb = smem + L::w_bytes + buf * L::x_buf;
+        if (XS) {
+#pragma unroll
+            for (int i = 0; i < XU; ++i) *reinterpret_cast<u32x4*>(xb + xl_off[i]) = xreg[i];
+            if (sum_lane) reinterpret_cast<float*>(xb + L::sums_off)[tid] = sreg;
+            return;
+        }
+        _Float16* xl = reinterpret_cast<_Float16*>(xb);
+        float* sl = reinterpret_cast<float*>(xb + L::x_halves * 2);
+        float v[EPT];
+#pragma unroll
+        for (int i = 0; i < XR; ++i) {
+            const f32x4 f = __builtin_bit_cast(f32x4, xreg[i]);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) v[4 * i + k] = tok_ok ? f[k] : 0.0f;
+        }
+        float mx = 0.0f;
+#pragma unroll
+        for (int i = 0; i < EPT; ++i) mx = fmaxf(mx, fabsf(v[i]));
+#pragma unroll
+        for (int o = 1; o < TPT; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+        float inv = 1.0f, sinv = 1.0f;
+        if (mx > 0.0f && mx <= 3.0e38f) {
+            int ex = 0;
+            (void)frexpf(mx, &ex);  // mx in [2^(ex-1), 2^ex)
+            const int e = min(126, max(-126, 14 - ex));
+            inv = ldexpf(1.0f, e);
+            sinv = ldexpf(1.0f, -e);
+        }
+        if (tid % TPT == 0) sl[tok] = sinv;
+#pragma unroll
+        for (int i = 0; i < EPT; ++i) v[i] *= inv;
+        const int j = e0 >> 5;  // block within the chunk
+        const int o = e0 & 31;  // first element within the block
+        if (QT == 3) {
+            float sum = 0.0f;
+#pragma unroll
+            for (int q = 0; q < EPT / 4; ++q) sum += (v[4 * q] + v[4 * q + 1]) + (v[4 * q + 2] + v[4 * q + 3]);
+#pragma unroll
+            for (int w = 1; w < 32 / EPT; w <<= 1) sum += __shfl_xor(sum, w, 64);
+            if (o == 0) reinterpret_cast<float*>(xb + L::sums_off)[j * BN + tok] = sum;
+        }
+        _Float16* row = xl + (j * BN + tok) * kXRowHalves;
+        typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+        for (int q = 0; q < EPT / 4; ++q) {
+            const int e = o + 4 * q;
+            float a0, a1, a2, a3;
+            int slot;
+            if (QT == 1) {
+                slot = e;
+                a0 = v[4 * q], a1 = v[4 * q + 1], a2 = v[4 * q + 2], a3 = v[4 * q + 3];
+            } else {
+                slot = 8 * ((e & 15) >> 2) + 4 * (e >> 4);
+                a0 = v[4 * q], a1 = v[4 * q + 2], a2 = v[4 * q + 1], a3 = v[4 * q + 3];
+            }
+            const _Float16 h0 = static_cast<_Float16>(a0), h1 = static_cast<_Float16>(a1);
+            const _Float16 h2 = static_cast<_Float16>(a2), h3 = static_cast<_Float16>(a3);
+            *reinterpret_cast<f16x4*>(row + slot) = f16x4{h0, h1, h2, h3};
+            *reinterpret_cast<f16x4*>(row + 32 + slot) =
+                f16x4{static_cast<_Float16>(a0 - static_cast<float>(h0)), static_cast<_Float16>(a1 - static_cast<float>(h1)),
+                      static_cast<_Float16>(a2 - static_cast<float>(h2)), static_cast<_Float16>(a3 - static_cast<float>(h3))};
+        }
+    };
+
+    f32x4 acc[RW][TT];
+#pragma unroll
+    for (int r = 0; r < RW; ++r)
+#pragma unroll
+        for (int t = 0; t < TT; ++t) acc[r][t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    const f32x4 zero{0.0f, 0.0f, 0.0f, 0.0f};
+
+    // Per block: all RW x TT tiles get their two MFMAs (hi, lo) from zero;
+    // the scale epilogue of a block runs while the next block's MFMAs are in
+    // flight, so no VALU op waits on a fresh MFMA result.
+    auto compute = [&](int buf) {
+        const char* wb = smem + (buf * 4 + wave) * L::w_wave;
+        const char* xb = smem + L::w_bytes + buf * L::x_buf;
+        const _Float16* xl = reinterpret_cast<const _Float16*>(xb);
+        const float* ssum = reinterpret_cast<const float*>(xb + L::sums_off);
+        f32x4 cacc[XS ? 1 : RW][XS ? 1 : TT];
+        f32x4 bprev[RW][TT];
+        float dprev[RW], mprev[RW];
+        f32x4 svprev[TT];
+        auto epilogue = [&](int jb) {
+#pragma unroll
+            for (int r = 0; r < RW; ++r)
+#pragma unroll
+                for (int t = 0; t < TT; ++t)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        if (XS) {
+                            float v = __builtin_fmaf(dprev[r], bprev[r][t][q], acc[r][t][q]);
+                            if (QT == 3) v = __builtin_fmaf(mprev[r], svprev[t][q], v);
+                            acc[r][t][q] = v;
+                        } else {
+                            float v = jb == 0 ? dprev[r] * bprev[r][t][q]
+                                              : __builtin_fmaf(dprev[r], bprev[r][t][q], cacc[r][t][q]);
+                            if (QT == 3) v = __builtin_fmaf(mprev[r], svprev[t][q], v);
+                            cacc[r][t][q] = v;
+                        }
+                    }
+        };
+#pragma unroll
+        for (int p = 0; p < kChunkBlocks / 2; ++p) {
+            uint32_t wr[RW][7];
+#pragma unroll
+            for (int r = 0; r < RW; ++r)
+                load_pair<QT>(reinterpret_cast<const uint32_t*>(wb + (r * 16 + i16) * F::WROW + p * 2 * F::BB), g, wr[r]);
+            WFrag f0[RW], f1[RW];
+#pragma unroll
+            for (int r = 0; r < RW; ++r) decode_pair<QT>(wr[r], f0[r], f1[r], mask, magic);
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int j = 2 * p + h;
+                f16x8 ahi[TT], alo[TT];
+                f32x4 sv[TT];
+#pragma unroll
+                for (int t = 0; t < TT; ++t) {
+                    const _Float16* src = xl + (j * BN + t * 16 + i16) * kXRowHalves + 8 * g;
+                    ahi[t] = *reinterpret_cast<const f16x8*>(src);
+                    alo[t] = *reinterpret_cast<const f16x8*>(src + 32);
+                    if (QT == 3) sv[t] = *reinterpret_cast<const f32x4*>(ssum + j * BN + t * 16 + 4 * g);
+                }
+                f32x4 bcur[RW][TT];
+#pragma unroll
+                for (int r = 0; r < RW; ++r)
+#pragma unroll
+                    for (int t = 0; t < TT; ++t)
+                        bcur[r][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[t], (h ? f1[r] : f0[r]).b, zero, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < RW; ++r)
+#pragma unroll
+                    for (int t = 0; t < TT; ++t)
+                        bcur[r][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[t], (h ? f1[r] : f0[r]).b, bcur[r][t], 0, 0, 0);
+                if (j > 0) epilogue(j - 1);
+#pragma unroll
+                for (int r = 0; r < RW; ++r) {
+                    const WFrag& f = h ? f1[r] : f0[r];
+                    dprev[r] = f.d;
+                    mprev[r] = f.m;
+#pragma unroll
+                    for (int t = 0; t < TT; ++t) bprev[r][t] = bcur[r][t];
+                }
+#pragma unroll
+                for (int t = 0; t < TT; ++t) svprev[t] = sv[t];
+            }
+        }
+        epilogue(kChunkBlocks - 1);
+        if (!XS) {
+            const float* sl = reinterpret_cast<const float*>(xb + L::x_halves * 2);
+#pragma unroll
+            for (int t = 0; t < TT; ++t) {
+                const f32x4 s4 = *reinterpret_cast<const f32x4*>(sl + t * 16 + 4 * g);
+#pragma unroll
+                for (int r = 0; r < RW; ++r)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        acc[r][t][q] = __builtin_fmaf(s4[q], cacc[XS ? 0 : r][XS ? 0 : t][q], acc[r][t][q]);
+            }
+        }
+    };
+
+    // Pipeline.  Register set k % P holds weight chunk k; at step c the set of
+    // chunk c + 1 goes to LDS buffer (c + 1) & 1 and is refilled with chunk
+    // c + 1 + P; x chunk c + 1 (loaded one step earlier) goes to its buffer
+    // and chunk c + 2 is requested; then chunk c is computed.  The barrier at
+    // the end of step c publishes buffer (c + 1) & 1 and frees buffer c & 1.
+    // Memory counters drain in issue order, so each step requests x (needed
+    // next step) before the weights (needed P steps later), with a scheduling
+    // barrier between them: waiting for x then leaves the weight prefetch in
+    // flight.  Requests past the last chunk re-read the last chunk (L2 hits),
+    // so that every load is unconditional and can be counted exactly.
+    const int clast = nchunk - 1;
+    load_w(0, wreg[0]);
+#pragma unroll
+    for (int k = 1; k < P; ++k) load_w(min(k, clast), wreg[k]);
+    load_x(0);
+    store_w(wreg[0], 0);
+    put_x(0);
+    load_x(min(1, clast));
+    __builtin_amdgcn_sched_barrier(0);
+    load_w(min(P, clast), wreg[0]);
+    __syncthreads();
+    // Full groups of P steps without branches, then the last steps, which
+    // request nothing new except x.
+    int cb = 0;
+    for (; cb + P < nchunk; cb += P) {
+#pragma unroll
+        for (int u = 0; u < P; ++u) {
+            const int c = cb + u;
+            store_w(wreg[(u + 1) % P], (c + 1) & 1);
+            put_x((c + 1) & 1);
+            load_x(min(c + 2, clast));
+            __builtin_amdgcn_sched_barrier(0);
+            load_w(min(c + 1 + P, clast), wreg[(u + 1) % P]);
+            compute(c & 1);
+            __syncthreads();
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < P; ++u) {
+        const int c = cb + u;
+        if (c < nchunk) {
+            if (c + 1 < nchunk) {
+                store_w(wreg[(u + 1) % P], (c + 1) & 1);
+                put_x((c + 1) & 1);
+                if (c + 2 < nchunk) load_x(c + 2);
+            }
+            compute(c & 1);
+            __syncthreads();
+        }
+    }
+
+    // Token scale of output element q of token tile t (XS: the x split's
+    // per-token scale; !XS: already applied per chunk).
+    auto tok_scale = [&](int t, int q) {
+        if (!XS) return 1.0f;
+        return a.xscale[n_base + t * 16 + 4 * g + q];
+    };
+    if (a.splits == 1) {
+#pragma unroll
+        for (int t = 0; t < TT; ++t)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int n = n_base + t * 16 + 4 * g + q;
+                if (n >= N) continue;
+                const float sn = tok_scale(t, q);
+#pragma unroll
+                for (int r = 0; r < RW; ++r) {
+                    const int m = m_base + (wave * RW + r) * 16 + i16;
+                    if (m < M) a.y[static_cast<size_t>(n) * M + m] = acc[r][t][q] * sn;
+                }
+            }
+        return;
+    }
+
+    // Split K: partial tile [tile][split][r][t][thread] as float4, write-through.
+    const __amdgpu_buffer_rsrc_t prs = make_rsrc(a.part, a.part_bytes);
+    const uint32_t tile_base = static_cast<uint32_t>(tile) * a.splits * (RW * TT * kGemmThreads * 16);
+    constexpr uint32_t split_stride = RW * TT * kGemmThreads * 16;
+#pragma unroll
+    for (int r = 0; r < RW; ++r)
+#pragma unroll
+        for (int t = 0; t < TT; ++t)
+            __builtin_amdgcn_raw_buffer_store_b128(
+                __builtin_bit_cast(u32x4, acc[r][t]), prs,
+                tile_base + split * split_stride + ((r * TT + t) * kGemmThreads + tid) * 16, 0, kCoherent);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __shared__ unsigned last;
+    __syncthreads();
+    if (tid == 0) {
+        const unsigned done = __hip_atomic_fetch_add(a.tile_count + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last = done == static_cast<unsigned>(a.splits) - 1 ? 1u : 0u;
+    }
+    __syncthreads();
+    if (last == 0u) return;
+    // Sum the splits in order: every (r, t) tile of up to kBatch splits is
+    // requested before any is added, so the sum costs about one round trip
+    // to the point of coherence per batch.
+    constexpr int RT4 = RW * TT;
+    constexpr int kBatch = RT4 <= 2 ? 16 : RT4 <= 4 ? 8 : 4;
+    f32x4 sum[RT4];
+#pragma unroll
+    for (int k = 0; k < RT4; ++k) sum[k] = zero;
+    for (int s0 = 0; s0 < a.splits; s0 += kBatch) {
+        f32x4 v[kBatch][RT4];
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b) {
+            const int s = min(s0 + b, a.splits - 1);
+#pragma unroll
+            for (int k = 0; k < RT4; ++k)
+                v[b][k] = __builtin_bit_cast(
+                    f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                               prs, tile_base + s * split_stride + (k * kGemmThreads + tid) * 16, 0, kCoherent));
+        }
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b)
+            if (s0 + b < a.splits) {
+#pragma unroll
+                for (int k = 0; k < RT4; ++k) sum[k] += v[b][k];
+            }
+    }
+#pragma unroll
+    for (int k = 0; k < RT4; ++k) {
+        const int r = k / TT;
+        const int t = k % TT;
+        const int m = m_base + (wave * RW + r) * 16 + i16;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int n = n_base + t * 16 + 4 * g + q;
+            if (n < N && m < M) a.y[static_cast<size_t>(n) * M + m] = sum[k][q] * tok_scale(t, q);
+        }
+    }
+    if (tid == 0) __hip_atomic_store(a.tile_count + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---------------------------------------------------------------------------
 // Configurations: rows per wave (RT) and token tiles (TT) by batch size.  K is
 // split across workgroups until the grid gives every CU a few workgroups,
 // keeping at least eight pairs per split.
@@ -621,6 +1092,106 @@ hipError_t launch_q(const LinearShape& s, const GemmCfg& c, const WsLayout& l, c
     }
 }
 
+// Chunked-kernel configuration: 128 rows per workgroup, 16 tokens per
+// workgroup for batches up to 16 (x split in the kernel) and 32 above (x split
+// by xsplit_kernel first), K split until the grid is about two workgroups per
+// CU.
+struct ChunkCfg {
+    int tt, row_tiles, tok_tiles, splits, cps, npad;
+    bool xs;
+};
+
+bool chunk_supported(const LinearShape& s) {
+    return s.rows > 1 && s.nb >= 8 && s.nb % kChunkBlocks == 0 && s.K == s.nb * kQK && s.qtype >= 1 && s.qtype <= 3;
+}
+
+ChunkCfg choose_chunk(const LinearShape& s) {
+    ChunkCfg c;
+    c.tt = s.rows <= 16 ? 1 : 2;
+    c.xs = c.tt > 1;
+    c.row_tiles = (s.M + 127) / 128;
+    c.tok_tiles = (s.rows + 16 * c.tt - 1) / (16 * c.tt);
+    c.npad = c.tok_tiles * 16 * c.tt;
+    const long long tiles = static_cast<long long>(c.row_tiles) * c.tok_tiles;
+    const int nchunks = s.nb / kChunkBlocks;
+    const long long target = 512;
+    int splits = static_cast<int>((target + tiles - 1) / tiles);
+    splits = std::max(1, std::min(splits, nchunks / 2));
+    if (tiles > kGemmMaxTiles) splits = 1;
+    c.cps = (nchunks + splits - 1) / splits;
+    c.splits = (nchunks + c.cps - 1) / c.cps;
+    return c;
+}
+
+// Workspace: [split-K counters][split x][block sums][token scales][partials].
+struct ChunkWs {
+    size_t xs, bsum, scale, part, part_bytes, total;
+};
+
+ChunkWs chunk_layout(const LinearShape& s, const ChunkCfg& c) {
+    auto up = [](size_t v) { return (v + 255) & ~static_cast<size_t>(255); };
+    ChunkWs l;
+    l.xs = up(static_cast<size_t>(kGemmMaxTiles) * sizeof(unsigned));
+    l.bsum = l.xs + (c.xs ? up(static_cast<size_t>(s.nb) * c.npad * 64 * sizeof(_Float16)) : 0);
+    l.scale = l.bsum + (c.xs ? up(static_cast<size_t>(s.nb) * c.npad * sizeof(float)) : 0);
+    l.part = l.scale + (c.xs ? up(static_cast<size_t>(c.npad) * sizeof(float)) : 0);
+    l.part_bytes = c.splits == 1 ? 0
+                                 : static_cast<size_t>(c.row_tiles) * c.tok_tiles * c.splits *
+                                       (2 * c.tt * kGemmThreads * 16);
+    l.total = l.part + l.part_bytes;
+    return l;
+}
+
+size_t chunk_workspace_bytes(const LinearShape& s) { return chunk_layout(s, choose_chunk(s)).total; }
+
+template <int QT, int TT, bool XS, int P = (TT == 1 ? 4 : 2)>
+hipError_t launch_chunk_t(const LinearShape& s, const ChunkCfg& c, const void* w, const float* x, float* y,
+                          char* ws, hipStream_t stream) {
+    constexpr int lds = ChunkLds<QT, 2, TT, XS>::bytes;
+    auto kern = gemm_chunk_kernel<QT, 2, TT, P, XS>;
+    static bool attr = [&] {
+        return hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                   lds) == hipSuccess;
+    }();
+    if (!attr) return hipErrorInvalidConfiguration;
+    const ChunkWs l = chunk_layout(s, c);
+    ChunkArgs a;
+    a.W = static_cast<const uint8_t*>(w);
+    a.x = x;
+    a.xs = XS ? reinterpret_cast<const _Float16*>(ws + l.xs) : nullptr;
+    a.bsum = XS ? reinterpret_cast<const float*>(ws + l.bsum) : nullptr;
+    a.xscale = XS ? reinterpret_cast<const float*>(ws + l.scale) : nullptr;
+    a.y = y;
+    a.part = reinterpret_cast<float*>(ws + l.part);
+    a.part_bytes = static_cast<uint32_t>(l.part_bytes);
+    a.tile_count = reinterpret_cast<unsigned*>(ws);
+    a.M = s.M, a.N = s.rows, a.K = s.K, a.nb = s.nb, a.npad = c.npad;
+    a.row_tiles = c.row_tiles, a.splits = c.splits, a.chunks_per_split = c.cps;
+    if (XS) {
+        hipLaunchKernelGGL((xsplit_kernel<QT>), dim3(c.npad), dim3(256), 0, stream, x, s.rows, s.K, s.nb, c.npad,
+                           reinterpret_cast<_Float16*>(ws + l.xs), reinterpret_cast<float*>(ws + l.bsum),
+                           reinterpret_cast<float*>(ws + l.scale));
+    }
+    const int grid = c.row_tiles * c.tok_tiles * c.splits;
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(kGemmThreads), lds, stream, a);
+    return hipGetLastError();
+}
+
+template <int QT>
+hipError_t launch_chunk_q(const LinearShape& s, const ChunkCfg& c, const void* w, const float* x, float* y,
+                          char* ws, hipStream_t stream) {
+    if (c.tt == 1) return launch_chunk_t<QT, 1, false>(s, c, w, x, y, ws, stream);
+    return launch_chunk_t<QT, 2, true>(s, c, w, x, y, ws, stream);
+}
+
+bool use_chunk(const LinearShape& s, const float* x) {
+    if (!chunk_supported(s)) return false;
+    const ChunkCfg c = choose_chunk(s);
+    const size_t wbytes = static_cast<size_t>(s.M) * s.nb * block_bytes(s.qtype);
+    return (c.xs || (reinterpret_cast<uintptr_t>(x) & 15u) == 0) && wbytes < (static_cast<size_t>(1) << 32) &&
+           chunk_layout(s, c).part_bytes < (static_cast<size_t>(1) << 31);
+}
+
 }  // namespace
 
 bool gemm_supported(const LinearShape& s) {
@@ -629,16 +1200,28 @@ bool gemm_supported(const LinearShape& s) {
 
 size_t gemm_workspace_bytes(const LinearShape& s) {
     if (!gemm_supported(s)) return 0;
-    return layout(s, choose(s)).total;
+    size_t b = layout(s, choose(s)).total;
+    if (chunk_supported(s)) b = std::max(b, chunk_workspace_bytes(s));
+    return b;
 }
 
 hipError_t launch_gemm(const LinearShape& s, const void* w, const float* x, float* y, void* ws,
                        size_t ws_bytes, hipStream_t stream) {
     if (!gemm_supported(s)) return hipErrorNotSupported;
+    if (ws == nullptr) return hipErrorInvalidValue;
+    char* base = static_cast<char*>(ws);
+    if (use_chunk(s, x)) {
+        if (ws_bytes < chunk_workspace_bytes(s)) return hipErrorInvalidValue;
+        const ChunkCfg c = choose_chunk(s);
+        switch (s.qtype) {
+            case 1: return launch_chunk_q<1>(s, c, w, x, y, base, stream);
+            case 2: return launch_chunk_q<2>(s, c, w, x, y, base, stream);
+            default: return launch_chunk_q<3>(s, c, w, x, y, base, stream);
+        }
+    }
     const GemmCfg c = choose(s);
     const WsLayout l = layout(s, c);
-    if (ws == nullptr || ws_bytes < l.total) return hipErrorInvalidValue;
-    char* base = static_cast<char*>(ws);
+    if (ws_bytes < l.total) return hipErrorInvalidValue;
     switch (s.qtype) {
         case 1: return launch_q<1>(s, c, l, w, x, y, base, stream);
         case 2: return launch_q<2>(s, c, l, w, x, y, base, stream);
@@ -648,8 +1231,14 @@ hipError_t launch_gemm(const LinearShape& s, const void* w, const float* x, floa
 
 const char* gemm_kernel_name(const LinearShape& s) {
     static thread_local char buf[96];
-    const GemmCfg c = choose(s);
     const char* fmt = s.qtype == 1 ? "q8_0" : s.qtype == 2 ? "q4_0" : "q4_1";
+    if (chunk_supported(s)) {
+        const ChunkCfg c = choose_chunk(s);
+        snprintf(buf, sizeof buf, "gemm_mfma_%s_chunk%s_bm128_bn%d_splitk%d", fmt, c.xs ? "_xs" : "", 16 * c.tt,
+                 c.splits);
+        return buf;
+    }
+    const GemmCfg c = choose(s);
     snprintf(buf, sizeof buf, "gemm_mfma_%s_bm%d_bn%d_splitk%d", fmt, c.bm, c.bn, c.splits);
     return buf;
 }
