@@ -68,8 +68,11 @@ __device__ __forceinline__ int slot_k(int g, int j) {
 // ---------------------------------------------------------------------------
 // xsplit: one workgroup per (padded) token row; thread t takes the half blocks
 // t, t + 256, ... (16 consecutive floats each, so a wave reads 4 KB contiguous).
-// Pass 1 finds max|x| of the row, pass 2 (L2 hits) scales, splits and writes
-// each half block's 16 hi and 16 lo halves into its fragment slots.
+// The first kXsCache of them stay in registers between the two passes (the
+// max|x| of the row, then the scaled split), so rows up to 16 384 elements are
+// read once; longer rows re-read the rest (L2 hits).
+constexpr int kXsCache = 4;
+
 template <int QT>
 __global__ __launch_bounds__(256) void xsplit_kernel(const float* __restrict__ x, int N, int K,
                                                      int nb, int npad, _Float16* __restrict__ xs,
@@ -83,7 +86,10 @@ __global__ __launch_bounds__(256) void xsplit_kernel(const float* __restrict__ x
 
     auto load16 = [&](int hb, float (&v)[16]) {
         const int k0 = hb * 16;
-        if (valid && k0 + 16 <= K && (reinterpret_cast<uintptr_t>(xr + k0) & 15u) == 0) {
+        if (!valid || hb >= nhb) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) v[i] = 0.0f;
+        } else if (k0 + 16 <= K && (reinterpret_cast<uintptr_t>(xr + k0) & 15u) == 0) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const float4 f = reinterpret_cast<const float4*>(xr + k0)[i];
@@ -94,12 +100,19 @@ __global__ __launch_bounds__(256) void xsplit_kernel(const float* __restrict__ x
             }
         } else {
 #pragma unroll
-            for (int i = 0; i < 16; ++i) v[i] = (valid && k0 + i < K) ? xr[k0 + i] : 0.0f;
+            for (int i = 0; i < 16; ++i) v[i] = (k0 + i < K) ? xr[k0 + i] : 0.0f;
         }
     };
 
+    float cache[kXsCache][16];
     float mx = 0.0f;
-    for (int hb = threadIdx.x; hb < nhb; hb += 256) {
+#pragma unroll
+    for (int c = 0; c < kXsCache; ++c) {
+        load16(threadIdx.x + 256 * c, cache[c]);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, fabsf(cache[c][i]));
+    }
+    for (int hb = threadIdx.x + 256 * kXsCache; hb < nhb; hb += 256) {
         float v[16];
         load16(hb, v);
 #pragma unroll
@@ -122,18 +135,10 @@ __global__ __launch_bounds__(256) void xsplit_kernel(const float* __restrict__ x
     }
     if (threadIdx.x == 0) scale[n] = sc;
 
-    // The loop bound is uniform per wave pair, so the shuffle partner exists.
-    const int iters = (nhb + 255) / 256;
-    for (int it = 0; it < iters; ++it) {
-        const int hb = threadIdx.x + 256 * it;
+    // Scale, split and store one half block.  Called uniformly by all lanes
+    // (the shuffle pairs half blocks hb and hb ^ 1, held by adjacent lanes).
+    auto emit = [&](int hb, float (&v)[16]) {
         const bool have = hb < nhb;
-        float v[16];
-        if (have) {
-            load16(hb, v);
-        } else {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) v[i] = 0.0f;
-        }
 #pragma unroll
         for (int i = 0; i < 16; ++i) v[i] *= inv;
         float sum = 0.0f;
@@ -142,7 +147,7 @@ __global__ __launch_bounds__(256) void xsplit_kernel(const float* __restrict__ x
         const float other = __shfl_xor(sum, 1, 64);
         const int b = hb >> 1;
         const int half = hb & 1;
-        if (!have) continue;
+        if (!have) return;
         if (half == 0) {
             // block sum in the order (elements 0..15) + (16..31), 4-element groups
             bsum[static_cast<size_t>(b) * npad + n] = sum + other;
@@ -186,6 +191,16 @@ __global__ __launch_bounds__(256) void xsplit_kernel(const float* __restrict__ x
                     f16x4{lo[4 * g], lo[4 * g + 1], lo[4 * g + 2], lo[4 * g + 3]};
             }
         }
+    };
+    const int iters = (nhb + 255) / 256;  // uniform across the workgroup
+#pragma unroll
+    for (int c = 0; c < kXsCache; ++c)
+        if (c < iters) emit(threadIdx.x + 256 * c, cache[c]);
+    for (int it = kXsCache; it < iters; ++it) {
+        float v[16];
+        const int hb = threadIdx.x + 256 * it;
+        load16(hb, v);
+        emit(hb, v);
     }
 }
 
@@ -1093,9 +1108,11 @@ hipError_t launch_q(const LinearShape& s, const GemmCfg& c, const WsLayout& l, c
 }
 
 // Chunked-kernel configuration: 128 rows per workgroup, 16 tokens per
-// workgroup for batches up to 16 (x split in the kernel) and 32 above (x split
-// by xsplit_kernel first), K split until the grid is about two workgroups per
-// CU.
+// workgroup for batches up to 16 and 32 above; x split in the kernel for
+// batches up to 16, and up to 64 when there are few row tiles, else by
+// xsplit_kernel first (the in-kernel split is repeated by every row tile:
+// measured on MI355X, 4096 rows x 64 tokens favour it, 11008 rows do not);
+// K split until the grid is about two workgroups per CU.
 struct ChunkCfg {
     int tt, row_tiles, tok_tiles, splits, cps, npad;
     bool xs;
@@ -1108,7 +1125,7 @@ bool chunk_supported(const LinearShape& s) {
 ChunkCfg choose_chunk(const LinearShape& s) {
     ChunkCfg c;
     c.tt = s.rows <= 16 ? 1 : 2;
-    c.xs = c.tt > 1;
+    c.xs = s.rows > 64 || (s.rows > 16 && s.M > 8192);
     c.row_tiles = (s.M + 127) / 128;
     c.tok_tiles = (s.rows + 16 * c.tt - 1) / (16 * c.tt);
     c.npad = c.tok_tiles * 16 * c.tt;
@@ -1181,6 +1198,7 @@ template <int QT>
 hipError_t launch_chunk_q(const LinearShape& s, const ChunkCfg& c, const void* w, const float* x, float* y,
                           char* ws, hipStream_t stream) {
     if (c.tt == 1) return launch_chunk_t<QT, 1, false>(s, c, w, x, y, ws, stream);
+    if (!c.xs) return launch_chunk_t<QT, 2, false>(s, c, w, x, y, ws, stream);
     return launch_chunk_t<QT, 2, true>(s, c, w, x, y, ws, stream);
 }
 
