@@ -41,21 +41,34 @@ inline int pair_lds_bytes(int nb) { return (nb / 2) * 256 + nb * 8; }
 //   Q4_1: c0 = 1024 * S, c1 = X  with X = sum(x), S = sum(x') over the block.
 // Elements past K read as 0, so a partial last block contributes nothing
 // (the reference loops only k < K, src/quant.cpp:421-426).
-// COHERENT reads x with agent-scope loads, which return what another
+// COHERENT reads x with agent-scope (sc1) loads, which return what another
 // workgroup of the same launch stored with agent-scope stores even when this
 // XCD's L2 holds an older copy of the line.  Those loads are not cached, so
-// they are issued coalesced (consecutive lanes, consecutive words) into the
-// pair region of LDS first; each thread then takes its block from LDS.  A
-// block's two pair partners (g, g ^ 1) are neighbouring lanes of one wave, so
-// every read of the region happens before any write that permutes it.
+// they are issued as coalesced 16-byte buffer loads (the buffer's range check
+// returns 0 past K) into the pair region of LDS first; each thread then takes
+// its block from LDS.  A block's two pair partners (g, g ^ 1) are neighbouring
+// lanes of one wave, so every read of the region happens before any write
+// that permutes it.
 template <int QT, bool COHERENT = false>
 __device__ __forceinline__ void stage_x(const float* __restrict__ x, int K, int nb,
                                         float4* __restrict__ xs4, float2* __restrict__ cb) {
     if (COHERENT) {
-        float* raw = reinterpret_cast<float*>(xs4);
-        const int n = nb * kQK;
-        for (int i = threadIdx.x; i < n; i += blockDim.x) {
-            raw[i] = i < K ? __hip_atomic_load(x + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.0f;
+        constexpr int kAgentScope = 16;  // sc1 cache policy
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(x), static_cast<short>(0), K * 4, 0x00020000);
+        const int n4 = nb * (kQK / 4);
+        const int k4 = K / 4;
+        for (int i = threadIdx.x; i < n4; i += blockDim.x) {
+            float4 v;
+            if (i < k4) {
+                v = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rs, i * 16, 0, kAgentScope));
+            } else {
+                v.x = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, i * 16, 0, kAgentScope));
+                v.y = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, i * 16 + 4, 0, kAgentScope));
+                v.z = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, i * 16 + 8, 0, kAgentScope));
+                v.w = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, i * 16 + 12, 0, kAgentScope));
+            }
+            xs4[i] = v;
         }
         __syncthreads();
     }

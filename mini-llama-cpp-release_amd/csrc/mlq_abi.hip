@@ -947,6 +947,16 @@ int mlq_hip_sequence_create(const mlq_linear_call* calls, int n, const int* stag
             delete seq;
             return hip_fail(e, "sequence occupancy");
         }
+        for (int k = g.stage_begin; k < g.stage_begin + g.nstages; ++k) {
+            // A stage reads x coherently when an earlier stage of the same
+            // launch writes where it reads.
+            descs[k].coherent = 0;
+            if (mode == MLQ_SEQ_PERSISTENT) {
+                for (int e2 = g.stage_begin; e2 < k; ++e2)
+                    for (int c = stage_first[e2]; c < stage_first[e2] + descs[e2].ncalls; ++c)
+                        if (overlaps(yr[c], xr[stage_first[k]])) descs[k].coherent = 1;
+            }
+        }
     }
     const size_t table_bytes = descs.size() * sizeof(mlq::SeqStageDesc);
     seq->sync_offset = (table_bytes + 255) & ~static_cast<size_t>(255);
@@ -980,9 +990,8 @@ int mlq_hip_sequence_launch(mlq_sequence_t seq, void* stream) {
     auto* syncs = reinterpret_cast<mlq::SeqSync*>(static_cast<char*>(seq->mem) + seq->sync_offset);
     for (size_t i = 0; i < seq->segs.size(); ++i) {
         const auto& g = seq->segs[i];
-        const bool coherent = seq->mode == MLQ_SEQ_PERSISTENT && g.nstages > 1;
         hipError_t e = mlq::launch_sequence(g.qtype, g.lpr, table + g.stage_begin, g.nstages, syncs + i, g.grid,
-                                            g.lds_bytes, seq->spin_limit, coherent, s);
+                                            g.lds_bytes, seq->spin_limit, s);
         if (e != hipSuccess) return hip_fail(e, mlq::sequence_kernel_name(g.qtype, g.lpr));
     }
     return MLQ_OK;

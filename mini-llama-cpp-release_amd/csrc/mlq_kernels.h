@@ -83,6 +83,7 @@ struct SeqStageDesc {
     int items;       // row items: ceil(rows / (64 / lane-group width))
     int ncalls;
     int barrier;     // 1: wait for every earlier stage of the launch first
+    int coherent;    // 1: x was written by an earlier stage of the same launch
     SeqCallDesc call[kSeqMaxCalls];
 };
 
@@ -101,12 +102,10 @@ struct SeqSync {
 
 bool sequence_supported(int qtype, int K);
 int sequence_lpr(int K);                 // lane-group width for rows of K elements: 16 or 64
-int sequence_stage_lds_bytes(int K);
+int sequence_stage_lds_bytes(int K);     // x area of a stage (the result area comes on top)
 hipError_t sequence_grid(int qtype, int lpr, int lds_bytes, int device, int* grid);
-// coherent_x: stage x with agent-scope loads (needed when an earlier stage of
-// the same launch wrote it; plain cached loads otherwise).
 hipError_t launch_sequence(int qtype, int lpr, const SeqStageDesc* stages, int nstages, SeqSync* sync,
-                           int grid, int lds_bytes, unsigned spin_limit, bool coherent_x, hipStream_t stream);
+                           int grid, int lds_bytes, unsigned spin_limit, hipStream_t stream);
 const char* sequence_kernel_name(int qtype, int lpr);
 
 // Device quantizer and synthetic-data generator.

@@ -3,38 +3,42 @@
 // A decode step issues a fixed chain of GEMVs (LLaMA: q, k, v -> o ->
 // gate, up -> down per layer, then lm_head).  Launched one kernel at a time,
 // every call pays the launch, the first-byte latency of its weights and the
-// drain of its last wave; at 4096x4096 Q4_0 (9.4 MB, ~1.5 us of HBM time)
-// those cost more than the transfer itself.  This kernel runs the chain in one
-// launch:
+// drain of its last wave (about 4.5 us per launch on MI355X, against 1.5 us of
+// HBM time for a 4096x4096 Q4_0 matrix).  This kernel runs the chain in one
+// launch and keeps the weights streaming across stage boundaries:
 //  * The chain is split into *stages*: up to kSeqMaxCalls GEMVs that read the
 //    same x (q, k, v or gate, up) and write disjoint outputs.  A stage's rows
-//    are concatenated and dealt to all waves of the grid (wave w takes row
-//    items w, w + GW, ...), so a fused q/k/v stage is one balanced pass.
+//    are concatenated into row items and dealt to all waves of the grid (wave
+//    w takes items w, w + GW, ...), so a fused q/k/v stage is one balanced
+//    pass.
+//  * Each wave walks its work units (row item x chunk of LPR pairs) with a
+//    D-deep register ring of weight requests.  Inside a stage the ring runs D
+//    units ahead; at a stage's end the wave arrives at the barrier first and
+//    then requests the next stage's first D units at once, so they stream
+//    from HBM while the grid synchronises and stages x (weights never depend
+//    on earlier outputs).
 //  * Between stages a grid-wide barrier makes every output of the earlier
 //    stages visible before any wave stages the next x, so a call may consume
 //    any earlier call's y, exactly as with one launch per call in stream order.
-//  * Weights never depend on earlier outputs, so each wave requests the next
-//    chunk of W (one pair per lane) before computing the current one - also
-//    across the stage boundary: the next stage's first weights are in flight
-//    while the grid waits at the barrier and stages x.
 //  * Per row the arithmetic is that of the GEMV kernels in gemv.hip (same pair
 //    dot, same lane-group width and chunk order, same DPP reduction), so
 //    outputs are bit-identical to one launch per call.
 //
 // Barrier protocol (device memory, agent scope, no cache-maintenance fences):
 //  * outputs are written with agent-scope stores (write-through to the point
-//    of coherence) and the next stage reads x with agent-scope loads, so no L2
-//    writeback or invalidate is needed - those cost ~20-40 us per grid
-//    barrier on MI355X when every workgroup issues them;
-//  * arrival: each wave waits for its stores to complete, the workgroup
-//    synchronises, and thread 0 adds 1 to sub[b % 8]; the last arrival of a
-//    group adds 1 to `top` (a two-level tree: one hot address would serialise
-//    all arrivals, ~90 ns each);
-//  * the next stage's first weights are requested right after arriving, then
-//    thread 0 polls `top`; the poll is bounded by `spin_limit`: a workgroup
-//    that gives up sets `error` and stops waiting, so every wave always reaches
-//    the end of the kernel (the launch's outputs are then void and the host
-//    reports it);
+//    of coherence); a stage whose x an earlier stage of the launch wrote reads
+//    it with agent-scope loads, so no L2 writeback or invalidate is needed -
+//    those cost ~20-40 us per grid barrier on MI355X when every workgroup
+//    issues them;
+//  * arrival: each wave waits for its stores to complete (its ring holds no
+//    request then: the next stage's are issued after arriving), the
+//    workgroup synchronises, and thread 0 adds 1 to sub[b % 8]; the last
+//    arrival of a group adds 1 to `top` (a two-level tree: one hot address
+//    would serialise all arrivals, ~90 ns each);
+//  * thread 0 polls `top`; the poll is bounded by `spin_limit`: a workgroup
+//    that gives up sets `error` and stops waiting, so every wave always
+//    reaches the end of the kernel (the launch's outputs are then void and the
+//    host reports it);
 //  * the workgroups count themselves out through `exit`; the last one resets
 //    all counters, so the next launch starts from zero without a host reset.
 // All workgroups must be resident together: the host sizes the grid from the
@@ -50,9 +54,16 @@
 namespace mlq {
 namespace {
 
+// First stage at or after `s` in which wave `gw` has a row item.
+__device__ __forceinline__ int seq_next_stage(const SeqStageDesc* __restrict__ st, int nstages, int s, int gw) {
+    while (s < nstages && gw >= st[s].items) ++s;
+    return s;
+}
+
+// Unit i of wave gw in stage S: row item gw + (i / nch) * GW, chunk i % nch.
 template <int QT, int LPR>
-__device__ __forceinline__ void seq_load_chunk(const SeqStageDesc& S, int it, int c, int slot, int pl,
-                                               uint32_t (&w)[Fmt<QT>::DW]) {
+__device__ __forceinline__ void seq_load(const SeqStageDesc& S, int it, int c, int slot, int pl,
+                                         uint32_t (&w)[Fmt<QT>::DW]) {
     constexpr int DW = Fmt<QT>::DW;
     constexpr int SUB = 64 / LPR;
     // Rows / pairs past the end re-read the last one; their results are dropped.
@@ -86,17 +97,11 @@ __device__ __forceinline__ void seq_store_row(const SeqStageDesc& S, int row, fl
     __hip_atomic_store(y + (row - rb), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// First stage at or after `s` in which wave `gw` has a row item.
-__device__ __forceinline__ int seq_next_stage(const SeqStageDesc* __restrict__ st, int nstages, int s, int gw) {
-    while (s < nstages && gw >= st[s].items) ++s;
-    return s;
-}
-
-__device__ __forceinline__ unsigned seq_load(const unsigned* p) {
+__device__ __forceinline__ unsigned seq_load_word(const unsigned* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-__device__ __forceinline__ void seq_store(unsigned* p, unsigned v) {
+__device__ __forceinline__ void seq_store_word(unsigned* p, unsigned v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -122,9 +127,9 @@ __device__ __forceinline__ void seq_wait(SeqSync* sync, unsigned n, unsigned spi
     if (threadIdx.x == 0 && !gave_up) {
         const unsigned target = n * seq_groups();
         unsigned polls = 0;
-        while (seq_load(&sync->top[0]) < target) {
+        while (seq_load_word(&sync->top[0]) < target) {
             if (++polls > spin_limit) {
-                seq_store(&sync->error[0], 1u);
+                seq_store_word(&sync->error[0], 1u);
                 gave_up = true;
                 break;
             }
@@ -134,16 +139,19 @@ __device__ __forceinline__ void seq_wait(SeqSync* sync, unsigned n, unsigned spi
     __syncthreads();
 }
 
-// Waves per SIMD the register budget is sized for: two workgroups per CU for
-// the 4-bit formats; Q8_0's 17-dword pairs fit one (same bytes in flight).
-template <int QT> struct SeqOcc { static constexpr int waves_per_simd = QT == 1 ? 2 : 4; };
+// Register budget: 128 VGPRs (the x pair, the weight ring and the cursors),
+// so that two workgroups fit per CU: every wave of the grid is needed to
+// give the 4096-row stages one row per wave.
+template <int QT> struct SeqOcc { static constexpr int waves_per_simd = 4; };
+// Weight ring depth (work units in flight per wave).
+template <int QT> struct SeqDepth { static constexpr int D = QT == 1 ? 1 : 2; };
 
 template <int QT, int LPR>
-__global__ __launch_bounds__(kWaves * 64, SeqOcc<QT>::waves_per_simd) void gemv_sequence_kernel(const SeqStageDesc* __restrict__ st,
-                                                                       int nstages, SeqSync* __restrict__ sync,
-                                                                       unsigned spin_limit, int coherent_x) {
+__global__ __launch_bounds__(kWaves * 64, SeqOcc<QT>::waves_per_simd) void gemv_sequence_kernel(
+    const SeqStageDesc* __restrict__ st, int nstages, SeqSync* __restrict__ sync, unsigned spin_limit) {
     constexpr int DW = Fmt<QT>::DW;
     constexpr int SUB = 64 / LPR;
+    constexpr int D = SeqDepth<QT>::D;
     extern __shared__ float4 lds4[];
     const int lane = threadIdx.x & 63;
     const int slot = lane / LPR;
@@ -153,13 +161,23 @@ __global__ __launch_bounds__(kWaves * 64, SeqOcc<QT>::waves_per_simd) void gemv_
     const NibConsts nk = NibConsts::make();
     bool gave_up = false;
 
-    // Cursor of this wave: stage cs, row item cit, chunk cc (pairs cc*LPR + pl);
-    // wc holds that chunk's weights (or their request in flight).
-    int cs = seq_next_stage(st, nstages, 0, gw);
-    int cit = gw;
-    int cc = 0;
-    uint32_t wc[DW];
-    if (cs < nstages) seq_load_chunk<QT, LPR>(st[cs], cit, cc, slot, pl, wc);
+    // The ring holds units 0 .. D-1 of stage `ws` (the next stage with items
+    // for this wave) or, inside a stage, the next D units.
+    uint32_t wq[D][DW];
+    auto fill = [&](int s) {
+        const SeqStageDesc& S = st[s];
+        int it = gw, c = 0;
+#pragma unroll
+        for (int i = 0; i < D; ++i) {
+            seq_load<QT, LPR>(S, it, c, slot, pl, wq[i]);
+            if (++c == S.nch) {
+                c = 0;
+                if (it + GW < S.items) it += GW;  // past the wave's last item: re-read it
+            }
+        }
+    };
+    int ws = seq_next_stage(st, nstages, 0, gw);
+    if (ws < nstages) fill(ws);
 
     unsigned barriers = 0;
     for (int s = 0; s < nstages; ++s) {
@@ -174,92 +192,88 @@ __global__ __launch_bounds__(kWaves * 64, SeqOcc<QT>::waves_per_simd) void gemv_
         const int np = S.np;
         float4* xs4 = lds4;
         float2* cb = reinterpret_cast<float2*>(lds4 + np * 16);
-        if (coherent_x) {
+        if (S.coherent) {
             stage_x<QT, true>(S.x, S.K, S.nb, xs4, cb);
         } else {
             stage_x<QT, false>(S.x, S.K, S.nb, xs4, cb);
         }
         __syncthreads();
 
-        bool pending = false;  // successor lies in a later stage, not yet requested
-        if (S.nch == 1) {
-            // Rows of one chunk: every item of the stage uses the same x pair.
-            const int pp = min(pl, np - 1);
-            float xv[64];
-            load_xv(xs4, pp, xv);
-            const float2 c0 = cb[2 * pp];
-            const float2 c1 = cb[2 * pp + 1];
-            const bool active = pl < np;
-            while (cs == s) {
-                int ns = cs;
-                int nit = cit + GW;
-                if (nit >= S.items) {
-                    ns = seq_next_stage(st, nstages, s + 1, gw);
-                    nit = gw;
+        if (ws == s) {
+            // Units of this wave: items gw, gw + GW, ... (< items), nch chunks each.
+            const int nit = (S.items - gw + GW - 1) / GW;
+            const int nu = nit * S.nch;
+            int it = gw, c = 0;        // unit being computed
+            int pit = gw, pc = 0;      // unit D ahead (the next request)
+            for (int i = 0; i < D; ++i) {
+                if (++pc == S.nch) {
+                    pc = 0;
+                    pit += GW;
                 }
-                uint32_t wn[DW];
-                const bool same_stage = ns == s;
-                if (same_stage) seq_load_chunk<QT, LPR>(S, nit, 0, slot, pl, wn);
-                float acc = active ? PairDot<QT>::run(wc, xv, c0, c1, 0.0f, nk) : 0.0f;
-                acc = group_sum<LPR>(acc);
-                const int row = cit * SUB + slot;
-                if (pl == LPR - 1 && row < S.rows) seq_store_row(S, row, acc);
-                if (same_stage) {
-#pragma unroll
-                    for (int i = 0; i < DW; ++i) wc[i] = wn[i];
-                } else {
-                    pending = ns < nstages;
-                }
-                cs = ns;
-                cit = nit;
             }
-        } else {
-            float acc = 0.0f;
-            while (cs == s) {
-                int ns = cs;
-                int nit = cit;
-                int nc = cc + 1;
-                if (nc >= S.nch) {
-                    nc = 0;
-                    nit = cit + GW;
-                    if (nit >= S.items) {
-                        ns = seq_next_stage(st, nstages, s + 1, gw);
-                        nit = gw;
+            if (S.nch == 1) {
+                // Rows of one chunk: every item of the stage uses the same x pair.
+                const int pp = min(pl, np - 1);
+                float xv[64];
+                load_xv(xs4, pp, xv);
+                const float2 c0 = cb[2 * pp];
+                const float2 c1 = cb[2 * pp + 1];
+                const bool active = pl < np;
+                for (int u = 0; u < nu; ++u) {
+                    float acc = active ? PairDot<QT>::run(wq[0], xv, c0, c1, 0.0f, nk) : 0.0f;
+#pragma unroll
+                    for (int i = 0; i + 1 < D; ++i)
+#pragma unroll
+                        for (int j = 0; j < DW; ++j) wq[i][j] = wq[i + 1][j];
+                    if (u + D < nu) seq_load<QT, LPR>(S, pit, 0, slot, pl, wq[D - 1]);
+                    pit += GW;
+                    acc = group_sum<LPR>(acc);
+                    const int row = it * SUB + slot;
+                    if (pl == LPR - 1 && row < S.rows) seq_store_row(S, row, acc);
+                    it += GW;
+                }
+            } else {
+                float acc = 0.0f;
+                for (int u = 0; u < nu; ++u) {
+                    const int p = c * LPR + pl;
+                    {
+                        const int pp = min(p, np - 1);
+                        float xv[64];
+                        load_xv(xs4, pp, xv);
+                        const float2 c0 = cb[2 * pp];
+                        const float2 c1 = cb[2 * pp + 1];
+                        if (p < np) acc = PairDot<QT>::run(wq[0], xv, c0, c1, acc, nk);
+                    }
+#pragma unroll
+                    for (int i = 0; i + 1 < D; ++i)
+#pragma unroll
+                        for (int j = 0; j < DW; ++j) wq[i][j] = wq[i + 1][j];
+                    if (u + D < nu) seq_load<QT, LPR>(S, pit, pc, slot, pl, wq[D - 1]);
+                    if (++pc == S.nch) {
+                        pc = 0;
+                        pit += GW;
+                    }
+                    if (c == S.nch - 1) {
+                        const float r = group_sum<LPR>(acc);
+                        acc = 0.0f;
+                        const int row = it * SUB + slot;
+                        if (pl == LPR - 1 && row < S.rows) seq_store_row(S, row, r);
+                    }
+                    if (++c == S.nch) {
+                        c = 0;
+                        it += GW;
                     }
                 }
-                uint32_t wn[DW];
-                const bool same_stage = ns == s;
-                if (same_stage) seq_load_chunk<QT, LPR>(S, nit, nc, slot, pl, wn);
-                const int p = cc * LPR + pl;
-                {
-                    const int pp = min(p, np - 1);
-                    float xv[64];
-                    load_xv(xs4, pp, xv);
-                    const float2 c0 = cb[2 * pp];
-                    const float2 c1 = cb[2 * pp + 1];
-                    if (p < np) acc = PairDot<QT>::run(wc, xv, c0, c1, acc, nk);
-                }
-                if (cc == S.nch - 1) {
-                    const float r = group_sum<LPR>(acc);
-                    acc = 0.0f;
-                    const int row = cit * SUB + slot;
-                    if (pl == LPR - 1 && row < S.rows) seq_store_row(S, row, r);
-                }
-                if (same_stage) {
-#pragma unroll
-                    for (int i = 0; i < DW; ++i) wc[i] = wn[i];
-                } else {
-                    pending = ns < nstages;
-                }
-                cs = ns;
-                cit = nit;
-                cc = nc;
             }
         }
         // Arrive before requesting the next stage's weights, so the arrival
-        // does not wait for them.
+        // does not wait for them; then fill the ring for the next stage with
+        // items for this wave.
         if (s + 1 < nstages && st[s + 1].barrier) seq_arrive(sync, ++barriers);
-        if (pending) seq_load_chunk<QT, LPR>(st[cs], cit, cc, slot, pl, wc);
+        if (ws == s) {
+            ws = seq_next_stage(st, nstages, s + 1, gw);
+            if (ws < nstages) fill(ws);
+        }
     }
 
     // Count out; the last workgroup resets the counters for the next launch.
@@ -267,9 +281,9 @@ __global__ __launch_bounds__(kWaves * 64, SeqOcc<QT>::waves_per_simd) void gemv_
     if (threadIdx.x == 0) {
         const unsigned done = __hip_atomic_fetch_add(&sync->exit[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (done == gridDim.x - 1) {
-            for (int g = 0; g < kSeqGroups; ++g) seq_store(&sync->sub[g][0], 0u);
-            seq_store(&sync->top[0], 0u);
-            seq_store(&sync->exit[0], 0u);
+            for (int g = 0; g < kSeqGroups; ++g) seq_store_word(&sync->sub[g][0], 0u);
+            seq_store_word(&sync->top[0], 0u);
+            seq_store_word(&sync->exit[0], 0u);
         }
     }
 }
@@ -331,11 +345,10 @@ hipError_t sequence_grid(int qtype, int lpr, int lds_bytes, int device, int* gri
 }
 
 hipError_t launch_sequence(int qtype, int lpr, const SeqStageDesc* stages, int nstages, SeqSync* sync,
-                           int grid, int lds_bytes, unsigned spin_limit, bool coherent_x, hipStream_t stream) {
+                           int grid, int lds_bytes, unsigned spin_limit, hipStream_t stream) {
     const void* k = seq_kernel(qtype, lpr);
     if (k == nullptr || nstages <= 0 || grid <= 0) return hipErrorInvalidValue;
-    int coh = coherent_x ? 1 : 0;
-    void* args[] = {&stages, &nstages, &sync, &spin_limit, &coh};
+    void* args[] = {&stages, &nstages, &sync, &spin_limit};
     return hipLaunchKernel(k, dim3(grid), dim3(kWaves * 64), args, static_cast<size_t>(lds_bytes), stream);
 }
 
