@@ -131,8 +131,11 @@ __global__ __launch_bounds__(WAVES * 64, (SingleOcc<QT, R>::waves_per_simd)) voi
     const int gstride = gridDim.x * WAVES;
     int gi = blockIdx.x * WAVES + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 
+    // Every weight request is unconditional (a group past the end re-reads the
+    // last one; its result is dropped): a guarded request makes the compiler
+    // wait for it right away, which serialises the prefetch.
     uint32_t wc[R][DW];
-    if (gi < groups) load_rows<R, DW>(g, row_dw, gi * (SUB * R) + slot * R, M, p, wc);
+    load_rows<R, DW>(g, row_dw, min(gi, groups - 1) * (SUB * R) + slot * R, M, p, wc);
     stage_x<QT>(x, K, nb, xs4, cb);
     __syncthreads();
     float xv[64];
@@ -143,8 +146,9 @@ __global__ __launch_bounds__(WAVES * 64, (SingleOcc<QT, R>::waves_per_simd)) voi
 
     for (; gi < groups; gi += gstride) {
         uint32_t wn[R][DW];
-        const int gn = gi + gstride;
-        if (gn < groups) load_rows<R, DW>(g, row_dw, gn * (SUB * R) + slot * R, M, p, wn);
+        const int gn = min(gi + gstride, groups - 1);
+        load_rows<R, DW>(g, row_dw, gn * (SUB * R) + slot * R, M, p, wn);
+        __builtin_amdgcn_sched_barrier(0);  // the request stays ahead of this group's compute
         float acc[R];
 #pragma unroll
         for (int r = 0; r < R; ++r) {
@@ -183,23 +187,33 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_multi_kernel(
     const int row0 = (blockIdx.x * WAVES + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) * (SUB * R) + slot * R;
     const size_t row_dw = static_cast<size_t>(np) * DW;
 
+    // Chunks c = 0 .. nch-1 (pair c * LPR + pl of every lane) in a uniform loop;
+    // lanes past the row keep their sum.  Requests are unconditional (past the
+    // row: re-read the last pair) so the prefetch is never waited for early.
+    const int nch = (np + LPR - 1) / LPR;
     uint32_t wc[R][DW];
-    if (pl < np) load_rows<R, DW>(g, row_dw, row0, M, pl, wc);
+    load_rows<R, DW>(g, row_dw, row0, M, min(pl, np - 1), wc);
     stage_x<QT>(x, K, nb, xs4, cb);
     __syncthreads();
     const NibConsts nk = NibConsts::make();
     float acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = 0.0f;
-    for (int p = pl; p < np; p += LPR) {
+    for (int c = 0; c < nch; ++c) {
+        const int p = c * LPR + pl;
+        const int pc = min(p, np - 1);
         uint32_t wn[R][DW];
-        if (p + LPR < np) load_rows<R, DW>(g, row_dw, row0, M, p + LPR, wn);
+        load_rows<R, DW>(g, row_dw, row0, M, min(p + LPR, np - 1), wn);
+        __builtin_amdgcn_sched_barrier(0);  // the request stays ahead of this chunk's compute
         float xv[64];
-        load_xv(xs4, p, xv);
-        const float2 c0 = cb[2 * p];
-        const float2 c1 = cb[2 * p + 1];
+        load_xv(xs4, pc, xv);
+        const float2 c0 = cb[2 * pc];
+        const float2 c1 = cb[2 * pc + 1];
 #pragma unroll
-        for (int r = 0; r < R; ++r) acc[r] = PairDot<QT>::run(wc[r], xv, c0, c1, acc[r], nk);
+        for (int r = 0; r < R; ++r) {
+            const float a = PairDot<QT>::run(wc[r], xv, c0, c1, acc[r], nk);
+            acc[r] = p < np ? a : acc[r];
+        }
 #pragma unroll
         for (int r = 0; r < R; ++r)
 #pragma unroll

@@ -27,6 +27,17 @@ template <> struct Fmt<1> { static constexpr int BB = 34, DW = 17; };  // Q8_0
 template <> struct Fmt<2> { static constexpr int BB = 18, DW = 9; };   // Q4_0
 template <> struct Fmt<3> { static constexpr int BB = 20, DW = 10; };  // Q4_1
 
+// Device pointers that the compiler cannot trace to a kernel argument (loaded
+// from a descriptor table) are generic; generic accesses become FLAT
+// instructions, which count against the LDS counter as well and make every
+// wait conservative.  These casts state that the memory is global.
+typedef __attribute__((address_space(1))) const uint32_t g_u32;
+typedef __attribute__((address_space(1))) const float g_f32;
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(1))) const f32x4_t g_f4;
+__device__ __forceinline__ g_u32* as_global(const uint32_t* p) { return (g_u32*)p; }
+__device__ __forceinline__ g_f32* as_global(const float* p) { return (g_f32*)p; }
+
 constexpr int kMaxPairLdsBytes = 64 * 1024;
 constexpr int kWaves = 8;             // waves per workgroup
 constexpr int kPersistentWgs = 512;   // ~2 workgroups per CU on a 256-CU MI355X
@@ -88,7 +99,8 @@ __device__ __forceinline__ void stage_x(const float* __restrict__ x, int K, int 
         } else if (k0 + kQK <= K && (reinterpret_cast<uintptr_t>(x + k0) & 15u) == 0) {
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                const float4 f = reinterpret_cast<const float4*>(x + k0)[i];
+                const f32x4_t fv = ((g_f4*)(x + k0))[i];
+                const float4 f = make_float4(fv.x, fv.y, fv.z, fv.w);
                 v[4 * i] = f.x;
                 v[4 * i + 1] = f.y;
                 v[4 * i + 2] = f.z;
@@ -96,7 +108,7 @@ __device__ __forceinline__ void stage_x(const float* __restrict__ x, int K, int 
             }
         } else {
 #pragma unroll
-            for (int i = 0; i < 32; ++i) v[i] = (k0 + i < K) ? x[k0 + i] : 0.0f;
+            for (int i = 0; i < 32; ++i) v[i] = (k0 + i < K) ? as_global(x)[k0 + i] : 0.0f;
         }
         float X = 0.0f;
         float S = 0.0f;

@@ -78,12 +78,24 @@ __device__ __forceinline__ void seq_load(const SeqStageDesc& S, int it, int c, i
             rb = S.call[j].row_begin;
         }
     }
-    const uint32_t* src = static_cast<const uint32_t*>(W) + static_cast<size_t>(row - rb) * (static_cast<size_t>(S.np) * DW) +
-                          static_cast<size_t>(p) * DW;
+    g_u32* src = as_global(static_cast<const uint32_t*>(W)) + static_cast<size_t>(row - rb) * (static_cast<size_t>(S.np) * DW) +
+                 static_cast<size_t>(p) * DW;
 #pragma unroll
     for (int i = 0; i < DW; ++i) w[i] = src[i];
 }
 
+// The row sum of lane group `slot` (held by its last lane after group_sum)
+// in every lane of the group.
+template <int LPR>
+__device__ __forceinline__ float seq_bcast(float v) {
+    const int src = (threadIdx.x & 63) | (LPR - 1);
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src << 2, __builtin_bit_cast(int, v)));
+}
+
+// Every lane stores: the lanes of a row group store the same value, and a
+// group past the stage's rows recomputed the last row (its requests are
+// clamped to it), so it stores that row's own value again.  No store is
+// predicated, which keeps the weight requests' waits exact.
 __device__ __forceinline__ void seq_store_row(const SeqStageDesc& S, int row, float v) {
     float* y = S.call[0].y;
     int rb = 0;
@@ -94,7 +106,8 @@ __device__ __forceinline__ void seq_store_row(const SeqStageDesc& S, int row, fl
             rb = S.call[j].row_begin;
         }
     }
-    __hip_atomic_store(y + (row - rb), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store((__attribute__((address_space(1))) float*)(y + (row - rb)), v, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __device__ __forceinline__ unsigned seq_load_word(const unsigned* p) {
@@ -211,6 +224,10 @@ __global__ __launch_bounds__(kWaves * 64, SeqOcc<QT>::waves_per_simd) void gemv_
                     pit += GW;
                 }
             }
+            // Ring slot k holds units k, k + D, k + 2D, ...: a slot is computed,
+            // then refilled in place with the unit D ahead (no register copies,
+            // which would wait for a request just issued).  Full rounds of D
+            // units run without branches; the last round's units are guarded.
             if (S.nch == 1) {
                 // Rows of one chunk: every item of the stage uses the same x pair.
                 const int pp = min(pl, np - 1);
@@ -219,51 +236,55 @@ __global__ __launch_bounds__(kWaves * 64, SeqOcc<QT>::waves_per_simd) void gemv_
                 const float2 c0 = cb[2 * pp];
                 const float2 c1 = cb[2 * pp + 1];
                 const bool active = pl < np;
-                for (int u = 0; u < nu; ++u) {
-                    float acc = active ? PairDot<QT>::run(wq[0], xv, c0, c1, 0.0f, nk) : 0.0f;
-#pragma unroll
-                    for (int i = 0; i + 1 < D; ++i)
-#pragma unroll
-                        for (int j = 0; j < DW; ++j) wq[i][j] = wq[i + 1][j];
-                    if (u + D < nu) seq_load<QT, LPR>(S, pit, 0, slot, pl, wq[D - 1]);
+                auto step = [&](uint32_t (&w)[DW]) {
+                    const float acc = active ? PairDot<QT>::run(w, xv, c0, c1, 0.0f, nk) : 0.0f;
+                    seq_load<QT, LPR>(S, pit, 0, slot, pl, w);  // past the end: clamped, unused
                     pit += GW;
-                    acc = group_sum<LPR>(acc);
-                    const int row = it * SUB + slot;
-                    if (pl == LPR - 1 && row < S.rows) seq_store_row(S, row, acc);
+                    seq_store_row(S, min(it * SUB + slot, S.rows - 1), seq_bcast<LPR>(group_sum<LPR>(acc)));
                     it += GW;
+                };
+                int u = 0;
+                for (; u + D <= nu; u += D) {
+#pragma unroll
+                    for (int k = 0; k < D; ++k) step(wq[k]);
                 }
+#pragma unroll
+                for (int k = 0; k < D; ++k)
+                    if (u + k < nu) step(wq[k]);
             } else {
                 float acc = 0.0f;
-                for (int u = 0; u < nu; ++u) {
+                auto step = [&](uint32_t (&w)[DW]) {
                     const int p = c * LPR + pl;
-                    {
-                        const int pp = min(p, np - 1);
-                        float xv[64];
-                        load_xv(xs4, pp, xv);
-                        const float2 c0 = cb[2 * pp];
-                        const float2 c1 = cb[2 * pp + 1];
-                        if (p < np) acc = PairDot<QT>::run(wq[0], xv, c0, c1, acc, nk);
-                    }
-#pragma unroll
-                    for (int i = 0; i + 1 < D; ++i)
-#pragma unroll
-                        for (int j = 0; j < DW; ++j) wq[i][j] = wq[i + 1][j];
-                    if (u + D < nu) seq_load<QT, LPR>(S, pit, pc, slot, pl, wq[D - 1]);
+                    const int pp = min(p, np - 1);
+                    float xv[64];
+                    load_xv(xs4, pp, xv);
+                    const float2 c0 = cb[2 * pp];
+                    const float2 c1 = cb[2 * pp + 1];
+                    const float a = PairDot<QT>::run(w, xv, c0, c1, acc, nk);
+                    acc = p < np ? a : acc;
+                    seq_load<QT, LPR>(S, pit, pc, slot, pl, w);  // past the end: clamped, unused
                     if (++pc == S.nch) {
                         pc = 0;
                         pit += GW;
                     }
-                    if (c == S.nch - 1) {
-                        const float r = group_sum<LPR>(acc);
-                        acc = 0.0f;
-                        const int row = it * SUB + slot;
-                        if (pl == LPR - 1 && row < S.rows) seq_store_row(S, row, r);
-                    }
+                    // The running row sum is stored after every chunk (the last
+                    // chunk's store is the result; nothing reads y before the
+                    // next barrier), so that no store sits in a branch.
+                    seq_store_row(S, min(it * SUB + slot, S.rows - 1), seq_bcast<LPR>(group_sum<LPR>(acc)));
+                    acc = c == S.nch - 1 ? 0.0f : acc;
                     if (++c == S.nch) {
                         c = 0;
                         it += GW;
                     }
+                };
+                int u = 0;
+                for (; u + D <= nu; u += D) {
+#pragma unroll
+                    for (int k = 0; k < D; ++k) step(wq[k]);
                 }
+#pragma unroll
+                for (int k = 0; k < D; ++k)
+                    if (u + k < nu) step(wq[k]);
             }
         }
         // Arrive before requesting the next stage's weights, so the arrival
