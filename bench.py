@@ -212,11 +212,14 @@ GEMV_CONFIGS = (
 )
 
 
-def gemv_shape_bench(name, qt, m, k, stream, reps_target=400):
+def weight_copies(qt, m, k, seed):
+    """One seeded weight and enough device copies of it that cycling through
+    them streams at least 1 GB (no copy is still in the 256 MB MALL when it is
+    read again)."""
     wbytes = m * ((k + 31) // 32) * BB[qt]
     copies = max(32, math.ceil(1e9 / wbytes))
     tmp = hip.DeviceBuffer(4 * m * k)
-    base = make_weight(qt, m, k, 4242 + m + k + qt, tmp)
+    base = make_weight(qt, m, k, seed, tmp)
     tmp.free()
     bufs = [base._keep]
     for _ in range(copies - 1):
@@ -224,6 +227,11 @@ def gemv_shape_bench(name, qt, m, k, stream, reps_target=400):
         hip.load().mlq_hip_memcpy_dtod(b.ptr, base._keep.ptr, wbytes, None)
         bufs.append(b)
     ws = [hip.Weight.wrap(qt, b, m * ((k + 31) // 32), m, k) for b in bufs]
+    return wbytes, copies, bufs, ws
+
+
+def gemv_shape_bench(name, qt, m, k, stream, reps_target=400):
+    wbytes, copies, bufs, ws = weight_copies(qt, m, k, 4242 + m + k + qt)
     x = hip.DeviceBuffer(4 * k)
     hip.fill_normal(x, k, 99, 0.0, 1.0)
     y = hip.DeviceBuffer(4 * m)
@@ -244,6 +252,57 @@ def gemv_shape_bench(name, qt, m, k, stream, reps_target=400):
     for w in ws:
         w.free()
     for b in bufs:
+        b.free()
+    return res
+
+
+PICK_CONFIGS = ([("c2_qwen_lm_head", qt, 151936, 896) for qt in (hip.Q8_0, hip.Q4_0, hip.Q4_1)] +
+                [("c3_llama_lm_head", qt, 32000, 4096) for qt in (hip.Q8_0, hip.Q4_0, hip.Q4_1)])
+
+
+def pick_shape_bench(name, qt, m, k, stream, reps_target=400):
+    """Greedy decode's last step: the lm_head GEMV with the argmax fused in
+    (mlq_hip_quant_linear_argmax, logits not written) against the plain GEMV
+    that writes the logits for a host argmax.  Both as graphs over the same
+    cycled weight copies; every copy must pick the plain GEMV's argmax."""
+    wbytes, copies, bufs, ws = weight_copies(qt, m, k, 4242 + m + k + qt)
+    x = hip.DeviceBuffer(4 * k)
+    hip.fill_normal(x, k, 99, 0.0, 1.0)
+    y = hip.DeviceBuffer(4 * m)
+    tok = hip.DeviceBuffer(4 * copies)
+    calls = hip.make_calls([(w, x, y, 1) for w in ws])
+    plain = hip.Graph(calls, stream)
+    ws[0].linear_argmax(x, None, tok, stream)  # creates the stream's pick state outside capture
+    hip.synchronize(stream)
+
+    def issue():
+        for i, w in enumerate(ws):
+            hip._check(hip.load().mlq_hip_quant_linear_argmax(w.h, x.ptr, None, tok.ptr + 4 * i, stream))
+
+    picked = hip.Graph.record(issue, stream, keep=(x, tok))
+    loops = max(1, reps_target // copies)
+    plain.launch(stream)
+    picked.launch(stream)
+    ms_plain = time_region(lambda: plain.launch(stream), loops, stream)
+    ms_pick = time_region(lambda: picked.launch(stream), loops, stream)
+    hip.synchronize(stream)
+    want = int(np.argmax(y.download(np.float32)))
+    got = tok.download(np.int32)
+    if not (got == want).all():
+        raise SystemExit(f"{name}: fused pick {sorted(set(got.tolist()))} != argmax of the GEMV's logits {want}")
+    plain.destroy()
+    picked.destroy()
+    n = loops * copies
+    us_plain, us_pick = ms_plain * 1e3 / n, ms_pick * 1e3 / n
+    pick_bytes = wbytes + 4.0 * k  # the pick writes no logits
+    res = {"name": name, "fmt": FMT_NAME[qt], "M": m, "K": k, "copies": copies,
+           "us_gemv_logits": round(us_plain, 3), "us_gemv_argmax": round(us_pick, 3),
+           "gbs_argmax": round(pick_bytes / (us_pick * 1e-6) / 1e9, 1),
+           "frac_of_peak_argmax": round(pick_bytes / (us_pick * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+           "d2h_bytes_per_token": {"logits": 4 * m, "argmax": 4}, "token": want}
+    for w in ws:
+        w.free()
+    for b in bufs + [x, y, tok]:
         b.free()
     return res
 
@@ -385,6 +444,15 @@ def main():
                 f"{r['gbs']:8.1f} GB/s ({100 * r['frac_of_peak']:.1f}%) {r['kernel']}")
             shapes.append(r)
 
+    picks = []
+    if not args.no_shapes:
+        for cfg in PICK_CONFIGS:
+            r = pick_shape_bench(*cfg, stream)
+            log(f"  pick {r['name']:18s} {r['fmt']} {r['M']:>6}x{r['K']:<5} GEMV+logits {r['us_gemv_logits']:7.2f} us, "
+                f"GEMV+argmax {r['us_gemv_argmax']:7.2f} us ({100 * r['frac_of_peak_argmax']:.1f}% of peak), "
+                f"token {r['token']}")
+            picks.append(r)
+
     gemm = []
     if not args.no_shapes:
         for cfg in GEMM_CONFIGS:
@@ -441,6 +509,7 @@ def main():
         "cpu_baseline": cpu,
         "parity": parity,
         "gemv": shapes,
+        "lm_head_argmax": picks,
         "gemm": gemm,
     }
     print(json.dumps(out), flush=True)

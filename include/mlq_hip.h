@@ -133,6 +133,24 @@ int mlq_hip_quant_linear_many(const mlq_linear_call* calls, int n, void* stream)
  * src/forward.cpp:172-227).  Asynchronous on `stream`. */
 int mlq_hip_quant_linear_fused(const mlq_linear_call* calls, int n, void* stream);
 
+/* Greedy pick fused into the decode GEMV of an output projection (lm_head):
+ * y = W x as mlq_hip_quant_linear (bit for bit; y may be NULL when the logits
+ * are not needed) and *token = the first index of the largest y, or -1 when
+ * any y is infinite or NaN.  Replaces downloading the logits
+ * (compute_logits_device, src/forward.cpp:849-853) and picking on the host
+ * (MiniSampler::sample_greedy, src/sampler.cpp:91-95: validate_logits,
+ * src/sampler.cpp:15-24, then argmax, src/ops.cpp:179-192), so greedy decode
+ * moves 4 bytes per token instead of the logits.  x, y and token are device
+ * pointers on the weight's device; asynchronous on `stream`.  Uses a small
+ * per-stream state the library creates on the stream's first call (which
+ * must not be under graph capture); calls on one stream are ordered by it. */
+int mlq_hip_quant_linear_argmax(mlq_weight_t w, const float* x, float* y, int32_t* token, void* stream);
+
+/* Synchronous form: the token is returned to the host.  Fails with
+ * MLQ_ERR_INVALID and the reference's message "sampler: logits must be
+ * finite" when any logit is not finite (src/sampler.cpp:19-22). */
+int mlq_hip_sample_greedy(mlq_weight_t w, const float* x, float* y, int* token, void* stream);
+
 /* Quantize an f32 [rows, row_len] matrix that is already on `device` into
  * blocks on the same device, bit-identical to the reference quantizers:
  * quantize_to_q8_0 / quantize_to_q4_0 (src/quant.cpp:112-170, 207-270) and
@@ -162,6 +180,16 @@ typedef struct mlq_graph_s* mlq_graph_t;
 int mlq_hip_graph_capture_many(const mlq_linear_call* calls, int n, void* stream, mlq_graph_t* out);
 int mlq_hip_graph_launch(mlq_graph_t g, void* stream);
 int mlq_hip_graph_destroy(mlq_graph_t g);
+
+/* Record any asynchronous launches this thread issues on `stream` between
+ * begin and end (mlq_hip_quant_linear with device x/y and MLQ_ASYNC, _many,
+ * _fused, _argmax, sequence launches) as one graph, e.g. a whole decode step.
+ * Calls that synchronize or copy host memory fail under capture, and so does
+ * the first batched or picking call on a stream (it creates the stream's
+ * state): make one of each before capturing.  No counterpart in the
+ * reference, which launches eagerly (src/cuda_quant.cu:289-496). */
+int mlq_hip_graph_begin(int device, void* stream);
+int mlq_hip_graph_end(int device, void* stream, mlq_graph_t* out);
 
 /* A decode step's chain of GEMVs run as one persistent launch (per run of
  * same-format stages).  No counterpart in the reference, whose forward pass

@@ -105,13 +105,64 @@ __device__ __forceinline__ void load_rows(const GemvGroup& g, size_t row_dw, int
     }
 }
 
+// Greedy pick (argmax of y, first index on ties).  A row's key orders by
+// value, then by lower row: the float's bits mapped to an unsigned order
+// (-0 taken as +0, since the two compare equal) above the complemented row.
+// A value that is not finite gives the all-ones key, which decodes to -1.
+__device__ __forceinline__ unsigned long long pick_key(float v, int row) {
+    uint32_t b = __builtin_bit_cast(uint32_t, v);
+    if ((b & 0x7F800000u) == 0x7F800000u) return ~0ull;
+    b = b == 0x80000000u ? 0u : b;
+    const uint32_t ord = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return (static_cast<unsigned long long>(ord) << 32) | static_cast<uint32_t>(~static_cast<uint32_t>(row));
+}
+
+// Folds every lane's key into the launch's result; called once by every
+// thread of every workgroup.  The workgroup's best key goes to its group slot
+// with one atomic max, then the workgroup arrives; the last arrival of the
+// last group swaps the slots back to zero and writes the token.  Atomics are
+// agent-scope and each returns before the next is issued, so every max is
+// performed before the arrival that counts it.  Nothing waits on another
+// workgroup: the launch always drains.
+template <int WAVES>
+__device__ __forceinline__ void pick_finish(PickState* ps, int32_t* token, unsigned long long best) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const unsigned long long other = __shfl_xor(best, o, 64);
+        best = other > best ? other : best;
+    }
+    __shared__ unsigned long long wave_best[WAVES];
+    if ((threadIdx.x & 63) == 0) wave_best[threadIdx.x >> 6] = best;
+    __syncthreads();
+    if (threadIdx.x != 0) return;
+    unsigned long long b = wave_best[0];
+#pragma unroll
+    for (int i = 1; i < WAVES; ++i) b = wave_best[i] > b ? wave_best[i] : b;
+    const unsigned j = blockIdx.x % kPickGroups;
+    const unsigned in_group = (gridDim.x - j + kPickGroups - 1) / kPickGroups;
+    const unsigned groups = gridDim.x < kPickGroups ? gridDim.x : kPickGroups;
+    const unsigned long long before =
+        __hip_atomic_fetch_max(&ps->key[j][0], b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    asm volatile("s_waitcnt vmcnt(0)" ::"v"(before) : "memory");
+    if (__hip_atomic_fetch_add(&ps->sub[j][0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != in_group - 1) return;
+    __hip_atomic_store(&ps->sub[j][0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (__hip_atomic_fetch_add(&ps->top[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != groups - 1) return;
+    __hip_atomic_store(&ps->top[0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    unsigned long long k = 0;
+    for (unsigned i = 0; i < groups; ++i) {
+        const unsigned long long v = __hip_atomic_exchange(&ps->key[i][0], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        k = v > k ? v : k;
+    }
+    *token = k == ~0ull ? -1 : static_cast<int32_t>(~static_cast<uint32_t>(k));
+}
+
 // Waves per SIMD the single kernel's registers are bounded for: four (two
 // workgroups per CU) except Q8_0 with two rows per slot, whose 2 x 17 pair
 // dwords in flight do not fit 128 VGPRs without spilling.
 template <int QT, int R> struct SingleOcc { static constexpr int waves_per_simd = (QT == 1 && R == 2) ? 2 : 4; };
 
 // Rows of at most LPR pairs: x in VGPRs, persistent over row groups.
-template <int QT, int LPR, int R, int WAVES>
+template <int QT, int LPR, int R, int WAVES, bool PICK>
 __global__ __launch_bounds__(WAVES * 64, (SingleOcc<QT, R>::waves_per_simd)) void gemv_single_kernel(
     const GemvGroup g, const float* __restrict__ x, int M, int K, int nb, int groups) {
     constexpr int DW = Fmt<QT>::DW;
@@ -143,6 +194,8 @@ __global__ __launch_bounds__(WAVES * 64, (SingleOcc<QT, R>::waves_per_simd)) voi
     const float2 c0 = cb[2 * p];
     const float2 c1 = cb[2 * p + 1];
     const NibConsts nk = NibConsts::make();
+    const bool store_y = !PICK || g.y[0] != nullptr;
+    unsigned long long best = 0;
 
     for (; gi < groups; gi += gstride) {
         uint32_t wn[R][DW];
@@ -159,7 +212,13 @@ __global__ __launch_bounds__(WAVES * 64, (SingleOcc<QT, R>::waves_per_simd)) voi
             const int row0 = gi * (SUB * R) + slot * R;
 #pragma unroll
             for (int r = 0; r < R; ++r) {
-                if (row0 + r < M) *group_y(g, row0 + r, M, blockIdx.y) = acc[r];
+                if (row0 + r < M) {
+                    if (store_y) *group_y(g, row0 + r, M, blockIdx.y) = acc[r];
+                    if (PICK) {
+                        const unsigned long long k = pick_key(acc[r], row0 + r);
+                        best = k > best ? k : best;
+                    }
+                }
             }
         }
 #pragma unroll
@@ -167,10 +226,11 @@ __global__ __launch_bounds__(WAVES * 64, (SingleOcc<QT, R>::waves_per_simd)) voi
 #pragma unroll
             for (int i = 0; i < DW; ++i) wc[r][i] = wn[r][i];
     }
+    if (PICK) pick_finish<WAVES>(g.pick, g.token, best);
 }
 
 // Rows of more than LPR pairs: one row group per wave, x from LDS per pair.
-template <int QT, int LPR, int R, int WAVES>
+template <int QT, int LPR, int R, int WAVES, bool PICK>
 __global__ __launch_bounds__(WAVES * 64) void gemv_multi_kernel(
     const GemvGroup g, const float* __restrict__ x, int M, int K, int nb) {
     constexpr int DW = Fmt<QT>::DW;
@@ -221,24 +281,35 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_multi_kernel(
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = group_sum<LPR>(acc[r]);
+    unsigned long long best = 0;
     if (pl == LPR - 1) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            if (row0 + r < M) *group_y(g, row0 + r, M, blockIdx.y) = acc[r];
+            if (row0 + r < M) {
+                if (!PICK || g.y[0] != nullptr) *group_y(g, row0 + r, M, blockIdx.y) = acc[r];
+                if (PICK) {
+                    const unsigned long long k = pick_key(acc[r], row0 + r);
+                    best = k > best ? k : best;
+                }
+            }
         }
     }
+    if (PICK) pick_finish<WAVES>(g.pick, g.token, best);
 }
 
 // ---------------------------------------------------------------------------
 // Generic kernel: one wave per output row, lanes over blocks, byte loads.
 // Handles every shape (odd block counts, K beyond the LDS budget).
-template <int QT>
+template <int QT, bool PICK>
 __global__ __launch_bounds__(256) void gemv_generic_kernel(const GemvGroup g, const float* __restrict__ x,
                                                            int M, int K, int nb) {
     constexpr int BB = Fmt<QT>::BB;
     const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    if (row >= M) return;
+    const int wave_row = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // A wave past the last row computes row M-1 again and drops it (every
+    // wave of a picking workgroup has to reach the final fold).
+    const bool live = wave_row < M;
+    const int row = live ? wave_row : M - 1;
     x += static_cast<size_t>(blockIdx.y) * K;
     const int k = group_call(g, row);
     const uint8_t* W = static_cast<const uint8_t*>(g.W[k]) +
@@ -273,7 +344,8 @@ __global__ __launch_bounds__(256) void gemv_generic_kernel(const GemvGroup g, co
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
-    if (lane == 0) *group_y(g, row, M, blockIdx.y) = acc;
+    if (lane == 0 && live && (!PICK || g.y[0] != nullptr)) *group_y(g, row, M, blockIdx.y) = acc;
+    if (PICK) pick_finish<4>(g.pick, g.token, lane == 0 && live ? pick_key(acc, row) : 0ull);
 }
 
 // ---------------------------------------------------------------------------
@@ -301,41 +373,41 @@ PairCfg choose_pair(const LinearShape& s) {
     return PairCfg{Kind::Multi, 16, 1};
 }
 
-template <int QT, int LPR, int R>
+template <int QT, int LPR, int R, bool PICK>
 hipError_t launch_single_t(const LinearShape& s, const GemvGroup& g, const float* x, hipStream_t stream) {
     constexpr int rows_per_group = (64 / LPR) * R;
     const int groups = (s.M + rows_per_group - 1) / rows_per_group;
     int grid = (groups + kWaves - 1) / kWaves;
     if (grid > kPersistentWgs) grid = kPersistentWgs;
-    hipLaunchKernelGGL((gemv_single_kernel<QT, LPR, R, kWaves>), dim3(grid, s.rows), dim3(kWaves * 64),
+    hipLaunchKernelGGL((gemv_single_kernel<QT, LPR, R, kWaves, PICK>), dim3(grid, s.rows), dim3(kWaves * 64),
                        pair_lds_bytes(s.nb), stream, g, x, s.M, s.K, s.nb, groups);
     return hipGetLastError();
 }
 
-template <int QT, int LPR>
+template <int QT, int LPR, bool PICK>
 hipError_t launch_multi_t(const LinearShape& s, const GemvGroup& g, const float* x, hipStream_t stream) {
     constexpr int rows_per_wg = kWaves * (64 / LPR);
     dim3 grid((s.M + rows_per_wg - 1) / rows_per_wg, s.rows);
-    hipLaunchKernelGGL((gemv_multi_kernel<QT, LPR, 1, kWaves>), grid, dim3(kWaves * 64), pair_lds_bytes(s.nb),
+    hipLaunchKernelGGL((gemv_multi_kernel<QT, LPR, 1, kWaves, PICK>), grid, dim3(kWaves * 64), pair_lds_bytes(s.nb),
                        stream, g, x, s.M, s.K, s.nb);
     return hipGetLastError();
 }
 
-template <int QT>
+template <int QT, bool PICK>
 hipError_t launch_q(const LinearShape& s, const PairCfg& c, const GemvGroup& g, const float* x,
                     hipStream_t stream) {
     if (c.kind == Kind::Single) {
-        if (c.lpr == 16) return launch_single_t<QT, 16, 1>(s, g, x, stream);
-        if (c.r == 2) return launch_single_t<QT, 64, 2>(s, g, x, stream);
-        return launch_single_t<QT, 64, 1>(s, g, x, stream);
+        if (c.lpr == 16) return launch_single_t<QT, 16, 1, PICK>(s, g, x, stream);
+        if (c.r == 2) return launch_single_t<QT, 64, 2, PICK>(s, g, x, stream);
+        return launch_single_t<QT, 64, 1, PICK>(s, g, x, stream);
     }
     if (c.kind == Kind::Multi) {
-        if (c.lpr == 64) return launch_multi_t<QT, 64>(s, g, x, stream);
-        if (c.lpr == 32) return launch_multi_t<QT, 32>(s, g, x, stream);
-        return launch_multi_t<QT, 16>(s, g, x, stream);
+        if (c.lpr == 64) return launch_multi_t<QT, 64, PICK>(s, g, x, stream);
+        if (c.lpr == 32) return launch_multi_t<QT, 32, PICK>(s, g, x, stream);
+        return launch_multi_t<QT, 16, PICK>(s, g, x, stream);
     }
     dim3 grid((s.M + 3) / 4, s.rows);
-    hipLaunchKernelGGL((gemv_generic_kernel<QT>), grid, dim3(256), 0, stream, g, x, s.M, s.K, s.nb);
+    hipLaunchKernelGGL((gemv_generic_kernel<QT, PICK>), grid, dim3(256), 0, stream, g, x, s.M, s.K, s.nb);
     return hipGetLastError();
 }
 
@@ -345,9 +417,27 @@ hipError_t launch_gemv_group(const LinearShape& s, const GemvGroup& g, const flo
     if (g.ncalls < 1 || g.ncalls > kGroupMaxCalls) return hipErrorInvalidValue;
     const PairCfg c = choose_pair(s);
     switch (s.qtype) {
-        case 1: return launch_q<1>(s, c, g, x, stream);
-        case 2: return launch_q<2>(s, c, g, x, stream);
-        case 3: return launch_q<3>(s, c, g, x, stream);
+        case 1: return launch_q<1, false>(s, c, g, x, stream);
+        case 2: return launch_q<2, false>(s, c, g, x, stream);
+        case 3: return launch_q<3, false>(s, c, g, x, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_gemv_pick(const LinearShape& s, const void* w, const float* x, float* y, PickState* ps,
+                            int32_t* token, hipStream_t stream) {
+    if (s.rows != 1 || ps == nullptr || token == nullptr) return hipErrorInvalidValue;
+    GemvGroup g{};
+    g.W[0] = w;
+    g.y[0] = y;
+    g.ncalls = 1;
+    g.pick = ps;
+    g.token = token;
+    const PairCfg c = choose_pair(s);
+    switch (s.qtype) {
+        case 1: return launch_q<1, true>(s, c, g, x, stream);
+        case 2: return launch_q<2, true>(s, c, g, x, stream);
+        case 3: return launch_q<3, true>(s, c, g, x, stream);
         default: return hipErrorInvalidValue;
     }
 }

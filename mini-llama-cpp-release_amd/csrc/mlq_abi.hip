@@ -92,6 +92,15 @@ struct Workspace {
     size_t bytes;
 };
 
+// Greedy-pick state of one stream (created on the stream's first pick call,
+// kept until the process ends): the fold words, zero between launches, and
+// the token word the synchronous entry reads back.
+struct PickSlot {
+    hipStream_t stream;
+    mlq::PickState* state;
+    int32_t* token;
+};
+
 struct DeviceState {
     std::once_flag once;
     hipError_t init_err = hipSuccess;
@@ -99,8 +108,9 @@ struct DeviceState {
     std::mutex mu;             // guards the host-pointer staging buffers
     void* stage = nullptr;     // x and y staging for host-pointer calls
     size_t stage_bytes = 0;
-    std::mutex ws_mu;          // guards the GEMM workspaces
+    std::mutex ws_mu;          // guards the GEMM workspaces and the pick states
     std::vector<Workspace> ws;
+    std::vector<PickSlot> picks;
 };
 
 DeviceState g_dev[kMaxDevices];
@@ -209,6 +219,34 @@ int validate_linear(int qtype, int M, int K, size_t n_blocks, int rows) {
     return MLQ_OK;
 }
 
+// Ends the capture on `s` and instantiates what it recorded; a failed launch
+// inside the capture (launch_rc) discards the graph.
+int end_capture(hipStream_t s, int device, int launch_rc, mlq_graph_t* out) {
+    hipGraph_t graph = nullptr;
+    hipError_t end_err = hipStreamEndCapture(s, &graph);
+    if (launch_rc != MLQ_OK) {
+        if (graph) (void)hipGraphDestroy(graph);
+        return launch_rc;
+    }
+    if (end_err != hipSuccess) {
+        if (graph) (void)hipGraphDestroy(graph);
+        return hip_fail(end_err, "hipStreamEndCapture");
+    }
+    hipGraphExec_t exec = nullptr;
+    hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        (void)hipGraphDestroy(graph);
+        return hip_fail(e, "hipGraphInstantiate");
+    }
+    *out = new mlq_graph_s{graph, exec, device};
+    return MLQ_OK;
+}
+
+bool capturing(hipStream_t s) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    return hipStreamIsCapturing(s, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
+}
+
 // Returns a workspace of at least `bytes` for `stream` on `device`.  Growing
 // waits for the stream first so a buffer is never freed under a running kernel.
 int stream_workspace(int device, hipStream_t stream, size_t bytes, void** out) {
@@ -217,6 +255,10 @@ int stream_workspace(int device, hipStream_t stream, size_t bytes, void** out) {
     for (Workspace& w : st.ws) {
         if (w.stream != stream) continue;
         if (w.bytes < bytes) {
+            if (capturing(stream)) {
+                return fail(MLQ_ERR_INVALID, "the stream's batched-call workspace must grow, which cannot happen "
+                                             "under graph capture: make the largest batched call once first");
+            }
             MLQ_HIP_CHECK(hipStreamSynchronize(stream));
             MLQ_HIP_CHECK(hipFree(w.ptr));
             w.ptr = nullptr;
@@ -230,10 +272,38 @@ int stream_workspace(int device, hipStream_t stream, size_t bytes, void** out) {
         *out = w.ptr;
         return MLQ_OK;
     }
+    if (capturing(stream)) {
+        return fail(MLQ_ERR_INVALID, "the stream's batched-call workspace is created by a first call outside "
+                                     "graph capture");
+    }
     void* p = nullptr;
     MLQ_HIP_CHECK(hipMalloc(&p, bytes));
     MLQ_HIP_CHECK(hipMemsetAsync(p, 0, bytes, stream));
     st.ws.push_back(Workspace{stream, p, bytes});
+    *out = p;
+    return MLQ_OK;
+}
+
+int stream_pick(int device, hipStream_t stream, const char* caller, PickSlot* out) {
+    DeviceState& st = g_dev[device];
+    std::lock_guard<std::mutex> lock(st.ws_mu);
+    for (const PickSlot& p : st.picks) {
+        if (p.stream == stream) {
+            *out = p;
+            return MLQ_OK;
+        }
+    }
+    if (capturing(stream)) {
+        return fail(MLQ_ERR_INVALID, std::string(caller) +
+                                         ": the stream's pick state is created by a first call outside graph capture");
+    }
+    void* mem = nullptr;
+    const size_t bytes = sizeof(mlq::PickState) + 128;
+    MLQ_HIP_CHECK(hipMalloc(&mem, bytes));
+    MLQ_HIP_CHECK(hipMemsetAsync(mem, 0, bytes, stream));
+    PickSlot p{stream, static_cast<mlq::PickState*>(mem),
+               reinterpret_cast<int32_t*>(static_cast<char*>(mem) + sizeof(mlq::PickState))};
+    st.picks.push_back(p);
     *out = p;
     return MLQ_OK;
 }
@@ -537,6 +607,59 @@ int mlq_hip_quant_linear_fused(const mlq_linear_call* calls, int n, void* stream
     return MLQ_OK;
 }
 
+namespace {
+
+// Shared front of the two greedy-pick entries: validates, then launches the
+// picking GEMV with the token going to `token` (or to the stream's own word
+// when `token` is null).
+int launch_pick(mlq_weight_t w, const float* x, float* y, int32_t* token, void* stream, PickSlot* slot,
+                hipStream_t* used) {
+    if (w == nullptr) return fail(MLQ_ERR_INVALID, "hip_quant_linear_argmax: null weight handle");
+    const char* caller = caller_for(w->qtype);
+    if (x == nullptr) return fail(MLQ_ERR_INVALID, std::string(caller) + ": input pointer is null");
+    int rc = validate_linear(w->qtype, w->M, w->K, w->n_blocks, 1);
+    if (rc != MLQ_OK) return rc;
+    if ((rc = ensure_device(w->device)) != MLQ_OK) return rc;
+    const size_t xb = static_cast<size_t>(w->K) * sizeof(float);
+    const size_t yb = static_cast<size_t>(w->M) * sizeof(float);
+    if ((rc = check_device_ptr(x, w->device, caller, "input", xb)) != MLQ_OK) return rc;
+    if (y != nullptr && (rc = check_device_ptr(y, w->device, caller, "output", yb)) != MLQ_OK) return rc;
+    if (token != nullptr && (rc = check_device_ptr(token, w->device, caller, "token", sizeof(int32_t))) != MLQ_OK) {
+        return rc;
+    }
+    const hipStream_t s = resolve_stream(w->device, stream);
+    if ((rc = stream_pick(w->device, s, caller, slot)) != MLQ_OK) return rc;
+    const mlq::LinearShape shape{w->qtype, w->M, w->K, w->nb, 1};
+    const hipError_t e =
+        mlq::launch_gemv_pick(shape, w->ptr, x, y, slot->state, token != nullptr ? token : slot->token, s);
+    if (e != hipSuccess) return hip_fail(e, caller);
+    *used = s;
+    return MLQ_OK;
+}
+
+}  // namespace
+
+int mlq_hip_quant_linear_argmax(mlq_weight_t w, const float* x, float* y, int32_t* token, void* stream) {
+    if (token == nullptr) return fail(MLQ_ERR_INVALID, "hip_quant_linear_argmax: token pointer is null");
+    PickSlot slot{};
+    hipStream_t s = nullptr;
+    return launch_pick(w, x, y, token, stream, &slot, &s);
+}
+
+int mlq_hip_sample_greedy(mlq_weight_t w, const float* x, float* y, int* token, void* stream) {
+    if (token == nullptr) return fail(MLQ_ERR_INVALID, "hip_sample_greedy: token pointer is null");
+    PickSlot slot{};
+    hipStream_t s = nullptr;
+    int rc = launch_pick(w, x, y, nullptr, stream, &slot, &s);
+    if (rc != MLQ_OK) return rc;
+    int32_t t = -1;
+    MLQ_HIP_CHECK(hipMemcpyAsync(&t, slot.token, sizeof t, hipMemcpyDeviceToHost, s));
+    MLQ_HIP_CHECK(hipStreamSynchronize(s));
+    if (t < 0) return fail(MLQ_ERR_INVALID, "sampler: logits must be finite");
+    *token = t;
+    return MLQ_OK;
+}
+
 int mlq_hip_quantize(int device, int qtype, const float* src, int rows, int row_len,
                      void* device_blocks, void* stream) {
     if (qtype != MLQ_Q8_0 && qtype != MLQ_Q4_0 && qtype != MLQ_Q4_1) {
@@ -711,21 +834,7 @@ int mlq_hip_graph_capture_many(const mlq_linear_call* calls, int n, void* stream
         mlq::LinearShape shape{c.w->qtype, c.w->M, c.w->K, c.w->nb, c.rows};
         launch_rc = dispatch(device, shape, c.w->ptr, c.x, c.y, s);
     }
-    hipGraph_t graph = nullptr;
-    hipError_t end_err = hipStreamEndCapture(s, &graph);
-    if (launch_rc != MLQ_OK) {
-        if (graph) (void)hipGraphDestroy(graph);
-        return launch_rc;
-    }
-    if (end_err != hipSuccess) return hip_fail(end_err, "hipStreamEndCapture");
-    hipGraphExec_t exec = nullptr;
-    hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
-    if (e != hipSuccess) {
-        (void)hipGraphDestroy(graph);
-        return hip_fail(e, "hipGraphInstantiate");
-    }
-    *out = new mlq_graph_s{graph, exec, device};
-    return MLQ_OK;
+    return end_capture(s, device, launch_rc, out);
 }
 
 int mlq_hip_graph_launch(mlq_graph_t g, void* stream) {
@@ -742,6 +851,21 @@ int mlq_hip_graph_destroy(mlq_graph_t g) {
     if (g->graph) (void)hipGraphDestroy(g->graph);
     delete g;
     return MLQ_OK;
+}
+
+int mlq_hip_graph_begin(int device, void* stream) {
+    int rc = ensure_device(device);
+    if (rc != MLQ_OK) return rc;
+    MLQ_HIP_CHECK(hipStreamBeginCapture(resolve_stream(device, stream), hipStreamCaptureModeThreadLocal));
+    return MLQ_OK;
+}
+
+int mlq_hip_graph_end(int device, void* stream, mlq_graph_t* out) {
+    if (out == nullptr) return fail(MLQ_ERR_INVALID, "mlq_hip_graph_end: null output");
+    *out = nullptr;
+    int rc = ensure_device(device);
+    if (rc != MLQ_OK) return rc;
+    return end_capture(resolve_stream(device, stream), device, MLQ_OK, out);
 }
 
 int mlq_hip_fill_normal(float* device_dst, size_t n, uint64_t seed, float mean, float stddev,
@@ -1056,21 +1180,7 @@ int mlq_hip_graph_capture_sequence(mlq_sequence_t seq, void* stream, mlq_graph_t
     hipStream_t s = resolve_stream(seq->device, stream);
     MLQ_HIP_CHECK(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
     const int launch_rc = mlq_hip_sequence_launch(seq, s);
-    hipGraph_t graph = nullptr;
-    hipError_t end_err = hipStreamEndCapture(s, &graph);
-    if (launch_rc != MLQ_OK) {
-        if (graph) (void)hipGraphDestroy(graph);
-        return launch_rc;
-    }
-    if (end_err != hipSuccess) return hip_fail(end_err, "hipStreamEndCapture");
-    hipGraphExec_t exec = nullptr;
-    hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
-    if (e != hipSuccess) {
-        (void)hipGraphDestroy(graph);
-        return hip_fail(e, "hipGraphInstantiate");
-    }
-    *out = new mlq_graph_s{graph, exec, seq->device};
-    return MLQ_OK;
+    return end_capture(s, seq->device, launch_rc, out);
 }
 
 }  // extern "C"

@@ -41,14 +41,36 @@ const char* gemv_kernel_name(const LinearShape& s);
 // computed exactly as by a launch of its own call.
 constexpr int kGroupMaxCalls = 4;
 
+struct PickState;
+
 struct GemvGroup {
     const void* W[kGroupMaxCalls];
     float* y[kGroupMaxCalls];
     int row_begin[kGroupMaxCalls];
     int ncalls;
+    PickState* pick;  // greedy-pick launches only (launch_gemv_pick)
+    int32_t* token;
 };
 
 hipError_t launch_gemv_group(const LinearShape& s, const GemvGroup& g, const float* x, hipStream_t stream);
+
+// Greedy pick fused into the GEMV (one call, rows == 1): besides y (skipped
+// when y is null) the launch writes *token = the first index of the largest
+// y, or -1 when any y is not finite.  Workgroup b folds its best key into
+// key[b % kPickGroups] and arrives on sub[b % kPickGroups]; the last arrival
+// of a group bumps `top`, and the last of those decodes the token.  Every
+// word is zero before a launch and left at zero by it; launches that share a
+// PickState must not overlap in time.
+constexpr int kPickGroups = 8;
+
+struct PickState {
+    unsigned long long key[kPickGroups][16];  // one 128-byte line each
+    unsigned sub[kPickGroups][32];
+    unsigned top[32];
+};
+
+hipError_t launch_gemv_pick(const LinearShape& s, const void* w, const float* x, float* y, PickState* ps,
+                            int32_t* token, hipStream_t stream);
 
 // Batched prefill GEMM for rows > 1 (MFMA).  Needs a device workspace of
 // gemm_workspace_bytes(s) bytes (split x, scales, split-K partials) that no

@@ -60,6 +60,8 @@ _SIGS = {
                                                     ctypes.c_int, ctypes.c_int, _vp, ctypes.c_int, _vp, _vp]),
     "mlq_hip_quant_linear_many": (ctypes.c_int, [ctypes.POINTER(LinearCall), ctypes.c_int, _vp]),
     "mlq_hip_quant_linear_fused": (ctypes.c_int, [ctypes.POINTER(LinearCall), ctypes.c_int, _vp]),
+    "mlq_hip_quant_linear_argmax": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp]),
+    "mlq_hip_sample_greedy": (ctypes.c_int, [_vp, _vp, _vp, ctypes.POINTER(ctypes.c_int), _vp]),
     "mlq_hip_quantize": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, _vp, ctypes.c_int, ctypes.c_int, _vp, _vp]),
     "mlq_hip_malloc": (ctypes.c_int, [ctypes.c_int, ctypes.c_size_t, ctypes.POINTER(_vp)]),
     "mlq_hip_free": (ctypes.c_int, [_vp]),
@@ -77,6 +79,8 @@ _SIGS = {
                                                    ctypes.POINTER(_vp)]),
     "mlq_hip_graph_launch": (ctypes.c_int, [_vp, _vp]),
     "mlq_hip_graph_destroy": (ctypes.c_int, [_vp]),
+    "mlq_hip_graph_begin": (ctypes.c_int, [ctypes.c_int, _vp]),
+    "mlq_hip_graph_end": (ctypes.c_int, [ctypes.c_int, _vp, ctypes.POINTER(_vp)]),
     "mlq_hip_sequence_create": (ctypes.c_int, [ctypes.POINTER(LinearCall), ctypes.c_int,
                                                 ctypes.POINTER(ctypes.c_int), ctypes.c_int, ctypes.POINTER(_vp)]),
     "mlq_hip_sequence_launch": (ctypes.c_int, [_vp, _vp]),
@@ -227,6 +231,19 @@ class Weight:
         flags = X_ON_DEVICE | Y_ON_DEVICE | (0 if sync else ASYNC)
         _check(_LIB.mlq_hip_quant_linear(self.h, x.ptr, rows, y.ptr, flags, stream))
 
+    def linear_argmax(self, x: DeviceBuffer, y: "DeviceBuffer | None", token: DeviceBuffer,
+                      stream=None) -> None:
+        """y = W x (skipped when y is None) and token[0] = first argmax of y, or -1
+        when a logit is not finite; asynchronous (mlq_hip_quant_linear_argmax)."""
+        _check(_LIB.mlq_hip_quant_linear_argmax(self.h, x.ptr, None if y is None else y.ptr, token.ptr, stream))
+
+    def sample_greedy(self, x: DeviceBuffer, y: "DeviceBuffer | None" = None, stream=None) -> int:
+        """Greedy token of the logits W x, returned to the host (mlq_hip_sample_greedy);
+        raises MlqError("sampler: logits must be finite") like the reference sampler."""
+        t = ctypes.c_int(-1)
+        _check(_LIB.mlq_hip_sample_greedy(self.h, x.ptr, None if y is None else y.ptr, ctypes.byref(t), stream))
+        return t.value
+
     def free(self) -> None:
         if getattr(self, "h", None):
             _LIB.mlq_hip_free_weight(self.h)
@@ -336,6 +353,25 @@ class Graph:
         self.h = h.value
         self._arr = arr
         self._seq = sequence
+
+    @classmethod
+    def record(cls, fn, stream=None, device: int = 0, keep=None) -> "Graph":
+        """Capture whatever ``fn()`` launches asynchronously on ``stream``
+        (mlq_hip_graph_begin / mlq_hip_graph_end); ``keep`` holds objects the
+        graph's launches use."""
+        lib = load()
+        _check(lib.mlq_hip_graph_begin(device, stream))
+        h = _vp()
+        try:
+            fn()
+        except BaseException:
+            if lib.mlq_hip_graph_end(device, stream, ctypes.byref(h)) == 0 and h.value:
+                lib.mlq_hip_graph_destroy(h.value)
+            raise
+        _check(lib.mlq_hip_graph_end(device, stream, ctypes.byref(h)))
+        g = cls.__new__(cls)
+        g.h, g._arr, g._seq = h.value, keep, None
+        return g
 
     def launch(self, stream=None) -> None:
         _check(_LIB.mlq_hip_graph_launch(self.h, stream))
