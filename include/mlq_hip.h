@@ -239,6 +239,43 @@ int mlq_hip_fill_normal(float* device_dst, size_t n, uint64_t seed, float mean, 
 int mlq_hip_kernel_name(int qtype, int rows, int out_features, int in_features, char* buf,
                         size_t len);
 
+/* ---- GGUF ingest: quantized linear weights straight from a model file ----
+ * The file is memory-mapped read-only and indexed once; a weight's raw block
+ * bytes go from the mapping to device memory without an intermediate host
+ * copy of the tensor (the reference reads each tensor into a std::vector,
+ * read_gguf_tensor_raw, src/gguf.cpp:586-622, copies it into a
+ * QuantizedTensor, load_quantized_tensor, src/gguf_loader.cpp:110-184, and
+ * then uploads, src/model.cpp:145-272).  Block layouts are ggml's, so real
+ * llama.cpp files load unchanged. */
+typedef struct mlq_gguf_s* mlq_gguf_t;
+
+/* Map and parse `path` (GGUFReader::load, src/gguf.cpp:371-530): version 3
+ * only, the reader's limits, data section aligned to general.alignment
+ * (default 32).  On failure the message is the reader's load_error. */
+int mlq_hip_gguf_open(const char* path, mlq_gguf_t* out);
+int mlq_hip_gguf_close(mlq_gguf_t g);
+/* GGUFReader's version, n_tensors, n_metadata and data_offset (any may be NULL). */
+int mlq_hip_gguf_header(mlq_gguf_t g, uint32_t* version, uint64_t* n_tensors, uint64_t* n_metadata,
+                        uint64_t* data_offset);
+/* Metadata entry i: key, GGUF value type and value rendered as
+ * GGUFMetadataKV::value_str (include/mini_llama/gguf.h:55-59).  Buffers too
+ * small give MLQ_ERR_LIMIT; NULL buffers are skipped. */
+int mlq_hip_gguf_metadata(mlq_gguf_t g, uint64_t i, char* key, size_t key_cap, uint32_t* type, char* value,
+                          size_t value_cap);
+/* Tensor i (GGUFTensorInfo, include/mini_llama/gguf.h:46-51): name, dims
+ * (ne0 first, 8 slots, unused ones 0), GGML type, offset in the data section
+ * and data bytes (gguf_tensor_data_size; 0 for types without a known size). */
+int mlq_hip_gguf_tensor(mlq_gguf_t g, uint64_t i, char* name, size_t name_cap, uint32_t* n_dims, uint64_t* dims,
+                        uint32_t* ggml_type, uint64_t* offset, uint64_t* nbytes);
+/* Index of the tensor named `name` ("Missing tensor: NAME" otherwise). */
+int mlq_hip_gguf_find(mlq_gguf_t g, const char* name, uint64_t* index);
+/* Host pointer to tensor i's bytes inside the mapping (valid until close). */
+int mlq_hip_gguf_tensor_data(mlq_gguf_t g, uint64_t i, const void** data, uint64_t* nbytes);
+/* Upload the 2-D Q8_0 / Q4_0 / Q4_1 tensor `name` ([ne0 = in, ne1 = out])
+ * to `device` as a weight handle owning its memory, byte for byte.
+ * Validation messages follow the upload's (src/model.cpp:145-272). */
+int mlq_hip_gguf_upload_weight(mlq_gguf_t g, const char* name, int device, mlq_weight_t* out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -6,6 +6,7 @@
 // replaced by "hip".  Every check runs on the host before any launch, so a
 // malformed call never reaches a kernel.
 
+#include "gguf_index.h"
 #include "mlq_kernels.h"
 
 #include "../../include/mlq_hip.h"
@@ -28,6 +29,10 @@ struct mlq_weight_s {
     size_t n_blocks;
     void* ptr;
     bool owned;
+};
+
+struct mlq_gguf_s {
+    mlq::GgufIndex index;
 };
 
 struct mlq_graph_s {
@@ -111,6 +116,9 @@ struct DeviceState {
     std::mutex ws_mu;          // guards the GEMM workspaces and the pick states
     std::vector<Workspace> ws;
     std::vector<PickSlot> picks;
+    std::mutex pin_mu;         // guards the pinned stage of file uploads
+    void* pin[2] = {nullptr, nullptr};
+    hipEvent_t pin_done[2] = {nullptr, nullptr};
 };
 
 DeviceState g_dev[kMaxDevices];
@@ -1168,6 +1176,171 @@ int mlq_hip_sequence_destroy(mlq_sequence_t seq) {
     }
     delete seq;
     if (e != hipSuccess) return hip_fail(e, "mlq_hip_sequence_destroy");
+    return MLQ_OK;
+}
+
+namespace {
+
+constexpr size_t kPinChunk = size_t(16) << 20;
+
+// Copies `bytes` from host memory that is not pinned (a file mapping) into
+// device memory: 16 MiB pieces go through two pinned buffers in turn, so the
+// host copy of one piece overlaps the DMA of the other.  Synchronous.
+int upload_from_host(int device, void* dst, const uint8_t* src, uint64_t bytes) {
+    DeviceState& st = g_dev[device];
+    std::lock_guard<std::mutex> lock(st.pin_mu);
+    for (int b = 0; b < 2; ++b) {
+        if (st.pin[b] == nullptr) {
+            MLQ_HIP_CHECK(hipHostMalloc(&st.pin[b], kPinChunk, hipHostMallocDefault));
+            MLQ_HIP_CHECK(hipEventCreateWithFlags(&st.pin_done[b], hipEventDisableTiming));
+        }
+    }
+    const hipStream_t s = st.stream;
+    uint64_t k = 0;
+    for (uint64_t off = 0; off < bytes; off += kPinChunk, ++k) {
+        const int b = static_cast<int>(k & 1);
+        const size_t n = static_cast<size_t>(std::min<uint64_t>(kPinChunk, bytes - off));
+        if (k >= 2) MLQ_HIP_CHECK(hipEventSynchronize(st.pin_done[b]));
+        std::memcpy(st.pin[b], src + off, n);
+        MLQ_HIP_CHECK(hipMemcpyAsync(static_cast<char*>(dst) + off, st.pin[b], n, hipMemcpyHostToDevice, s));
+        MLQ_HIP_CHECK(hipEventRecord(st.pin_done[b], s));
+    }
+    MLQ_HIP_CHECK(hipStreamSynchronize(s));
+    return MLQ_OK;
+}
+
+int copy_out(const std::string& v, char* buf, size_t cap, const char* caller, const char* what) {
+    if (buf == nullptr) return MLQ_OK;
+    if (v.size() + 1 > cap) {
+        return fail(MLQ_ERR_LIMIT, std::string(caller) + ": " + what + " needs " + std::to_string(v.size() + 1) +
+                                       " bytes, the buffer holds " + std::to_string(cap));
+    }
+    std::memcpy(buf, v.c_str(), v.size() + 1);
+    return MLQ_OK;
+}
+
+}  // namespace
+
+int mlq_hip_gguf_open(const char* path, mlq_gguf_t* out) {
+    if (out == nullptr) return fail(MLQ_ERR_INVALID, "mlq_hip_gguf_open: null output");
+    *out = nullptr;
+    if (path == nullptr) return fail(MLQ_ERR_INVALID, "mlq_hip_gguf_open: null path");
+    mlq_gguf_t g = new mlq_gguf_s;
+    if (!g->index.open(path)) {
+        const std::string msg = g->index.error;
+        delete g;
+        return fail(MLQ_ERR_INVALID, msg);
+    }
+    *out = g;
+    return MLQ_OK;
+}
+
+int mlq_hip_gguf_close(mlq_gguf_t g) {
+    delete g;
+    return MLQ_OK;
+}
+
+int mlq_hip_gguf_header(mlq_gguf_t g, uint32_t* version, uint64_t* n_tensors, uint64_t* n_metadata,
+                        uint64_t* data_offset) {
+    if (g == nullptr) return fail(MLQ_ERR_INVALID, "mlq_hip_gguf_header: null file");
+    if (version) *version = g->index.version;
+    if (n_tensors) *n_tensors = g->index.n_tensors;
+    if (n_metadata) *n_metadata = g->index.n_metadata;
+    if (data_offset) *data_offset = g->index.data_offset;
+    return MLQ_OK;
+}
+
+int mlq_hip_gguf_metadata(mlq_gguf_t g, uint64_t i, char* key, size_t key_cap, uint32_t* type, char* value,
+                          size_t value_cap) {
+    static const char* caller = "mlq_hip_gguf_metadata";
+    if (g == nullptr) return fail(MLQ_ERR_INVALID, std::string(caller) + ": null file");
+    if (i >= g->index.metadata.size()) return fail(MLQ_ERR_INVALID, std::string(caller) + ": index out of range");
+    const mlq::GgufMeta& m = g->index.metadata[i];
+    int rc = copy_out(m.key, key, key_cap, caller, "key");
+    if (rc == MLQ_OK) rc = copy_out(m.value, value, value_cap, caller, "value");
+    if (rc == MLQ_OK && type) *type = m.type;
+    return rc;
+}
+
+int mlq_hip_gguf_tensor(mlq_gguf_t g, uint64_t i, char* name, size_t name_cap, uint32_t* n_dims, uint64_t* dims,
+                        uint32_t* ggml_type, uint64_t* offset, uint64_t* nbytes) {
+    static const char* caller = "mlq_hip_gguf_tensor";
+    if (g == nullptr) return fail(MLQ_ERR_INVALID, std::string(caller) + ": null file");
+    if (i >= g->index.tensors.size()) return fail(MLQ_ERR_INVALID, std::string(caller) + ": index out of range");
+    const mlq::GgufTensor& t = g->index.tensors[i];
+    int rc = copy_out(t.name, name, name_cap, caller, "name");
+    if (rc != MLQ_OK) return rc;
+    if (n_dims) *n_dims = static_cast<uint32_t>(t.dims.size());
+    if (dims) {
+        for (size_t d = 0; d < 8; ++d) dims[d] = d < t.dims.size() ? t.dims[d] : 0;
+    }
+    if (ggml_type) *ggml_type = t.type;
+    if (offset) *offset = t.offset;
+    if (nbytes) *nbytes = t.nbytes;
+    return MLQ_OK;
+}
+
+int mlq_hip_gguf_find(mlq_gguf_t g, const char* name, uint64_t* index) {
+    if (g == nullptr || name == nullptr || index == nullptr) {
+        return fail(MLQ_ERR_INVALID, "mlq_hip_gguf_find: null argument");
+    }
+    const int64_t i = g->index.find(name);
+    if (i < 0) return fail(MLQ_ERR_INVALID, std::string("Missing tensor: ") + name);
+    *index = static_cast<uint64_t>(i);
+    return MLQ_OK;
+}
+
+int mlq_hip_gguf_tensor_data(mlq_gguf_t g, uint64_t i, const void** data, uint64_t* nbytes) {
+    if (g == nullptr || data == nullptr) return fail(MLQ_ERR_INVALID, "mlq_hip_gguf_tensor_data: null argument");
+    if (i >= g->index.tensors.size()) return fail(MLQ_ERR_INVALID, "mlq_hip_gguf_tensor_data: index out of range");
+    const mlq::GgufTensor& t = g->index.tensors[i];
+    *data = g->index.tensor_data(t);
+    if (nbytes) *nbytes = t.nbytes;
+    return MLQ_OK;
+}
+
+int mlq_hip_gguf_upload_weight(mlq_gguf_t g, const char* name, int device, mlq_weight_t* out) {
+    if (out == nullptr) return fail(MLQ_ERR_INVALID, "HIP weight upload: null output handle");
+    *out = nullptr;
+    if (g == nullptr || name == nullptr) return fail(MLQ_ERR_INVALID, "mlq_hip_gguf_upload_weight: null argument");
+    const int64_t i = g->index.find(name);
+    if (i < 0) return fail(MLQ_ERR_INVALID, std::string("Missing tensor: ") + name);
+    const mlq::GgufTensor& t = g->index.tensors[static_cast<size_t>(i)];
+    int qtype = 0;
+    switch (t.type) {
+        case mlq::kGgmlQ8_0: qtype = MLQ_Q8_0; break;
+        case mlq::kGgmlQ4_0: qtype = MLQ_Q4_0; break;
+        case mlq::kGgmlQ4_1: qtype = MLQ_Q4_1; break;
+        default:
+            return fail(MLQ_ERR_INVALID, std::string("HIP weight upload: ") + name + " is " +
+                                             mlq::ggml_type_label(t.type) +
+                                             "; only Q8_0, Q4_0 and Q4_1 linear weights are uploaded");
+    }
+    // A 2-D tensor [ne0, ne1] holds ne1 rows of ne0 values: W is [out = ne1, in = ne0].
+    if (t.dims.size() != 2 || t.dims[0] > static_cast<uint64_t>(INT32_MAX) ||
+        t.dims[1] > static_cast<uint64_t>(INT32_MAX)) {
+        return fail(MLQ_ERR_SHAPE, std::string("HIP weight upload: expected 2D ") + type_name(qtype) + " weight");
+    }
+    const int M = static_cast<int>(t.dims[1]);
+    const int K = static_cast<int>(t.dims[0]);
+    const size_t bb = static_cast<size_t>(mlq::block_bytes(qtype));
+    const size_t n_blocks = static_cast<size_t>(t.nbytes / bb);
+    const int nb = (K + mlq::kQK - 1) / mlq::kQK;
+    const size_t expected = static_cast<size_t>(M) * nb;
+    if (n_blocks != expected) {
+        return fail(MLQ_ERR_SHAPE, std::string("HIP weight upload: ") + type_name(qtype) +
+                                       " block count mismatch, expected " + std::to_string(expected) + ", got " +
+                                       std::to_string(n_blocks));
+    }
+    int rc = ensure_device(device);
+    if (rc != MLQ_OK) return rc;
+    void* ptr = nullptr;
+    MLQ_HIP_CHECK(hipMalloc(&ptr, t.nbytes));
+    if ((rc = upload_from_host(device, ptr, g->index.tensor_data(t), t.nbytes)) != MLQ_OK) {
+        (void)hipFree(ptr);
+        return rc;
+    }
+    *out = new mlq_weight_s{device, qtype, M, K, nb, n_blocks, ptr, true};
     return MLQ_OK;
 }
 

@@ -64,4 +64,11 @@ HipUploadedWeight hip_upload_linear_weight(const QuantizedTensor& weight, const 
 // forward_linear_device-style dispatch on an uploaded weight (src/forward.cpp:172-227).
 HipTensor hip_linear_device(const HipTensor& x, const HipUploadedWeight& w, int device_id = 0);
 
+// Greedy token of the logits w . x without downloading them: the output
+// projection of compute_logits_device (src/forward.cpp:849-853) followed by
+// MiniSampler::sample_greedy (src/sampler.cpp:91-95), i.e. the first index of
+// the largest logit.  x is [in_features] on the device.  Throws the sampler's
+// "sampler: logits must be finite" when a logit is infinite or NaN.
+int hip_sample_greedy_device(const HipTensor& x, const HipUploadedWeight& w, int device_id = 0);
+
 }  // namespace mlq

@@ -194,6 +194,29 @@ HipUploadedWeight hip_upload_linear_weight(const QuantizedTensor& weight, const 
     return up;
 }
 
+int hip_sample_greedy_device(const HipTensor& x, const HipUploadedWeight& w, int device_id) {
+    if (w.type != QuantType::Q8_0 && w.type != QuantType::Q4_0 && w.type != QuantType::Q4_1) {
+        throw std::runtime_error("HIP greedy sampling unsupported weight type: " + w.name);
+    }
+    const char* caller = caller_of(w.type);
+    if (x.ndim() != 1) {
+        throw std::runtime_error(std::string(caller) + ": greedy sampling expects x shape [in_features], got " +
+                                 x.shape_str());
+    }
+    validate_shape(x.shape(), x.shape_str(), w.shape, w.block_count, caller);
+    const int qtype = w.type == QuantType::Q8_0 ? MLQ_Q8_0 : w.type == QuantType::Q4_0 ? MLQ_Q4_0 : MLQ_Q4_1;
+    mlq_weight_t h = nullptr;
+    if (mlq_hip_wrap_weight(device_id, qtype, w.buffer.data(), w.block_count, w.shape[0], w.shape[1], &h) != MLQ_OK) {
+        throw_abi(caller);
+    }
+    int token = -1;
+    const int rc = mlq_hip_sample_greedy(h, static_cast<const float*>(x.data()), nullptr, &token, nullptr);
+    const std::string msg = rc == MLQ_OK ? std::string() : std::string(mlq_hip_last_error());
+    mlq_hip_free_weight(h);
+    if (rc != MLQ_OK) throw std::runtime_error(msg);
+    return token;
+}
+
 HipTensor hip_linear_device(const HipTensor& x, const HipUploadedWeight& w, int device_id) {
     switch (w.type) {
         case QuantType::Q8_0:

@@ -14,6 +14,7 @@
 #include <cmath>
 #include <cstring>
 #include <iostream>
+#include <limits>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -193,6 +194,37 @@ void test_forms() {
         threw = std::string(e.what()).find("HIP weight upload: Q4_0 block count mismatch for layers.0.wk") == 0;
     }
     require(threw, "upload block count message");
+
+    // Greedy sampling on the device (compute_logits_device + sample_greedy):
+    // the first maximum of the logits, and the sampler's error on Inf/NaN.
+    Tensor wl = pattern({1000, 4096}, 0.0009f, 0.0003f);
+    QuantizedTensor lm;
+    lm.type = QuantType::Q4_0;
+    lm.shape = wl.shape;
+    lm.q4_0_data = quantize<BlockQ4_0>(QuantType::Q4_0, wl);
+    HipUploadedWeight lmw = hip_upload_linear_weight(lm, "lm_head", 0);
+    Tensor logits = hip_linear_device(xd, lmw, 0).download();
+    int first_max = 0;
+    for (size_t i = 1; i < logits.data.size(); ++i) {
+        if (logits.data[i] > logits.data[first_max]) first_max = static_cast<int>(i);
+    }
+    const int token = hip_sample_greedy_device(xd, lmw, 0);
+    require(token == first_max, "greedy token is the first maximum of the device logits");
+    Tensor cpu_logits = cpu_linear(QuantType::Q4_0, x, lm.q4_0_data, lm.shape);
+    float cpu_max = cpu_logits.data[0];
+    for (float v : cpu_logits.data) cpu_max = v > cpu_max ? v : cpu_max;
+    require(cpu_max - cpu_logits.data[token] <= 1e-3f * (1.0f + std::fabs(cpu_max)),
+            "greedy token is a maximum of the CPU logits within tolerance");
+    Tensor xinf = x;
+    xinf.data[3] = std::numeric_limits<float>::infinity();
+    HipTensor xinf_d = hip_tensor_from_host(xinf, 0);
+    threw = false;
+    try {
+        (void)hip_sample_greedy_device(xinf_d, lmw, 0);
+    } catch (const std::exception& e) {
+        threw = std::string(e.what()) == "sampler: logits must be finite";
+    }
+    require(threw, "non-finite logits message");
 }
 
 }  // namespace

@@ -79,6 +79,20 @@ _SIGS = {
                                                    ctypes.POINTER(_vp)]),
     "mlq_hip_graph_launch": (ctypes.c_int, [_vp, _vp]),
     "mlq_hip_graph_destroy": (ctypes.c_int, [_vp]),
+    "mlq_hip_gguf_open": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(_vp)]),
+    "mlq_hip_gguf_close": (ctypes.c_int, [_vp]),
+    "mlq_hip_gguf_header": (ctypes.c_int, [_vp, ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(ctypes.c_uint64),
+                                            ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)]),
+    "mlq_hip_gguf_metadata": (ctypes.c_int, [_vp, ctypes.c_uint64, ctypes.c_char_p, ctypes.c_size_t,
+                                              ctypes.POINTER(ctypes.c_uint32), ctypes.c_char_p, ctypes.c_size_t]),
+    "mlq_hip_gguf_tensor": (ctypes.c_int, [_vp, ctypes.c_uint64, ctypes.c_char_p, ctypes.c_size_t,
+                                            ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(ctypes.c_uint64),
+                                            ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(ctypes.c_uint64),
+                                            ctypes.POINTER(ctypes.c_uint64)]),
+    "mlq_hip_gguf_find": (ctypes.c_int, [_vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_uint64)]),
+    "mlq_hip_gguf_tensor_data": (ctypes.c_int, [_vp, ctypes.c_uint64, ctypes.POINTER(_vp),
+                                                 ctypes.POINTER(ctypes.c_uint64)]),
+    "mlq_hip_gguf_upload_weight": (ctypes.c_int, [_vp, ctypes.c_char_p, ctypes.c_int, ctypes.POINTER(_vp)]),
     "mlq_hip_graph_begin": (ctypes.c_int, [ctypes.c_int, _vp]),
     "mlq_hip_graph_end": (ctypes.c_int, [ctypes.c_int, _vp, ctypes.POINTER(_vp)]),
     "mlq_hip_sequence_create": (ctypes.c_int, [ctypes.POINTER(LinearCall), ctypes.c_int,
@@ -119,11 +133,11 @@ def load(path: str = LIB_PATH):
 
 def _check(rc: int) -> None:
     if rc != 0:
-        raise MlqError(rc, _LIB.mlq_hip_last_error().decode())
+        raise MlqError(rc, _LIB.mlq_hip_last_error().decode(errors="surrogateescape"))
 
 
 def last_error() -> str:
-    return load().mlq_hip_last_error().decode()
+    return load().mlq_hip_last_error().decode(errors="surrogateescape")
 
 
 def device_count() -> int:
@@ -384,6 +398,86 @@ class Graph:
     def __del__(self):
         try:
             self.destroy()
+        except Exception:
+            pass
+
+
+GGML_QTYPE = {8: Q8_0, 2: Q4_0, 3: Q4_1}  # GGML tensor type -> quant type
+
+
+class GgufFile:
+    """A GGUF model file mapped read-only and indexed (mlq_hip_gguf_*).  Needs
+    no GPU except for upload_weight."""
+
+    def __init__(self, path: str):
+        h = _vp()
+        _check(load().mlq_hip_gguf_open(os.fsencode(path), ctypes.byref(h)))
+        self.h = h.value
+
+    def header(self) -> dict:
+        v, nt, nm, off = ctypes.c_uint32(), ctypes.c_uint64(), ctypes.c_uint64(), ctypes.c_uint64()
+        _check(_LIB.mlq_hip_gguf_header(self.h, ctypes.byref(v), ctypes.byref(nt), ctypes.byref(nm),
+                                        ctypes.byref(off)))
+        return {"version": v.value, "n_tensors": nt.value, "n_metadata": nm.value, "data_offset": off.value}
+
+    def metadata(self) -> list:
+        """[(key, value type, value as the reference renders it)]"""
+        out = []
+        for i in range(self.header()["n_metadata"]):
+            for cap in (1 << 16, (16 << 20) + 64):
+                key, val, t = ctypes.create_string_buffer(cap), ctypes.create_string_buffer(cap), ctypes.c_uint32()
+                rc = _LIB.mlq_hip_gguf_metadata(self.h, i, key, cap, ctypes.byref(t), val, cap)
+                if rc != 6:  # MLQ_ERR_LIMIT: retry with the largest size a value can have
+                    break
+            _check(rc)
+            out.append((key.value.decode(errors="surrogateescape"), t.value,
+                        val.value.decode(errors="surrogateescape")))
+        return out
+
+    def tensors(self) -> list:
+        out = []
+        for i in range(self.header()["n_tensors"]):
+            nd, t, off, nb = ctypes.c_uint32(), ctypes.c_uint32(), ctypes.c_uint64(), ctypes.c_uint64()
+            dims = (ctypes.c_uint64 * 8)()
+            for cap in (1 << 12, (16 << 20) + 64):
+                name = ctypes.create_string_buffer(cap)
+                rc = _LIB.mlq_hip_gguf_tensor(self.h, i, name, cap, ctypes.byref(nd), dims, ctypes.byref(t),
+                                              ctypes.byref(off), ctypes.byref(nb))
+                if rc != 6:  # MLQ_ERR_LIMIT: retry with the largest size a name can have
+                    break
+            _check(rc)
+            out.append({"name": name.value.decode(errors="surrogateescape"),
+                        "dims": [dims[d] for d in range(nd.value)],
+                        "type": t.value, "offset": off.value, "nbytes": nb.value})
+        return out
+
+    def find(self, name: str) -> int:
+        i = ctypes.c_uint64()
+        _check(_LIB.mlq_hip_gguf_find(self.h, name.encode(), ctypes.byref(i)))
+        return i.value
+
+    def tensor_bytes(self, name: str) -> np.ndarray:
+        """A copy of the tensor's bytes read from the mapping."""
+        p, n = _vp(), ctypes.c_uint64()
+        _check(_LIB.mlq_hip_gguf_tensor_data(self.h, self.find(name), ctypes.byref(p), ctypes.byref(n)))
+        if not n.value:
+            return np.zeros(0, np.uint8)
+        return np.frombuffer(ctypes.string_at(p.value, n.value), dtype=np.uint8).copy()
+
+    def upload_weight(self, name: str, device: int = 0) -> "Weight":
+        info = self.tensors()[self.find(name)]
+        h = _vp()
+        _check(_LIB.mlq_hip_gguf_upload_weight(self.h, name.encode(), device, ctypes.byref(h)))
+        return Weight(h.value, GGML_QTYPE[info["type"]], int(info["dims"][1]), int(info["dims"][0]))
+
+    def close(self) -> None:
+        if getattr(self, "h", None):
+            _LIB.mlq_hip_gguf_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
         except Exception:
             pass
 

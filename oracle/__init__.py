@@ -167,6 +167,96 @@ class Reference(_Lib):
     def hardware_threads(self) -> int:
         return int(self._hw())
 
+    # ---- GGUF (src/gguf.cpp, src/gguf_loader.cpp)
+    def gguf(self, path: str) -> dict:
+        """GGUFReader::load on ``path``: ok, load_error, the header fields and,
+        as far as they were read, the metadata and tensor infos."""
+        cp, vp, u32, u64 = ctypes.c_char_p, ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint64
+        load = self._fn("gguf_load", vp, [cp, ctypes.POINTER(ctypes.c_int)])
+        free = self._fn("gguf_free", None, [vp])
+        err = self._fn("gguf_error", cp, [vp])
+        hdr = self._fn("gguf_header", None, [vp] + [ctypes.POINTER(u32)] + [ctypes.POINTER(u64)] * 5)
+        meta = self._fn("gguf_metadata", None, [vp, u64, ctypes.POINTER(cp), ctypes.POINTER(u32),
+                                                 ctypes.POINTER(vp), ctypes.POINTER(u64)])
+        ten = self._fn("gguf_tensor", None, [vp, u64, ctypes.POINTER(cp), ctypes.POINTER(u32),
+                                              ctypes.POINTER(u64), ctypes.POINTER(u32), ctypes.POINTER(u64),
+                                              ctypes.POINTER(u64)])
+        ok = ctypes.c_int(0)
+        h = load(os.fsencode(path), ctypes.byref(ok))
+        try:
+            v, nt, nm, off, nmr, ntr = u32(), u64(), u64(), u64(), u64(), u64()
+            hdr(h, ctypes.byref(v), ctypes.byref(nt), ctypes.byref(nm), ctypes.byref(off), ctypes.byref(nmr),
+                ctypes.byref(ntr))
+            out = {"ok": bool(ok.value), "error": err(h).decode(errors="surrogateescape"), "version": v.value,
+                   "n_tensors": nt.value,
+                   "n_metadata": nm.value, "data_offset": off.value, "metadata": [], "tensors": []}
+            for i in range(nmr.value):
+                k, t, val, n = cp(), u32(), vp(), u64()
+                meta(h, i, ctypes.byref(k), ctypes.byref(t), ctypes.byref(val), ctypes.byref(n))
+                # Up to the first NUL, as a C string carries it.
+                raw = ctypes.string_at(val.value, n.value).split(b"\0")[0] if n.value else b""
+                out["metadata"].append((k.value.decode(errors="surrogateescape"), t.value,
+                                        raw.decode(errors="surrogateescape")))
+            for i in range(ntr.value):
+                nme, nd, t, o, nb = cp(), u32(), u32(), u64(), u64()
+                dims = (u64 * 8)()
+                ten(h, i, ctypes.byref(nme), ctypes.byref(nd), dims, ctypes.byref(t), ctypes.byref(o),
+                    ctypes.byref(nb))
+                out["tensors"].append({"name": nme.value.decode(errors="surrogateescape"),
+                                       "dims": [dims[d] for d in range(nd.value)],
+                                       "type": t.value, "offset": o.value, "nbytes": nb.value})
+            return out
+        finally:
+            free(h)
+
+    def gguf_tensor_raw(self, path: str, index: int) -> np.ndarray:
+        """read_gguf_tensor_raw for tensor ``index`` (empty where it fails)."""
+        vp, u64 = ctypes.c_void_p, ctypes.c_uint64
+        load = self._fn("gguf_load", vp, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_int)])
+        free = self._fn("gguf_free", None, [vp])
+        read = self._fn("gguf_read", ctypes.c_longlong, [ctypes.c_char_p, vp, u64, vp, u64])
+        ok = ctypes.c_int(0)
+        h = load(os.fsencode(path), ctypes.byref(ok))
+        try:
+            cap = os.path.getsize(path)
+            buf = np.empty(max(cap, 1), np.uint8)
+            n = read(os.fsencode(path), h, index, _ptr(buf), cap)
+            return buf[:max(n, 0)].copy()
+        finally:
+            free(h)
+
+    def type_names(self, t: int) -> tuple:
+        ggml = self._fn("ggml_type_name", ctypes.c_char_p, [ctypes.c_uint32])
+        val = self._fn("gguf_value_type_name", ctypes.c_char_p, [ctypes.c_uint32])
+        return ggml(t).decode(), val(t).decode()
+
+    def gguf_model_linears(self, path: str, names) -> dict:
+        """load_gguf_model, then {name: (quant type, rows, cols, block bytes)}
+        for the reference-named linears ``names``; raises with load_error."""
+        vp = ctypes.c_void_p
+        load = self._fn("gguf_model", vp, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_int)])
+        free = self._fn("model_free", None, [vp])
+        err = self._fn("model_error", ctypes.c_char_p, [vp])
+        lin = self._fn("model_linear", ctypes.c_int,
+                       [vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int),
+                        ctypes.POINTER(ctypes.c_int), ctypes.POINTER(vp), ctypes.POINTER(ctypes.c_uint64)])
+        ok = ctypes.c_int(0)
+        h = load(os.fsencode(path), ctypes.byref(ok))
+        try:
+            if not ok.value:
+                raise RuntimeError(err(h).decode())
+            out = {}
+            for n in names:
+                q, r, c, d, nb = ctypes.c_int(), ctypes.c_int(), ctypes.c_int(), vp(), ctypes.c_uint64()
+                if lin(h, n.encode(), ctypes.byref(q), ctypes.byref(r), ctypes.byref(c), ctypes.byref(d),
+                       ctypes.byref(nb)) != 0:
+                    raise KeyError(n)
+                out[n] = (q.value, r.value, c.value,
+                          np.frombuffer(ctypes.string_at(d.value, nb.value), np.uint8).copy())
+            return out
+        finally:
+            free(h)
+
     def fp16_probe_q4_1(self, v: float) -> int:
         return int(self._p41(float(v)))
 

@@ -15,6 +15,9 @@
 #include "tests/test_cuda_quant.cpp"
 #undef main
 
+#include "mini_llama/gguf.h"
+#include "mini_llama/gguf_loader.h"
+#include "mini_llama/model.h"
 #include "mini_llama/ops.h"
 #include "mini_llama/quant.h"
 #include "mini_llama/thread_pool.h"
@@ -177,6 +180,112 @@ int mlq_ref_argmax(const float* v, int n) {
 int mlq_ref_hardware_threads(void) {
     set_thread_count(0);
     return get_thread_count();
+}
+
+// ---- GGUF: the reference reader (src/gguf.cpp) and loader (src/gguf_loader.cpp)
+
+// Parses `path` with GGUFReader::load; the reader is returned whether or not
+// the load succeeded (*ok), so its fields and load_error can be read back.
+void* mlq_ref_gguf_load(const char* path, int* ok) {
+    GGUFReader* r = new GGUFReader;
+    *ok = r->load(path) ? 1 : 0;
+    return r;
+}
+
+void mlq_ref_gguf_free(void* h) { delete static_cast<GGUFReader*>(h); }
+
+const char* mlq_ref_gguf_error(void* h) { return static_cast<GGUFReader*>(h)->load_error.c_str(); }
+
+void mlq_ref_gguf_header(void* h, uint32_t* version, uint64_t* n_tensors, uint64_t* n_metadata,
+                         uint64_t* data_offset, uint64_t* n_meta_read, uint64_t* n_tensors_read) {
+    const GGUFReader* r = static_cast<GGUFReader*>(h);
+    *version = r->version;
+    *n_tensors = r->n_tensors;
+    *n_metadata = r->n_metadata;
+    *data_offset = r->data_offset;
+    *n_meta_read = r->metadata.size();
+    *n_tensors_read = r->tensors.size();
+}
+
+void mlq_ref_gguf_metadata(void* h, uint64_t i, const char** key, uint32_t* type, const char** value,
+                           uint64_t* value_len) {
+    const GGUFMetadataKV& kv = static_cast<GGUFReader*>(h)->metadata[i];
+    *key = kv.key.c_str();
+    *type = kv.type;
+    *value = kv.value_str.data();
+    *value_len = kv.value_str.size();
+}
+
+void mlq_ref_gguf_tensor(void* h, uint64_t i, const char** name, uint32_t* n_dims, uint64_t* dims, uint32_t* type,
+                         uint64_t* offset, uint64_t* nbytes) {
+    const GGUFTensorInfo& t = static_cast<GGUFReader*>(h)->tensors[i];
+    *name = t.name.c_str();
+    *n_dims = static_cast<uint32_t>(t.shape.size());
+    for (size_t d = 0; d < t.shape.size() && d < 8; ++d) dims[d] = t.shape[d];
+    *type = t.type;
+    *offset = t.offset;
+    uint64_t n = 0;
+    *nbytes = gguf_tensor_data_size(t, n) ? n : ~0ull;
+}
+
+// read_gguf_tensor_raw into `out` (capacity `cap`); returns the byte count.
+long long mlq_ref_gguf_read(const char* path, void* h, uint64_t i, void* out, uint64_t cap) {
+    const GGUFReader* r = static_cast<GGUFReader*>(h);
+    std::vector<uint8_t> raw = read_gguf_tensor_raw(path, r->tensors[i], r->data_offset);
+    if (raw.size() > cap) return -1;
+    std::memcpy(out, raw.data(), raw.size());
+    return static_cast<long long>(raw.size());
+}
+
+const char* mlq_ref_ggml_type_name(uint32_t t) { return ggml_type_name(t); }
+const char* mlq_ref_gguf_value_type_name(uint32_t t) { return gguf_value_type_name(t); }
+
+// load_gguf_model; the model is returned whether or not it loaded (*ok).
+void* mlq_ref_gguf_model(const char* path, int* ok) {
+    MiniLlamaModel* m = new MiniLlamaModel(load_gguf_model(path));
+    *ok = m->loaded ? 1 : 0;
+    return m;
+}
+
+void mlq_ref_model_free(void* h) { delete static_cast<MiniLlamaModel*>(h); }
+
+const char* mlq_ref_model_error(void* h) { return static_cast<MiniLlamaModel*>(h)->load_error.c_str(); }
+
+// A linear weight of a loaded model by the reference's own name ("lm_head",
+// "layers.N.wq" ... "layers.N.w_down"): quant type, shape and block bytes.
+int mlq_ref_model_linear(void* h, const char* name, int* qtype, int* rows, int* cols, const void** data,
+                         uint64_t* nbytes) {
+    MiniLlamaModel* m = static_cast<MiniLlamaModel*>(h);
+    const std::string n = name;
+    const QuantizedTensor* q = nullptr;
+    if (n == "lm_head") {
+        q = &m->lm_head;
+    } else if (n.rfind("layers.", 0) == 0) {
+        const size_t dot = n.find('.', 7);
+        if (dot == std::string::npos) return -1;
+        const int layer = std::stoi(n.substr(7, dot - 7));
+        if (layer < 0 || layer >= static_cast<int>(m->layers.size())) return -1;
+        LayerWeights& lw = m->layers[layer];
+        const std::string op = n.substr(dot + 1);
+        if (op == "wq") q = &lw.wq;
+        else if (op == "wk") q = &lw.wk;
+        else if (op == "wv") q = &lw.wv;
+        else if (op == "wo") q = &lw.wo;
+        else if (op == "w_gate") q = &lw.w_gate;
+        else if (op == "w_up") q = &lw.w_up;
+        else if (op == "w_down") q = &lw.w_down;
+    }
+    if (q == nullptr || q->shape.size() != 2) return -1;
+    *qtype = static_cast<int>(q->type);
+    *rows = q->shape[0];
+    *cols = q->shape[1];
+    switch (q->type) {
+        case QuantType::Q8_0: *data = q->q8_0_data.data(); *nbytes = q->q8_0_data.size() * sizeof(BlockQ8_0); break;
+        case QuantType::Q4_0: *data = q->q4_0_data.data(); *nbytes = q->q4_0_data.size() * sizeof(BlockQ4_0); break;
+        case QuantType::Q4_1: *data = q->q4_1_data.data(); *nbytes = q->q4_1_data.size() * sizeof(BlockQ4_1); break;
+        default: *data = q->f32_data.data(); *nbytes = q->f32_data.size() * sizeof(float); break;
+    }
+    return 0;
 }
 
 }  // extern "C"
