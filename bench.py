@@ -256,6 +256,62 @@ def gemv_shape_bench(name, qt, m, k, stream, reps_target=400):
     return res
 
 
+def ingest_bench(layers=4):
+    """GGUF ingest of LLaMA-7B-shaped Q4_0 linears (`layers` layers of q, k, v,
+    o, gate, up, down and the lm_head) from a page-cache-warm file: the
+    mapping straight to HBM (mlq_hip_gguf_upload_weight) against the
+    reference's sequence, each tensor read into host memory and then uploaded
+    (read_gguf_tensor_raw + upload, src/gguf.cpp:586-622, src/model.cpp:145-272)."""
+    import tempfile
+
+    sys.path.insert(0, os.path.join(REPO, "tests"))
+    import gguf_writer as gw
+
+    rng = np.random.default_rng(1)
+    shapes = []
+    for layer in range(layers):
+        for op, (m, k) in (("attn_q", (4096, 4096)), ("attn_k", (4096, 4096)), ("attn_v", (4096, 4096)),
+                           ("attn_output", (4096, 4096)), ("ffn_gate", (11008, 4096)), ("ffn_up", (11008, 4096)),
+                           ("ffn_down", (4096, 11008))):
+            shapes.append((f"blk.{layer}.{op}.weight", m, k))
+    shapes.append(("output.weight", 32000, 4096))
+    tensors = [(n, [k, m], gw.GGML_Q4_0, rng.integers(0, 256, m * (k // 32) * 18, dtype=np.uint8).tobytes())
+               for n, m, k in shapes]
+    fd, path = tempfile.mkstemp(suffix=".gguf")
+    os.close(fd)
+    try:
+        gw.write(path, [("general.architecture", gw.STRING, "llama")], tensors, alignment=32)
+        total = sum(len(t[3]) for t in tensors)
+        del tensors
+        g = hip.GgufFile(path)
+        infos = {t["name"]: t for t in g.tensors()}
+        data_offset = g.header()["data_offset"]
+        for n, _, _ in shapes[:2]:  # warm the pinned stage and the runtime
+            g.upload_weight(n).free()
+        t0 = time.perf_counter()
+        ws = [g.upload_weight(n) for n, _, _ in shapes]
+        t_map = time.perf_counter() - t0
+        for w in ws:
+            w.free()
+        g.close()
+        t0 = time.perf_counter()
+        ws = []
+        with open(path, "rb") as f:
+            for n, m, k in shapes:
+                f.seek(data_offset + infos[n]["offset"])
+                raw = np.frombuffer(f.read(infos[n]["nbytes"]), np.uint8)
+                ws.append(hip.Weight.upload(hip.Q4_0, raw.reshape(-1, 18), m, k))
+        t_read = time.perf_counter() - t0
+        for w in ws:
+            w.free()
+    finally:
+        os.unlink(path)
+    return {"tensors": len(shapes), "bytes": total, "s_mapping_to_hbm": round(t_map, 4),
+            "gbs_mapping_to_hbm": round(total / t_map / 1e9, 2), "s_read_then_upload": round(t_read, 4),
+            "gbs_read_then_upload": round(total / t_read / 1e9, 2),
+            "note": "file in the page cache; host-to-device over PCIe; synthetic Q4_0 blocks"}
+
+
 PICK_CONFIGS = ([("c2_qwen_lm_head", qt, 151936, 896) for qt in (hip.Q8_0, hip.Q4_0, hip.Q4_1)] +
                 [("c3_llama_lm_head", qt, 32000, 4096) for qt in (hip.Q8_0, hip.Q4_0, hip.Q4_1)])
 
@@ -453,6 +509,12 @@ def main():
                 f"token {r['token']}")
             picks.append(r)
 
+    ingest = None
+    if not args.no_shapes:
+        ingest = ingest_bench()
+        log(f"  gguf ingest {ingest['bytes'] / 1e6:.0f} MB in {ingest['tensors']} tensors: mapping -> HBM "
+            f"{ingest['gbs_mapping_to_hbm']} GB/s, read then upload {ingest['gbs_read_then_upload']} GB/s")
+
     gemm = []
     if not args.no_shapes:
         for cfg in GEMM_CONFIGS:
@@ -510,6 +572,7 @@ def main():
         "parity": parity,
         "gemv": shapes,
         "lm_head_argmax": picks,
+        "gguf_ingest": ingest,
         "gemm": gemm,
     }
     print(json.dumps(out), flush=True)
