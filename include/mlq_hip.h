@@ -276,6 +276,41 @@ int mlq_hip_gguf_tensor_data(mlq_gguf_t g, uint64_t i, const void** data, uint64
  * Validation messages follow the upload's (src/model.cpp:145-272). */
 int mlq_hip_gguf_upload_weight(mlq_gguf_t g, const char* name, int device, mlq_weight_t* out);
 
+/* ---- Device-resident decode (forward_token with every op on the device) ----
+ * A llama / qwen2 model loaded from a GGUF file as load_gguf_model loads it
+ * (src/gguf_loader.cpp:320-456: config from metadata, tensor names, F32 norms,
+ * embedding and biases, dequantized where stored quantized, tied lm_head),
+ * its quantized linears on the GEMV kernels and the ops between them
+ * (RMSNorm, RoPE, KV cache, attention, SwiGLU, residuals) as HIP kernels.
+ * The position and input token of a step live in device memory, so greedy
+ * generation replays one recorded step per token with the pick of one step
+ * feeding the next: one upload and one download per call, none per token. */
+typedef struct mlq_decoder_s* mlq_decoder_t;
+
+/* ModelConfig (include/mini_llama/model.h:17-29); rope_neox = 1 for qwen2. */
+typedef struct mlq_decoder_config {
+    int n_layers, dim, hidden_dim, n_heads, n_kv_heads, head_dim, vocab_size, max_seq_len;
+    float rope_theta, rms_norm_eps;
+    int rope_neox;
+} mlq_decoder_config;
+
+/* Load `gguf_path` onto `device`.  max_seq_len > 0 caps the KV cache below
+ * the model's context length.  Messages as the loader's ("GGUF parse error:
+ * ...", "Failed to build config: ...", "Failed to load GGUF weights: Missing
+ * tensor: layers.0.wq", ...). */
+int mlq_hip_decoder_open(const char* gguf_path, int device, int max_seq_len, mlq_decoder_t* out);
+int mlq_hip_decoder_config(mlq_decoder_t d, mlq_decoder_config* out);
+/* forward_token (src/forward.cpp:865-903) with ctx.pos = pos: logits
+ * [vocab_size] to host memory.  Positions below pos hold what earlier calls
+ * wrote (zeros otherwise), as the reference's KV cache. */
+int mlq_hip_decoder_forward(mlq_decoder_t d, int token, int pos, float* logits);
+/* Greedy generation: the prompt at positions 0..n_prompt-1 (forward_batch,
+ * src/batch.cpp:33-52), then n_new tokens, each the first maximum of the
+ * previous step's logits (MiniSampler::sample_greedy), into out_tokens.
+ * Fails with "sampler: logits must be finite" as the sampler does. */
+int mlq_hip_decoder_generate(mlq_decoder_t d, const int* prompt, int n_prompt, int n_new, int* out_tokens);
+int mlq_hip_decoder_close(mlq_decoder_t d);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,117 @@
+// Device-resident decode step of a llama / qwen2 model over the quantized
+// linears (internal interface between decoder.hip and mlq_abi.hip).
+//
+// Mirrors forward_token (src/forward.cpp:865-903) with every op on the
+// device: embedding lookup, per layer RMSNorm -> q/k/v (+ bias) -> RoPE ->
+// KV-cache write -> attention -> o -> residual -> RMSNorm -> gate/up ->
+// SwiGLU -> down -> residual, then the final RMSNorm and the lm_head.  The
+// token and position a step uses live in device memory, so one step is a
+// fixed sequence of launches that can be recorded once and replayed per
+// token, with the greedy pick of one step feeding the next.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <memory>
+#include <string>
+#include <vector>
+
+namespace mlq {
+
+struct DecoderConfig {
+    int n_layers = 0;
+    int dim = 0;
+    int hidden_dim = 0;
+    int n_heads = 0;
+    int n_kv_heads = 0;
+    int head_dim = 0;
+    int vocab_size = 0;
+    int max_seq_len = 0;
+    float rope_theta = 10000.0f;
+    float rms_norm_eps = 1e-5f;
+    int rope_neox = 0;  // RopeType::NeoX (general.architecture == "qwen2")
+};
+
+// State words of one decoder in device memory.
+struct DecodeState {
+    int32_t pos;     // position of the step about to run
+    int32_t token;   // its input token
+    int32_t next;    // greedy pick of the last step (-1: a logit was not finite)
+    int32_t error;   // bit 0: token out of range, 1: position out of range, 2: non-finite logits
+    int32_t n_prompt;
+    int32_t n_out;
+    int32_t pad[2];
+};
+
+constexpr int kDecodeErrToken = 1;
+constexpr int kDecodeErrPos = 2;
+constexpr int kDecodeErrLogits = 4;
+
+class Decoder {
+public:
+    // Loads a model the way load_gguf_model does (src/gguf_loader.cpp:320-456:
+    // config from metadata, tensor names, F32 norms / embedding / biases with
+    // quantized ones dequantized, tied lm_head) and places it on `device`.
+    // max_seq_len > 0 bounds the KV cache below the model's context length.
+    // Throws std::runtime_error with the loader's messages.
+    static std::unique_ptr<Decoder> from_gguf(const std::string& path, int device, int max_seq_len);
+    ~Decoder();
+
+    const DecoderConfig& config() const { return cfg_; }
+    int device() const { return device_; }
+
+    // forward_token with ctx.pos = pos: logits [vocab] to host memory.
+    void forward(int token, int pos, float* logits_host);
+    // Greedy generation: the prompt at positions 0..n_prompt-1, then n_new
+    // tokens each picked from the previous step's logits (first maximum) and
+    // fed back on the device.  One upload, one download, no host work per
+    // token.  Throws on a device-side error (bad prompt token, position past
+    // the cache, non-finite logits).
+    void generate(const int* prompt, int n_prompt, int n_new, int* out);
+
+private:
+    Decoder() = default;
+    void enqueue_step(hipStream_t s, bool pick, bool advance);
+    void check(hipError_t e, const char* what);
+
+    struct Linear {
+        int qtype = 0;   // 0 = F32 [M][K] floats, else MLQ_Q8_0 / Q4_0 / Q4_1 blocks
+        int M = 0;
+        int K = 0;
+        void* data = nullptr;
+    };
+    struct Layer {
+        float* attn_norm = nullptr;
+        float* ffn_norm = nullptr;
+        float* bq = nullptr;
+        float* bk = nullptr;
+        float* bv = nullptr;
+        Linear wq, wk, wv, wo, w_gate, w_up, w_down;
+    };
+
+    void linear_group(hipStream_t s, const Linear* const* ws, float* const* ys, int n, const float* x);
+
+    DecoderConfig cfg_;
+    int device_ = 0;
+    hipStream_t stream_ = nullptr;
+    std::vector<void*> allocs_;
+    float* embedding_ = nullptr;  // [vocab][dim]
+    float* final_norm_ = nullptr;
+    Linear lm_head_;
+    std::vector<Layer> layers_;
+    // Activations and cache.
+    float *x_ = nullptr, *h_ = nullptr, *q_ = nullptr, *k_ = nullptr, *v_ = nullptr, *att_ = nullptr;
+    float *proj_ = nullptr, *gate_ = nullptr, *up_ = nullptr, *act_ = nullptr, *ff_ = nullptr;
+    float* logits_ = nullptr;
+    float* scores_ = nullptr;    // [n_heads][max_seq_len]
+    float* kcache_ = nullptr;    // [n_layers][max_seq_len][n_kv_heads][head_dim]
+    float* vcache_ = nullptr;
+    DecodeState* state_ = nullptr;
+    int32_t* io_ = nullptr;      // prompt tokens then generated tokens
+    size_t io_cap_ = 0;
+    void* pick_ = nullptr;       // PickState
+    hipGraphExec_t graph_ = nullptr;
+};
+
+}  // namespace mlq

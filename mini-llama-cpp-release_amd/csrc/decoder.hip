@@ -1,0 +1,733 @@
+// Device-resident decode step (see decoder.h).
+//
+// Kernels for the ops between the quantized linears -- embedding lookup,
+// residual add + RMSNorm, bias + RoPE + KV-cache write, decode attention,
+// SwiGLU, an F32 GEMV for unquantized weights (tied embeddings) and the pick
+// over F32 logits -- and the host side that loads a GGUF model the way
+// load_gguf_model does and sequences one step.  Arithmetic follows the
+// reference's f32 ops (src/ops.cpp:18-175, src/forward.cpp:462-726); sums are
+// reduced in parallel, so results agree to rounding, not bit for bit.
+#include "decoder.h"
+
+#include "gguf_index.h"
+#include "mlq_kernels.h"
+#include "pick_key.h"
+
+#include "../../include/mlq_hip.h"
+
+#include <cmath>
+#include <cstring>
+#include <stdexcept>
+#include <string>
+
+namespace mlq {
+
+namespace {
+
+constexpr int kNormThreads = 1024;
+constexpr int kAttnThreads = 256;
+constexpr int kMaxHeadDim = 256;
+
+// Sum (or max) over a workgroup of `nthreads`; every thread gets the result.
+template <int NT, bool MAX>
+__device__ __forceinline__ float wg_reduce(float v, float* part) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float w = __shfl_xor(v, o, 64);
+        v = MAX ? fmaxf(v, w) : v + w;
+    }
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float r = part[0];
+#pragma unroll
+    for (int i = 1; i < NT / 64; ++i) r = MAX ? fmaxf(r, part[i]) : r + part[i];
+    return r;
+}
+
+// x[dim] = embedding[token] (embed_token, src/forward.cpp:496-503).  A token
+// out of range flags the step and reads row 0.
+__global__ __launch_bounds__(256) void embed_kernel(const float* __restrict__ emb, int vocab, int dim,
+                                                    DecodeState* st, float* __restrict__ x) {
+    const int t = st->token;
+    const bool ok = t >= 0 && t < vocab;
+    if (!ok && blockIdx.x == 0 && threadIdx.x == 0) st->error |= kDecodeErrToken;
+    const size_t row = static_cast<size_t>(ok ? t : 0) * dim;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < dim; i += gridDim.x * blockDim.x) x[i] = emb[row + i];
+}
+
+// x += delta (when given; forward_add) then out = rmsnorm(x) * w
+// (rmsnorm, src/ops.cpp:18-41: mean of squares, 1 / sqrt(ms + eps)).
+__global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(float* __restrict__ x,
+                                                                   const float* __restrict__ delta,
+                                                                   const float* __restrict__ w, int dim, float eps,
+                                                                   float* __restrict__ out) {
+    __shared__ float part[kNormThreads / 64];
+    float ss = 0.0f;
+    for (int i = threadIdx.x; i < dim; i += kNormThreads) {
+        float v = x[i];
+        if (delta != nullptr) {
+            v = v + delta[i];
+            x[i] = v;
+        }
+        ss += v * v;
+    }
+    ss = wg_reduce<kNormThreads, false>(ss, part);
+    const float scale = 1.0f / sqrtf(ss / static_cast<float>(dim) + eps);
+    for (int i = threadIdx.x; i < dim; i += kNormThreads) out[i] = x[i] * scale * w[i];
+}
+
+// Optional q/k/v biases, RoPE on q and k (src/ops.cpp:109-175: normal pairs
+// (2r, 2r+1) or NeoX pairs (r, r + hd/2), angle pos / theta^(2r/hd)), and
+// the KV-cache write at [layer][pos][kv head][d] (KVCache::write).
+__global__ __launch_bounds__(256) void rope_kv_kernel(float* __restrict__ q, float* __restrict__ k,
+                                                      const float* __restrict__ v, const float* __restrict__ bq,
+                                                      const float* __restrict__ bk, const float* __restrict__ bv,
+                                                      int n_heads, int n_kv, int hd, float theta, int neox,
+                                                      int max_seq, int layer, DecodeState* st,
+                                                      float* __restrict__ kc, float* __restrict__ vc) {
+    const int p0 = st->pos;
+    const bool ok = p0 >= 0 && p0 < max_seq;
+    if (!ok && blockIdx.x == 0 && threadIdx.x == 0) st->error |= kDecodeErrPos;
+    const int pos = ok ? p0 : 0;
+    const int half = hd / 2;
+    const int nq = n_heads * half;
+    const int nk = n_kv * half;
+    const int nv = n_kv * hd;
+    const size_t cache_row = (static_cast<size_t>(layer) * max_seq + pos) * n_kv * hd;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < nq + nk) {
+        const bool is_q = i < nq;
+        const int j = is_q ? i : i - nq;
+        const int h = j / half;
+        const int r = j % half;
+        const int i0 = h * hd + (neox ? r : 2 * r);
+        const int i1 = neox ? i0 + half : i0 + 1;
+        const float freq = 1.0f / powf(theta, static_cast<float>(2 * r) / static_cast<float>(hd));
+        const float ang = static_cast<float>(pos) * freq;
+        const float c = cosf(ang);
+        const float s = sinf(ang);
+        float* t = is_q ? q : k;
+        const float* b = is_q ? bq : bk;
+        float a0 = t[i0];
+        float a1 = t[i1];
+        if (b != nullptr) {
+            a0 = a0 + b[i0];
+            a1 = a1 + b[i1];
+        }
+        const float r0 = a0 * c - a1 * s;
+        const float r1 = a0 * s + a1 * c;
+        t[i0] = r0;
+        t[i1] = r1;
+        if (!is_q) {
+            kc[cache_row + i0] = r0;
+            kc[cache_row + i1] = r1;
+        }
+    } else if (i < nq + nk + nv) {
+        const int e = i - nq - nk;
+        vc[cache_row + e] = bv != nullptr ? v[e] + bv[e] : v[e];
+    }
+}
+
+// One workgroup per query head (attention_forward, src/forward.cpp:583-607):
+// scores q.k_t / sqrt(hd) for t <= pos, softmax (max, exp, sum, divide),
+// then sum_t p_t v_t.  Scores live in global scratch [head][max_seq].
+__global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __restrict__ q,
+                                                                 const float* __restrict__ kc,
+                                                                 const float* __restrict__ vc,
+                                                                 float* __restrict__ scores, float* __restrict__ out,
+                                                                 int n_heads, int n_kv, int hd, int max_seq, int layer,
+                                                                 const DecodeState* st) {
+    __shared__ float qs[kMaxHeadDim];
+    __shared__ float part[kAttnThreads / 64];
+    __shared__ float acc_part[kAttnThreads];
+    const int h = blockIdx.x;
+    const int kvh = h / (n_heads / n_kv);
+    const int p0 = st->pos;
+    const int pos = (p0 >= 0 && p0 < max_seq) ? p0 : 0;
+    float* sc = scores + static_cast<size_t>(h) * max_seq;
+    const size_t layer_base = static_cast<size_t>(layer) * max_seq * n_kv * hd;
+    const size_t t_stride = static_cast<size_t>(n_kv) * hd;
+    for (int d = threadIdx.x; d < hd; d += kAttnThreads) qs[d] = q[h * hd + d];
+    __syncthreads();
+    const float scale = 1.0f / sqrtf(static_cast<float>(hd));
+    float lmax = -INFINITY;
+    for (int t = threadIdx.x; t <= pos; t += kAttnThreads) {
+        const float* kp = kc + layer_base + t * t_stride + kvh * hd;
+        float dot = 0.0f;
+        for (int d = 0; d < hd; ++d) dot += qs[d] * kp[d];
+        const float s = dot * scale;
+        sc[t] = s;
+        lmax = fmaxf(lmax, s);
+    }
+    const float m = wg_reduce<kAttnThreads, true>(lmax, part);
+    float lsum = 0.0f;
+    for (int t = threadIdx.x; t <= pos; t += kAttnThreads) {
+        const float e = expf(sc[t] - m);
+        sc[t] = e;
+        lsum += e;
+    }
+    const float sum = wg_reduce<kAttnThreads, false>(lsum, part);
+    for (int t = threadIdx.x; t <= pos; t += kAttnThreads) sc[t] = sc[t] / sum;
+    __syncthreads();
+    // Output: thread (g, d) sums t = g, g + G, ... for dimension d.
+    const int groups = kAttnThreads / hd;
+    const int g = threadIdx.x / hd;
+    const int d = threadIdx.x % hd;
+    float acc = 0.0f;
+    if (g < groups) {
+        for (int t = g; t <= pos; t += groups) acc += sc[t] * vc[layer_base + t * t_stride + kvh * hd + d];
+    }
+    acc_part[threadIdx.x] = acc;
+    __syncthreads();
+    if (threadIdx.x < hd) {
+        float r = 0.0f;
+        for (int gg = 0; gg < groups; ++gg) r += acc_part[gg * hd + threadIdx.x];
+        out[h * hd + threadIdx.x] = r;
+    }
+}
+
+// out = silu(gate) * up (swiglu, src/ops.cpp:95-107).
+__global__ __launch_bounds__(256) void swiglu_kernel(const float* __restrict__ g, const float* __restrict__ u,
+                                                     float* __restrict__ out, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) {
+        const float v = g[i];
+        const float sig = 1.0f / (1.0f + expf(-v));
+        out[i] = v * sig * u[i];
+    }
+}
+
+// y[M] = W[M][K] . x for F32 weights: one wave per row.
+__global__ __launch_bounds__(256) void gemv_f32_kernel(const float* __restrict__ W, const float* __restrict__ x,
+                                                       float* __restrict__ y, int M, int K) {
+    const int row = blockIdx.x * 4 + static_cast<int>(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= M) return;
+    const float* w = W + static_cast<size_t>(row) * K;
+    float acc = 0.0f;
+    for (int k = lane; k < K; k += 64) acc += w[k] * x[k];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+    if (lane == 0) y[row] = acc;
+}
+
+// Greedy pick over F32 logits in one workgroup: st->next = first index of the
+// maximum, or -1 with the error bit when a logit is not finite.
+__global__ __launch_bounds__(1024) void pick_f32_kernel(const float* __restrict__ logits, int n, DecodeState* st) {
+    __shared__ unsigned long long part[16];
+    unsigned long long best = 0;
+    for (int i = threadIdx.x; i < n; i += 1024) {
+        const unsigned long long k = pick_key(logits[i], i);
+        best = k > best ? k : best;
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const unsigned long long other = __shfl_xor(best, o, 64);
+        best = other > best ? other : best;
+    }
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int i = 1; i < 16; ++i) best = part[i] > best ? part[i] : best;
+        best = part[0] > best ? part[0] : best;
+        st->next = pick_token(best);
+    }
+}
+
+// End of a step: the next input token (the prompt's, or this step's pick,
+// which is also stored as a generated token) and the next position.
+__global__ void advance_kernel(DecodeState* st, int32_t* io) {
+    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+    const int p = st->pos;
+    const int np = st->n_prompt;
+    if (p + 1 < np) {
+        st->token = io[p + 1];
+    } else {
+        const int picked = st->next;
+        const int g = p + 1 - np;
+        if (g >= 0 && g < st->n_out) io[np + g] = picked;
+        if (picked < 0) st->error |= kDecodeErrLogits;
+        st->token = picked < 0 ? 0 : picked;
+    }
+    st->pos = p + 1;
+}
+
+int qtype_of_ggml(uint32_t t) {
+    switch (t) {
+        case kGgmlQ8_0: return MLQ_Q8_0;
+        case kGgmlQ4_0: return MLQ_Q4_0;
+        case kGgmlQ4_1: return MLQ_Q4_1;
+        default: return -1;
+    }
+}
+
+float fp16_value(uint16_t h) {
+    const uint32_t sign = static_cast<uint32_t>(h >> 15) << 31;
+    const int e = (h >> 10) & 31;
+    const uint32_t m = h & 1023;
+    uint32_t bits;
+    if (e == 0) {
+        if (m == 0) {
+            bits = sign;
+        } else {  // subnormal: m * 2^-24, exact in f32
+            const float v = static_cast<float>(m) * 5.9604644775390625e-08f;
+            std::memcpy(&bits, &v, 4);
+            bits |= sign;
+        }
+    } else if (e == 31) {
+        bits = sign | 0x7F800000u | (m << 13);
+    } else {
+        bits = sign | (static_cast<uint32_t>(e - 15 + 127) << 23) | (m << 13);
+    }
+    float f;
+    std::memcpy(&f, &bits, 4);
+    return f;
+}
+
+// Block bytes to f32 rows of `row` values, as dequantize_from_q8_0 / _q4_0 /
+// _q4_1 (src/quant.cpp:172-360): d * q, d * (n - 8), d * n + m (one multiply,
+// then one add).
+void dequantize_rows(int qtype, const uint8_t* blk, size_t rows, size_t row, float* out) {
+    const size_t nb = (row + 31) / 32;
+    const size_t bb = static_cast<size_t>(block_bytes(qtype));
+    for (size_t r = 0; r < rows; ++r) {
+        for (size_t b = 0; b < nb; ++b) {
+            const uint8_t* p = blk + (r * nb + b) * bb;
+            uint16_t dh;
+            std::memcpy(&dh, p, 2);
+            const float d = fp16_value(dh);
+            float m = 0.0f;
+            if (qtype == MLQ_Q4_1) {
+                uint16_t mh;
+                std::memcpy(&mh, p + 2, 2);
+                m = fp16_value(mh);
+            }
+            for (size_t j = 0; j < 32; ++j) {
+                const size_t col = b * 32 + j;
+                if (col >= row) break;
+                float v;
+                if (qtype == MLQ_Q8_0) {
+                    v = d * static_cast<float>(static_cast<int8_t>(p[2 + j]));
+                } else {
+                    const int off = qtype == MLQ_Q4_0 ? 2 : 4;
+                    const uint8_t byte = p[off + (j & 15)];
+                    const int n = j < 16 ? (byte & 15) : (byte >> 4);
+                    if (qtype == MLQ_Q4_0) {
+                        v = d * static_cast<float>(n - 8);
+                    } else {
+                        v = d * static_cast<float>(n);
+                        v = v + m;
+                    }
+                }
+                out[r * row + col] = v;
+            }
+        }
+    }
+}
+
+std::string shape_text(const std::vector<int>& s) {
+    std::string t = "[";
+    for (size_t i = 0; i < s.size(); ++i) t += (i ? ", " : "") + std::to_string(s[i]);
+    return t + "]";
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------ loading
+
+void Decoder::check(hipError_t e, const char* what) {
+    if (e != hipSuccess) throw std::runtime_error(std::string("HIP error in ") + what + ": " + hipGetErrorString(e));
+}
+
+std::unique_ptr<Decoder> Decoder::from_gguf(const std::string& path, int device, int max_seq_len) {
+    GgufIndex g;
+    if (!g.open(path)) throw std::runtime_error("GGUF parse error: " + g.error);
+
+    // Config (build_config, src/gguf_loader.cpp:241-310).
+    DecoderConfig c;
+    {
+        auto get_int = [&](const std::string& key, int fallback) {
+            int64_t v = 0;
+            return g.get_int(key, v) ? static_cast<int>(v) : fallback;
+        };
+        auto get_float = [&](const std::string& key, float fallback) {
+            double v = 0.0;
+            return g.get_float(key, v) ? static_cast<float>(v) : fallback;
+        };
+        std::string arch;
+        if (g.get_string("general.architecture", arch) && arch == "qwen2") c.rope_neox = 1;
+        c.n_layers = get_int("qwen2.block_count", get_int("llama.block_count", 0));
+        c.dim = get_int("qwen2.embedding_length", get_int("llama.embedding_length", 0));
+        c.hidden_dim = get_int("qwen2.feed_forward_length", get_int("llama.feed_forward_length", 0));
+        c.n_heads = get_int("qwen2.attention.head_count", get_int("llama.attention.head_count", 0));
+        c.n_kv_heads = get_int("qwen2.attention.head_count_kv", get_int("llama.attention.head_count_kv", 0));
+        c.max_seq_len = get_int("qwen2.context_length", get_int("llama.context_length", 0));
+        c.rope_theta = get_float("qwen2.rope.freq_base", get_float("llama.rope.freq_base", 10000.0f));
+        c.rms_norm_eps = get_float("qwen2.attention.layer_norm_rms_epsilon",
+                                   get_float("llama.attention.layer_norm_rms_epsilon", 1e-5f));
+        // Without the token list the vocabulary keeps ModelConfig's default
+        // (include/mini_llama/model.h:18), as in the reference.
+        c.vocab_size = 128;
+        uint64_t vocab = 0;
+        if (g.get_string_array_size("tokenizer.ggml.tokens", vocab)) c.vocab_size = static_cast<int>(vocab);
+        if (c.n_layers <= 0 || c.dim <= 0 || c.hidden_dim <= 0 || c.n_heads <= 0 || c.n_kv_heads <= 0 ||
+            c.max_seq_len <= 0 || c.vocab_size <= 0) {
+            throw std::runtime_error("Failed to build config: Invalid model config from GGUF: dim=" +
+                                     std::to_string(c.dim) + " layers=" + std::to_string(c.n_layers) +
+                                     " heads=" + std::to_string(c.n_heads) + " vocab=" + std::to_string(c.vocab_size));
+        }
+        if (c.dim % c.n_heads != 0) throw std::runtime_error("Failed to build config: dim not divisible by n_heads");
+        if (c.n_heads % c.n_kv_heads != 0) {
+            throw std::runtime_error("Failed to build config: n_heads not divisible by n_kv_heads");
+        }
+        c.head_dim = c.dim / c.n_heads;
+    }
+    if (c.head_dim % 2 != 0 || c.head_dim > kMaxHeadDim) {
+        throw std::runtime_error("HIP decoder: head_dim " + std::to_string(c.head_dim) +
+                                 " is not supported (even, at most " + std::to_string(kMaxHeadDim) + ")");
+    }
+    if (max_seq_len > 0 && max_seq_len < c.max_seq_len) c.max_seq_len = max_seq_len;
+
+    std::unique_ptr<Decoder> d(new Decoder);
+    d->cfg_ = c;
+    d->device_ = device;
+    d->check(hipSetDevice(device), "hipSetDevice");
+    d->check(hipStreamCreateWithFlags(&d->stream_, hipStreamNonBlocking), "hipStreamCreateWithFlags");
+
+    auto alloc = [&](size_t bytes) {
+        void* p = nullptr;
+        d->check(hipMalloc(&p, bytes == 0 ? 4 : bytes), "hipMalloc");
+        d->allocs_.push_back(p);
+        return p;
+    };
+    auto upload = [&](const void* src, size_t bytes) {
+        void* p = alloc(bytes);
+        d->check(hipMemcpy(p, src, bytes, hipMemcpyHostToDevice), "hipMemcpy");
+        return p;
+    };
+
+    // Tensors by the loader's names (map_tensor_name, src/gguf_loader.cpp:15-84),
+    // reported under the model's names as load_weight does.
+    const std::string fail = "Failed to load GGUF weights: ";
+    auto tensor = [&](const std::string& gguf_name, const std::string& model_name, bool required) -> const GgufTensor* {
+        const int64_t i = g.find(gguf_name);
+        if (i < 0) {
+            if (required) throw std::runtime_error(fail + "Missing tensor: " + model_name);
+            return nullptr;
+        }
+        const GgufTensor& t = g.tensors[static_cast<size_t>(i)];
+        if (t.type != kGgmlF32 && qtype_of_ggml(t.type) < 0) {
+            if (t.nbytes == 0) throw std::runtime_error(fail + "Failed to read tensor: " + model_name);
+            throw std::runtime_error(fail + "Unsupported GGUF tensor type: " + std::to_string(t.type));
+        }
+        return &t;
+    };
+    auto shape_of = [](const GgufTensor& t) {
+        std::vector<int> s;
+        if (t.dims.size() == 2) return std::vector<int>{static_cast<int>(t.dims[1]), static_cast<int>(t.dims[0])};
+        for (uint64_t v : t.dims) s.push_back(static_cast<int>(v));
+        return s;
+    };
+    // F32 roles (load_f32): F32 as stored, quantized ones dequantized.
+    auto load_f32 = [&](const GgufTensor& t, const std::vector<int>& want, const std::string& what) -> float* {
+        const std::vector<int> s = shape_of(t);
+        if (s != want) {
+            throw std::runtime_error(fail + "GGUF " + what + ": shape mismatch. expected " + shape_text(want) +
+                                     ", got " + shape_text(s));
+        }
+        size_t numel = 1;
+        for (int v : s) numel *= static_cast<size_t>(v);
+        const uint8_t* src = g.tensor_data(t);
+        if (t.type == kGgmlF32) return static_cast<float*>(upload(src, numel * 4));
+        const size_t row = s.size() >= 2 ? static_cast<size_t>(s.back()) : numel;
+        std::vector<float> tmp(numel);
+        dequantize_rows(qtype_of_ggml(t.type), src, numel / row, row, tmp.data());
+        return static_cast<float*>(upload(tmp.data(), numel * 4));
+    };
+    auto load_linear = [&](const GgufTensor& t, int rows, int cols, const std::string& what) -> Linear {
+        const std::vector<int> s = shape_of(t);
+        const std::vector<int> want{rows, cols};
+        if (s != want) {
+            throw std::runtime_error(fail + "GGUF " + what + ": shape mismatch, expected " + shape_text(want) +
+                                     ", got " + shape_text(s));
+        }
+        Linear l;
+        l.qtype = t.type == kGgmlF32 ? 0 : qtype_of_ggml(t.type);
+        l.M = rows;
+        l.K = cols;
+        if (l.qtype != 0) {
+            const size_t need = static_cast<size_t>(rows) * ((cols + 31) / 32) * block_bytes(l.qtype);
+            if (need != t.nbytes) {
+                throw std::runtime_error(fail + "GGUF " + what + ": block count mismatch for " + shape_text(want));
+            }
+        }
+        l.data = upload(g.tensor_data(t), t.nbytes);
+        return l;
+    };
+
+    const int q_dim = c.n_heads * c.head_dim;
+    const int kv_dim = c.n_kv_heads * c.head_dim;
+    const GgufTensor* emb = tensor("token_embd.weight", "token_embedding", true);
+    d->layers_.resize(c.n_layers);
+    struct Pending {
+        const GgufTensor* t[12];
+    };
+    std::vector<Pending> lt(c.n_layers);
+    for (int l = 0; l < c.n_layers; ++l) {
+        const std::string gp = "blk." + std::to_string(l) + ".";
+        const std::string mp = "layers." + std::to_string(l) + ".";
+        Pending& p = lt[l];
+        p.t[0] = tensor(gp + "attn_norm.weight", mp + "attention_norm", true);
+        p.t[1] = tensor(gp + "attn_q.weight", mp + "wq", true);
+        p.t[2] = tensor(gp + "attn_k.weight", mp + "wk", true);
+        p.t[3] = tensor(gp + "attn_v.weight", mp + "wv", true);
+        p.t[4] = tensor(gp + "attn_q.bias", mp + "bq", false);
+        p.t[5] = tensor(gp + "attn_k.bias", mp + "bk", false);
+        p.t[6] = tensor(gp + "attn_v.bias", mp + "bv", false);
+        p.t[7] = tensor(gp + "attn_output.weight", mp + "wo", true);
+        p.t[8] = tensor(gp + "ffn_norm.weight", mp + "ffn_norm", true);
+        p.t[9] = tensor(gp + "ffn_gate.weight", mp + "w_gate", true);
+        p.t[10] = tensor(gp + "ffn_up.weight", mp + "w_up", true);
+        p.t[11] = tensor(gp + "ffn_down.weight", mp + "w_down", true);
+    }
+    const GgufTensor* fnorm = tensor("output_norm.weight", "final_norm", true);
+    const GgufTensor* out = tensor("output.weight", "lm_head", false);
+
+    // Shapes as validate_loaded_shapes (src/gguf_loader.cpp:204-238).
+    d->embedding_ = load_f32(*emb, {c.vocab_size, c.dim}, "token_embedding");
+    d->final_norm_ = load_f32(*fnorm, {c.dim}, "final_norm");
+    if (out != nullptr) {
+        d->lm_head_ = load_linear(*out, c.vocab_size, c.dim, "lm_head");
+    } else {  // tied: the F32 embedding serves as the output projection
+        d->lm_head_ = Linear{0, c.vocab_size, c.dim, d->embedding_};
+    }
+    for (int l = 0; l < c.n_layers; ++l) {
+        const std::string pre = "layers." + std::to_string(l) + ".";
+        Layer& L = d->layers_[l];
+        const Pending& p = lt[l];
+        L.attn_norm = load_f32(*p.t[0], {c.dim}, pre + "attention_norm");
+        L.wq = load_linear(*p.t[1], q_dim, c.dim, pre + "wq");
+        L.wk = load_linear(*p.t[2], kv_dim, c.dim, pre + "wk");
+        L.wv = load_linear(*p.t[3], kv_dim, c.dim, pre + "wv");
+        if (p.t[4]) L.bq = load_f32(*p.t[4], {q_dim}, pre + "bq");
+        if (p.t[5]) L.bk = load_f32(*p.t[5], {kv_dim}, pre + "bk");
+        if (p.t[6]) L.bv = load_f32(*p.t[6], {kv_dim}, pre + "bv");
+        L.wo = load_linear(*p.t[7], c.dim, q_dim, pre + "wo");
+        L.ffn_norm = load_f32(*p.t[8], {c.dim}, pre + "ffn_norm");
+        L.w_gate = load_linear(*p.t[9], c.hidden_dim, c.dim, pre + "w_gate");
+        L.w_up = load_linear(*p.t[10], c.hidden_dim, c.dim, pre + "w_up");
+        L.w_down = load_linear(*p.t[11], c.dim, c.hidden_dim, pre + "w_down");
+    }
+
+    // Activations, scratch, cache and state.
+    auto f32buf = [&](size_t n) { return static_cast<float*>(alloc(n * 4)); };
+    d->x_ = f32buf(c.dim);
+    d->h_ = f32buf(c.dim);
+    d->q_ = f32buf(q_dim);
+    d->k_ = f32buf(kv_dim);
+    d->v_ = f32buf(kv_dim);
+    d->att_ = f32buf(q_dim);
+    d->proj_ = f32buf(c.dim);
+    d->gate_ = f32buf(c.hidden_dim);
+    d->up_ = f32buf(c.hidden_dim);
+    d->act_ = f32buf(c.hidden_dim);
+    d->ff_ = f32buf(c.dim);
+    d->logits_ = f32buf(c.vocab_size);
+    d->scores_ = f32buf(static_cast<size_t>(c.n_heads) * c.max_seq_len);
+    const size_t cache = static_cast<size_t>(c.n_layers) * c.max_seq_len * kv_dim;
+    d->kcache_ = f32buf(cache);
+    d->vcache_ = f32buf(cache);
+    d->check(hipMemset(d->kcache_, 0, cache * 4), "hipMemset");
+    d->check(hipMemset(d->vcache_, 0, cache * 4), "hipMemset");
+    d->state_ = static_cast<DecodeState*>(alloc(sizeof(DecodeState)));
+    d->check(hipMemset(d->state_, 0, sizeof(DecodeState)), "hipMemset");
+    d->pick_ = alloc(sizeof(PickState));
+    d->check(hipMemset(d->pick_, 0, sizeof(PickState)), "hipMemset");
+    d->check(hipDeviceSynchronize(), "hipDeviceSynchronize");
+    return d;
+}
+
+Decoder::~Decoder() {
+    if (device_ >= 0) (void)hipSetDevice(device_);
+    if (stream_) (void)hipStreamSynchronize(stream_);
+    if (graph_) (void)hipGraphExecDestroy(graph_);
+    for (void* p : allocs_) (void)hipFree(p);
+    if (stream_) (void)hipStreamDestroy(stream_);
+}
+
+// ---------------------------------------------------------------- one step
+
+void Decoder::linear_group(hipStream_t s, const Linear* const* ws, float* const* ys, int n, const float* x) {
+    // Consecutive quantized weights of one format and width share a launch.
+    int i = 0;
+    while (i < n) {
+        const Linear& w = *ws[i];
+        if (w.qtype == 0) {
+            hipLaunchKernelGGL(gemv_f32_kernel, dim3((w.M + 3) / 4), dim3(256), 0, s,
+                               static_cast<const float*>(w.data), x, ys[i], w.M, w.K);
+            check(hipGetLastError(), "gemv_f32_kernel");
+            ++i;
+            continue;
+        }
+        GemvGroup g{};
+        int rows = 0;
+        int j = i;
+        while (j < n && j - i < kGroupMaxCalls && ws[j]->qtype == w.qtype && ws[j]->K == w.K) {
+            g.W[j - i] = ws[j]->data;
+            g.y[j - i] = ys[j];
+            g.row_begin[j - i] = rows;
+            rows += ws[j]->M;
+            ++j;
+        }
+        g.ncalls = j - i;
+        const LinearShape shape{w.qtype, rows, w.K, (w.K + 31) / 32, 1};
+        check(launch_gemv_group(shape, g, x, s), "launch_gemv_group");
+        i = j;
+    }
+}
+
+void Decoder::enqueue_step(hipStream_t s, bool pick, bool advance) {
+    const DecoderConfig& c = cfg_;
+    const int q_dim = c.n_heads * c.head_dim;
+    const int kv_dim = c.n_kv_heads * c.head_dim;
+    hipLaunchKernelGGL(embed_kernel, dim3((c.dim + 255) / 256), dim3(256), 0, s, embedding_, c.vocab_size, c.dim,
+                       state_, x_);
+    check(hipGetLastError(), "embed_kernel");
+    for (int l = 0; l < c.n_layers; ++l) {
+        const Layer& L = layers_[l];
+        hipLaunchKernelGGL(add_rmsnorm_kernel, dim3(1), dim3(kNormThreads), 0, s, x_, l == 0 ? nullptr : ff_,
+                           L.attn_norm, c.dim, c.rms_norm_eps, h_);
+        check(hipGetLastError(), "add_rmsnorm_kernel");
+        const Linear* qkv[3] = {&L.wq, &L.wk, &L.wv};
+        float* qkv_y[3] = {q_, k_, v_};
+        linear_group(s, qkv, qkv_y, 3, h_);
+        const int rope_threads = q_dim / 2 + kv_dim / 2 + kv_dim;
+        hipLaunchKernelGGL(rope_kv_kernel, dim3((rope_threads + 255) / 256), dim3(256), 0, s, q_, k_, v_, L.bq,
+                           L.bk, L.bv, c.n_heads, c.n_kv_heads, c.head_dim, c.rope_theta, c.rope_neox,
+                           c.max_seq_len, l, state_, kcache_, vcache_);
+        check(hipGetLastError(), "rope_kv_kernel");
+        hipLaunchKernelGGL(attention_kernel, dim3(c.n_heads), dim3(kAttnThreads), 0, s, q_, kcache_, vcache_,
+                           scores_, att_, c.n_heads, c.n_kv_heads, c.head_dim, c.max_seq_len, l, state_);
+        check(hipGetLastError(), "attention_kernel");
+        const Linear* wo[1] = {&L.wo};
+        float* wo_y[1] = {proj_};
+        linear_group(s, wo, wo_y, 1, att_);
+        hipLaunchKernelGGL(add_rmsnorm_kernel, dim3(1), dim3(kNormThreads), 0, s, x_, proj_, L.ffn_norm, c.dim,
+                           c.rms_norm_eps, h_);
+        check(hipGetLastError(), "add_rmsnorm_kernel");
+        const Linear* gu[2] = {&L.w_gate, &L.w_up};
+        float* gu_y[2] = {gate_, up_};
+        linear_group(s, gu, gu_y, 2, h_);
+        hipLaunchKernelGGL(swiglu_kernel, dim3((c.hidden_dim + 255) / 256), dim3(256), 0, s, gate_, up_, act_,
+                           c.hidden_dim);
+        check(hipGetLastError(), "swiglu_kernel");
+        const Linear* wd[1] = {&L.w_down};
+        float* wd_y[1] = {ff_};
+        linear_group(s, wd, wd_y, 1, act_);
+    }
+    if (!pick && advance) {  // a prompt step before the last: no logits needed
+        hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(64), 0, s, state_, io_);
+        check(hipGetLastError(), "advance_kernel");
+        return;
+    }
+    hipLaunchKernelGGL(add_rmsnorm_kernel, dim3(1), dim3(kNormThreads), 0, s, x_, ff_, final_norm_, c.dim,
+                       c.rms_norm_eps, h_);
+    check(hipGetLastError(), "add_rmsnorm_kernel");
+    if (pick && lm_head_.qtype != 0) {
+        const LinearShape shape{lm_head_.qtype, lm_head_.M, lm_head_.K, (lm_head_.K + 31) / 32, 1};
+        check(launch_gemv_pick(shape, lm_head_.data, h_, nullptr, static_cast<PickState*>(pick_), &state_->next, s),
+              "launch_gemv_pick");
+    } else {
+        const Linear* lm[1] = {&lm_head_};
+        float* lm_y[1] = {logits_};
+        linear_group(s, lm, lm_y, 1, h_);
+        if (pick) {
+            hipLaunchKernelGGL(pick_f32_kernel, dim3(1), dim3(1024), 0, s, logits_, c.vocab_size, state_);
+            check(hipGetLastError(), "pick_f32_kernel");
+        }
+    }
+    if (advance) {
+        hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(64), 0, s, state_, io_);
+        check(hipGetLastError(), "advance_kernel");
+    }
+}
+
+void Decoder::forward(int token, int pos, float* logits_host) {
+    const DecoderConfig& c = cfg_;
+    if (token < 0 || token >= c.vocab_size) throw std::out_of_range("forward_token token id out of range");
+    if (pos < 0 || pos >= c.max_seq_len) throw std::out_of_range("forward_token position out of range");
+    check(hipSetDevice(device_), "hipSetDevice");
+    DecodeState st{};
+    st.pos = pos;
+    st.token = token;
+    check(hipMemcpyAsync(state_, &st, sizeof st, hipMemcpyHostToDevice, stream_), "hipMemcpyAsync");
+    enqueue_step(stream_, false, false);
+    check(hipMemcpyAsync(logits_host, logits_, static_cast<size_t>(c.vocab_size) * 4, hipMemcpyDeviceToHost, stream_),
+          "hipMemcpyAsync");
+    check(hipMemcpyAsync(&st, state_, sizeof st, hipMemcpyDeviceToHost, stream_), "hipMemcpyAsync");
+    check(hipStreamSynchronize(stream_), "hipStreamSynchronize");
+    if (st.error != 0) throw std::runtime_error("HIP decoder: device step reported error " + std::to_string(st.error));
+}
+
+void Decoder::generate(const int* prompt, int n_prompt, int n_new, int* out) {
+    const DecoderConfig& c = cfg_;
+    if (n_prompt <= 0) throw std::runtime_error("forward_batch: empty batch");
+    if (n_new <= 0) return;
+    for (int i = 0; i < n_prompt; ++i) {
+        if (prompt[i] < 0 || prompt[i] >= c.vocab_size) throw std::out_of_range("forward_token token id out of range");
+    }
+    if (static_cast<long long>(n_prompt) + n_new - 1 > c.max_seq_len) {
+        throw std::out_of_range("forward_token position out of range");
+    }
+    check(hipSetDevice(device_), "hipSetDevice");
+    // One upload: the state, then the prompt; the generated tokens follow it.
+    const size_t need = static_cast<size_t>(n_prompt) + n_new;
+    if (need > io_cap_) {
+        check(hipStreamSynchronize(stream_), "hipStreamSynchronize");
+        if (graph_) {
+            (void)hipGraphExecDestroy(graph_);
+            graph_ = nullptr;
+        }
+        void* p = nullptr;
+        check(hipMalloc(&p, need * 4), "hipMalloc");
+        allocs_.push_back(p);
+        io_ = static_cast<int32_t*>(p);
+        io_cap_ = need;
+    }
+    DecodeState st{};
+    st.pos = 0;
+    st.token = prompt[0];
+    st.n_prompt = n_prompt;
+    st.n_out = n_new;
+    check(hipMemcpyAsync(state_, &st, sizeof st, hipMemcpyHostToDevice, stream_), "hipMemcpyAsync");
+    check(hipMemcpyAsync(io_, prompt, static_cast<size_t>(n_prompt) * 4, hipMemcpyHostToDevice, stream_),
+          "hipMemcpyAsync");
+    // Prompt steps before the last run without the lm_head; every later step
+    // picks and feeds the token back.  The decode step is recorded once.
+    for (int i = 0; i + 1 < n_prompt; ++i) enqueue_step(stream_, false, true);
+    if (graph_ == nullptr) {
+        hipGraph_t gr = nullptr;
+        check(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+        try {
+            enqueue_step(stream_, true, true);
+        } catch (...) {
+            (void)hipStreamEndCapture(stream_, &gr);
+            if (gr) (void)hipGraphDestroy(gr);
+            throw;
+        }
+        check(hipStreamEndCapture(stream_, &gr), "hipStreamEndCapture");
+        const hipError_t e = hipGraphInstantiate(&graph_, gr, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(gr);
+        check(e, "hipGraphInstantiate");
+    }
+    for (int i = 0; i < n_new; ++i) check(hipGraphLaunch(graph_, stream_), "hipGraphLaunch");
+    check(hipMemcpyAsync(out, io_ + n_prompt, static_cast<size_t>(n_new) * 4, hipMemcpyDeviceToHost, stream_),
+          "hipMemcpyAsync");
+    check(hipMemcpyAsync(&st, state_, sizeof st, hipMemcpyDeviceToHost, stream_), "hipMemcpyAsync");
+    check(hipStreamSynchronize(stream_), "hipStreamSynchronize");
+    if (st.error & kDecodeErrLogits) throw std::runtime_error("sampler: logits must be finite");
+    if (st.error != 0) throw std::runtime_error("HIP decoder: device step reported error " + std::to_string(st.error));
+}
+
+}  // namespace mlq

@@ -47,6 +47,7 @@
 // go to a simple one-wave-per-row kernel with byte loads.
 
 #include "gemv_device.h"
+#include "pick_key.h"
 
 #include <hip/hip_runtime.h>
 
@@ -105,18 +106,6 @@ __device__ __forceinline__ void load_rows(const GemvGroup& g, size_t row_dw, int
     }
 }
 
-// Greedy pick (argmax of y, first index on ties).  A row's key orders by
-// value, then by lower row: the float's bits mapped to an unsigned order
-// (-0 taken as +0, since the two compare equal) above the complemented row.
-// A value that is not finite gives the all-ones key, which decodes to -1.
-__device__ __forceinline__ unsigned long long pick_key(float v, int row) {
-    uint32_t b = __builtin_bit_cast(uint32_t, v);
-    if ((b & 0x7F800000u) == 0x7F800000u) return ~0ull;
-    b = b == 0x80000000u ? 0u : b;
-    const uint32_t ord = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-    return (static_cast<unsigned long long>(ord) << 32) | static_cast<uint32_t>(~static_cast<uint32_t>(row));
-}
-
 // Folds every lane's key into the launch's result; called once by every
 // thread of every workgroup.  The workgroup's best key goes to its group slot
 // with one atomic max, then the workgroup arrives; the last arrival of the
@@ -153,7 +142,7 @@ __device__ __forceinline__ void pick_finish(PickState* ps, int32_t* token, unsig
         const unsigned long long v = __hip_atomic_exchange(&ps->key[i][0], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         k = v > k ? v : k;
     }
-    *token = k == ~0ull ? -1 : static_cast<int32_t>(~static_cast<uint32_t>(k));
+    *token = pick_token(k);
 }
 
 // Waves per SIMD the single kernel's registers are bounded for: four (two

@@ -289,6 +289,7 @@ bool GgufIndex::open(const std::string& path) {
             error = "failed to read metadata type for key: " + m.key;
             return false;
         }
+        m.value_pos = c.pos;
         if (!render_value(c, m.type, m.value)) {
             error = "failed to read metadata value for key: " + m.key;
             return false;
@@ -377,6 +378,70 @@ bool GgufIndex::open(const std::string& path) {
 const uint8_t* GgufIndex::tensor_data(const GgufTensor& t) const {
     if (t.nbytes == 0 || base_ == nullptr) return nullptr;
     return base_ + data_offset + t.offset;
+}
+
+namespace {
+
+const GgufMeta* meta_of(const std::vector<GgufMeta>& meta, const std::string& key) {
+    for (const GgufMeta& m : meta) {
+        if (m.key == key) return &m;
+    }
+    return nullptr;
+}
+
+template <typename T>
+T read_at(const uint8_t* base, uint64_t pos) {
+    T v;
+    std::memcpy(&v, base + pos, sizeof(T));
+    return v;
+}
+
+}  // namespace
+
+bool GgufIndex::get_int(const std::string& key, int64_t& out) const {
+    const GgufMeta* m = meta_of(metadata, key);
+    if (m == nullptr) return false;
+    const uint64_t p = m->value_pos;
+    switch (m->type) {
+        case kU8: out = read_at<uint8_t>(base_, p); return true;
+        case kI8: out = read_at<int8_t>(base_, p); return true;
+        case kU16: out = read_at<uint16_t>(base_, p); return true;
+        case kI16: out = read_at<int16_t>(base_, p); return true;
+        case kU32: out = read_at<uint32_t>(base_, p); return true;
+        case kI32: out = read_at<int32_t>(base_, p); return true;
+        case kU64: out = static_cast<int64_t>(read_at<uint64_t>(base_, p)); return true;
+        case kI64: out = read_at<int64_t>(base_, p); return true;
+        default: return false;
+    }
+}
+
+bool GgufIndex::get_float(const std::string& key, double& out) const {
+    const GgufMeta* m = meta_of(metadata, key);
+    if (m == nullptr) return false;
+    if (m->type == kF32) {
+        out = static_cast<double>(read_at<float>(base_, m->value_pos));
+        return true;
+    }
+    if (m->type == kF64) {
+        out = read_at<double>(base_, m->value_pos);
+        return true;
+    }
+    return false;
+}
+
+bool GgufIndex::get_string(const std::string& key, std::string& out) const {
+    const GgufMeta* m = meta_of(metadata, key);
+    if (m == nullptr || m->type != kString) return false;
+    out = m->value;
+    return true;
+}
+
+bool GgufIndex::get_string_array_size(const std::string& key, uint64_t& out) const {
+    const GgufMeta* m = meta_of(metadata, key);
+    if (m == nullptr || m->type != kArray) return false;
+    if (read_at<uint32_t>(base_, m->value_pos) != kString) return false;
+    out = read_at<uint64_t>(base_, m->value_pos + 4);
+    return true;
 }
 
 int64_t GgufIndex::find(const std::string& name) const {

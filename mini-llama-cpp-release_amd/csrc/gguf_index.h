@@ -24,6 +24,7 @@ struct GgufMeta {
     std::string key;
     uint32_t type = 0;   // GGUF value type (include/mini_llama/gguf.h:27-41)
     std::string value;   // rendered as the reference renders it
+    uint64_t value_pos = 0;  // file offset of the value
 };
 
 struct GgufTensor {
@@ -48,6 +49,15 @@ public:
     const uint8_t* tensor_data(const GgufTensor& t) const;
     // Index of the tensor called `name`, or -1.
     int64_t find(const std::string& name) const;
+
+    // Typed metadata reads with the acceptance rules of gguf_get_metadata_int /
+    // _float / _string / _string_array (src/gguf.cpp:674-820): integers of any
+    // width and sign, float32 / float64, strings, and the element count of an
+    // array of strings.  False when the key is absent or has another type.
+    bool get_int(const std::string& key, int64_t& out) const;
+    bool get_float(const std::string& key, double& out) const;
+    bool get_string(const std::string& key, std::string& out) const;
+    bool get_string_array_size(const std::string& key, uint64_t& out) const;
 
     uint32_t version = 0;
     uint64_t n_tensors = 0;

@@ -6,6 +6,7 @@
 // replaced by "hip".  Every check runs on the host before any launch, so a
 // malformed call never reaches a kernel.
 
+#include "decoder.h"
 #include "gguf_index.h"
 #include "mlq_kernels.h"
 
@@ -16,7 +17,9 @@
 #include <algorithm>
 #include <cstdio>
 #include <cstring>
+#include <memory>
 #include <mutex>
+#include <stdexcept>
 #include <string>
 #include <vector>
 
@@ -33,6 +36,10 @@ struct mlq_weight_s {
 
 struct mlq_gguf_s {
     mlq::GgufIndex index;
+};
+
+struct mlq_decoder_s {
+    std::unique_ptr<mlq::Decoder> dec;
 };
 
 struct mlq_graph_s {
@@ -1341,6 +1348,60 @@ int mlq_hip_gguf_upload_weight(mlq_gguf_t g, const char* name, int device, mlq_w
         return rc;
     }
     *out = new mlq_weight_s{device, qtype, M, K, nb, n_blocks, ptr, true};
+    return MLQ_OK;
+}
+
+int mlq_hip_decoder_open(const char* gguf_path, int device, int max_seq_len, mlq_decoder_t* out) {
+    if (out == nullptr) return fail(MLQ_ERR_INVALID, "mlq_hip_decoder_open: null output");
+    *out = nullptr;
+    if (gguf_path == nullptr) return fail(MLQ_ERR_INVALID, "mlq_hip_decoder_open: null path");
+    int rc = ensure_device(device);
+    if (rc != MLQ_OK) return rc;
+    try {
+        std::unique_ptr<mlq::Decoder> d = mlq::Decoder::from_gguf(gguf_path, device, max_seq_len);
+        *out = new mlq_decoder_s{std::move(d)};
+    } catch (const std::exception& e) {
+        return fail(MLQ_ERR_INVALID, e.what());
+    }
+    return MLQ_OK;
+}
+
+int mlq_hip_decoder_config(mlq_decoder_t d, mlq_decoder_config* out) {
+    if (d == nullptr || out == nullptr) return fail(MLQ_ERR_INVALID, "mlq_hip_decoder_config: null argument");
+    const mlq::DecoderConfig& c = d->dec->config();
+    *out = mlq_decoder_config{c.n_layers, c.dim, c.hidden_dim, c.n_heads, c.n_kv_heads, c.head_dim,
+                              c.vocab_size, c.max_seq_len, c.rope_theta, c.rms_norm_eps, c.rope_neox};
+    return MLQ_OK;
+}
+
+int mlq_hip_decoder_forward(mlq_decoder_t d, int token, int pos, float* logits) {
+    if (d == nullptr || logits == nullptr) return fail(MLQ_ERR_INVALID, "mlq_hip_decoder_forward: null argument");
+    try {
+        d->dec->forward(token, pos, logits);
+    } catch (const std::out_of_range& e) {
+        return fail(MLQ_ERR_SHAPE, e.what());
+    } catch (const std::exception& e) {
+        return fail(MLQ_ERR_INVALID, e.what());
+    }
+    return MLQ_OK;
+}
+
+int mlq_hip_decoder_generate(mlq_decoder_t d, const int* prompt, int n_prompt, int n_new, int* out_tokens) {
+    if (d == nullptr || prompt == nullptr || (n_new > 0 && out_tokens == nullptr)) {
+        return fail(MLQ_ERR_INVALID, "mlq_hip_decoder_generate: null argument");
+    }
+    try {
+        d->dec->generate(prompt, n_prompt, n_new, out_tokens);
+    } catch (const std::out_of_range& e) {
+        return fail(MLQ_ERR_SHAPE, e.what());
+    } catch (const std::exception& e) {
+        return fail(MLQ_ERR_INVALID, e.what());
+    }
+    return MLQ_OK;
+}
+
+int mlq_hip_decoder_close(mlq_decoder_t d) {
+    delete d;
     return MLQ_OK;
 }
 

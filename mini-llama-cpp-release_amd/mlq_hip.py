@@ -39,6 +39,12 @@ class LinearCall(ctypes.Structure):
     _fields_ = [("w", _vp), ("x", _vp), ("y", _vp), ("rows", ctypes.c_int)]
 
 
+class DecoderConfig(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int) for n in ("n_layers", "dim", "hidden_dim", "n_heads", "n_kv_heads", "head_dim",
+                                              "vocab_size", "max_seq_len")] + \
+               [("rope_theta", ctypes.c_float), ("rms_norm_eps", ctypes.c_float), ("rope_neox", ctypes.c_int)]
+
+
 _LIB = None
 
 _SIGS = {
@@ -93,6 +99,11 @@ _SIGS = {
     "mlq_hip_gguf_tensor_data": (ctypes.c_int, [_vp, ctypes.c_uint64, ctypes.POINTER(_vp),
                                                  ctypes.POINTER(ctypes.c_uint64)]),
     "mlq_hip_gguf_upload_weight": (ctypes.c_int, [_vp, ctypes.c_char_p, ctypes.c_int, ctypes.POINTER(_vp)]),
+    "mlq_hip_decoder_open": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_int, ctypes.c_int, ctypes.POINTER(_vp)]),
+    "mlq_hip_decoder_config": (ctypes.c_int, [_vp, ctypes.POINTER(DecoderConfig)]),
+    "mlq_hip_decoder_forward": (ctypes.c_int, [_vp, ctypes.c_int, ctypes.c_int, _vp]),
+    "mlq_hip_decoder_generate": (ctypes.c_int, [_vp, _vp, ctypes.c_int, ctypes.c_int, _vp]),
+    "mlq_hip_decoder_close": (ctypes.c_int, [_vp]),
     "mlq_hip_graph_begin": (ctypes.c_int, [ctypes.c_int, _vp]),
     "mlq_hip_graph_end": (ctypes.c_int, [ctypes.c_int, _vp, ctypes.POINTER(_vp)]),
     "mlq_hip_sequence_create": (ctypes.c_int, [ctypes.POINTER(LinearCall), ctypes.c_int,
@@ -473,6 +484,40 @@ class GgufFile:
     def close(self) -> None:
         if getattr(self, "h", None):
             _LIB.mlq_hip_gguf_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Decoder:
+    """A GGUF model decoding on the device (mlq_hip_decoder_*)."""
+
+    def __init__(self, path: str, device: int = 0, max_seq_len: int = 0):
+        h = _vp()
+        _check(load().mlq_hip_decoder_open(os.fsencode(path), device, max_seq_len, ctypes.byref(h)))
+        self.h = h.value
+        c = DecoderConfig()
+        _check(_LIB.mlq_hip_decoder_config(self.h, ctypes.byref(c)))
+        self.config = {n: getattr(c, n) for n, _ in DecoderConfig._fields_}
+
+    def forward(self, token: int, pos: int) -> np.ndarray:
+        logits = np.empty(self.config["vocab_size"], np.float32)
+        _check(_LIB.mlq_hip_decoder_forward(self.h, token, pos, logits.ctypes.data))
+        return logits
+
+    def generate(self, prompt, n_new: int) -> list:
+        p = np.ascontiguousarray(prompt, np.int32)
+        out = np.zeros(max(n_new, 1), np.int32)
+        _check(_LIB.mlq_hip_decoder_generate(self.h, p.ctypes.data, p.size, n_new, out.ctypes.data))
+        return out[:n_new].tolist()
+
+    def close(self) -> None:
+        if getattr(self, "h", None):
+            _LIB.mlq_hip_decoder_close(self.h)
             self.h = None
 
     def __del__(self):

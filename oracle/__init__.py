@@ -257,6 +257,9 @@ class Reference(_Lib):
         finally:
             free(h)
 
+    def decoder(self, path: str) -> "RefDecoder":
+        return RefDecoder(self, path)
+
     def fp16_probe_q4_1(self, v: float) -> int:
         return int(self._p41(float(v)))
 
@@ -319,6 +322,53 @@ class RefWeight:
     def __del__(self):
         if getattr(self, "h", None):
             self.ref._wfree(self.h)
+            self.h = None
+
+
+class RefDecoder:
+    """load_gguf_model + forward_token of the reference (CPU, f32)."""
+
+    def __init__(self, ref: Reference, path: str):
+        vp, cp = ctypes.c_void_p, ctypes.c_char_p
+        self._open = ref._fn("decoder_open", vp, [cp, ctypes.POINTER(ctypes.c_int)])
+        self._err = ref._fn("decoder_error", cp, [vp])
+        self._free = ref._fn("decoder_free", None, [vp])
+        self._cfg = ref._fn("decoder_config", None, [vp, ctypes.POINTER(ctypes.c_int)])
+        self._fwd = ref._fn("decoder_forward", ctypes.c_int,
+                            [vp, ctypes.c_int, ctypes.c_int, _f32p, ctypes.c_char_p, ctypes.c_size_t])
+        self._gen = ref._fn("decoder_generate", ctypes.c_int,
+                            [vp, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_char_p,
+                             ctypes.c_size_t])
+        ok = ctypes.c_int(0)
+        self.h = self._open(os.fsencode(path), ctypes.byref(ok))
+        if not ok.value:
+            msg = self._err(self.h).decode()
+            self._free(self.h)
+            self.h = None
+            raise RuntimeError(msg)
+        c = (ctypes.c_int * 9)()
+        self._cfg(self.h, c)
+        self.config = dict(zip(("n_layers", "dim", "hidden_dim", "n_heads", "n_kv_heads", "head_dim", "vocab_size",
+                                "max_seq_len", "rope_neox"), list(c)))
+
+    def forward(self, token: int, pos: int) -> np.ndarray:
+        out = np.empty(self.config["vocab_size"], np.float32)
+        err = ctypes.create_string_buffer(512)
+        if self._fwd(self.h, token, pos, _ptr(out, _f32p), err, 512) != 0:
+            raise RuntimeError(err.value.decode())
+        return out
+
+    def generate(self, prompt, n_new: int) -> list:
+        p = np.ascontiguousarray(prompt, np.int32)
+        out = np.zeros(max(n_new, 1), np.int32)
+        err = ctypes.create_string_buffer(512)
+        if self._gen(self.h, _ptr(p), p.size, n_new, _ptr(out), err, 512) != 0:
+            raise RuntimeError(err.value.decode())
+        return out[:n_new].tolist()
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            self._free(self.h)
             self.h = None
 
 

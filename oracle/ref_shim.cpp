@@ -15,7 +15,10 @@
 #include "tests/test_cuda_quant.cpp"
 #undef main
 
+#include "mini_llama/context.h"
+#include "mini_llama/forward.h"
 #include "mini_llama/gguf.h"
+#include "mini_llama/sampler.h"
 #include "mini_llama/gguf_loader.h"
 #include "mini_llama/model.h"
 #include "mini_llama/ops.h"
@@ -23,6 +26,7 @@
 #include "mini_llama/thread_pool.h"
 
 #include <cstdio>
+#include <memory>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -286,6 +290,71 @@ int mlq_ref_model_linear(void* h, const char* name, int* qtype, int* rows, int* 
         default: *data = q->f32_data.data(); *nbytes = q->f32_data.size() * sizeof(float); break;
     }
     return 0;
+}
+
+// ---- Decode: load_gguf_model + forward_token (src/forward.cpp:865-903)
+
+struct RefDecoder {
+    MiniLlamaModel model;
+    std::unique_ptr<MiniLlamaContext> ctx;
+};
+
+void* mlq_ref_decoder_open(const char* path, int* ok) {
+    RefDecoder* d = new RefDecoder;
+    d->model = load_gguf_model(path);
+    *ok = d->model.loaded ? 1 : 0;
+    if (d->model.loaded) d->ctx.reset(new MiniLlamaContext(&d->model));
+    return d;
+}
+
+const char* mlq_ref_decoder_error(void* h) { return static_cast<RefDecoder*>(h)->model.load_error.c_str(); }
+
+void mlq_ref_decoder_free(void* h) { delete static_cast<RefDecoder*>(h); }
+
+void mlq_ref_decoder_config(void* h, int* out) {
+    const ModelConfig& c = static_cast<RefDecoder*>(h)->model.config;
+    const int v[] = {c.n_layers, c.dim, c.hidden_dim, c.n_heads, c.n_kv_heads, c.head_dim, c.vocab_size,
+                     c.max_seq_len, c.rope_type == RopeType::NeoX ? 1 : 0};
+    std::memcpy(out, v, sizeof v);
+}
+
+// forward_token with ctx.pos = pos; logits to `out`.  Returns 0, or -1 with
+// the exception text in err.
+int mlq_ref_decoder_forward(void* h, int token, int pos, float* out, char* err, size_t err_len) {
+    RefDecoder* d = static_cast<RefDecoder*>(h);
+    try {
+        d->ctx->pos = pos;
+        Tensor logits = forward_token(d->model, *d->ctx, token);
+        std::memcpy(out, logits.data.data(), logits.data.size() * sizeof(float));
+        return 0;
+    } catch (const std::exception& e) {
+        std::snprintf(err, err_len, "%s", e.what());
+        return -1;
+    }
+}
+
+// Greedy generation as forward_batch over the prompt, then sample_greedy and
+// forward_token per new token.
+int mlq_ref_decoder_generate(void* h, const int* prompt, int n_prompt, int n_new, int* out, char* err,
+                             size_t err_len) {
+    RefDecoder* d = static_cast<RefDecoder*>(h);
+    try {
+        std::vector<int> toks(prompt, prompt + n_prompt);
+        Tensor logits = forward_batch(d->model, *d->ctx, MiniBatch::from_tokens(toks, 0));
+        int pos = n_prompt;
+        for (int i = 0; i < n_new; ++i) {
+            const int t = MiniSampler::sample_greedy(logits);
+            out[i] = t;
+            if (i + 1 < n_new) {
+                d->ctx->pos = pos++;
+                logits = forward_token(d->model, *d->ctx, t);
+            }
+        }
+        return 0;
+    } catch (const std::exception& e) {
+        std::snprintf(err, err_len, "%s", e.what());
+        return -1;
+    }
 }
 
 }  // extern "C"
