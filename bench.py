@@ -312,6 +312,89 @@ def ingest_bench(layers=4):
             "note": "file in the page cache; host-to-device over PCIe; synthetic Q4_0 blocks"}
 
 
+def write_llama7b_q4_0(path, layers=32):
+    """A LLaMA-7B-shaped Q4_0 model file (dim 4096, hidden 11008, 32 heads,
+    vocab 32000; F32 embedding and norms, Q4_0 linears and lm_head) with
+    synthetic weights: random nibbles, block scale 2^-10.  Returns its bytes."""
+    sys.path.insert(0, os.path.join(REPO, "tests"))
+    import gguf_writer as gw
+
+    dim, hidden, heads, vocab = 4096, 11008, 32, 32000
+    rng = np.random.default_rng(5)
+    meta = [("general.architecture", gw.STRING, "llama"), ("llama.block_count", gw.U32, layers),
+            ("llama.embedding_length", gw.U32, dim), ("llama.feed_forward_length", gw.U32, hidden),
+            ("llama.attention.head_count", gw.U32, heads), ("llama.attention.head_count_kv", gw.U32, heads),
+            ("llama.context_length", gw.U32, 4096), ("llama.rope.freq_base", gw.F32, 10000.0),
+            ("llama.attention.layer_norm_rms_epsilon", gw.F32, 1e-5),
+            ("tokenizer.ggml.tokens", gw.ARRAY, (gw.STRING, [f"t{i}" for i in range(vocab)]))]
+    specs, kinds = [], []
+
+    def q40(name, m, k):
+        specs.append((name, [k, m], gw.GGML_Q4_0, m * (k // 32) * 18))
+        kinds.append(("q", m, k))
+
+    def f32(name, shape):
+        n = int(np.prod(shape))
+        specs.append((name, list(reversed(shape)), gw.GGML_F32, 4 * n))
+        kinds.append(("f", n, 0))
+
+    f32("token_embd.weight", (vocab, dim))
+    for l in range(layers):
+        p = f"blk.{l}."
+        f32(p + "attn_norm.weight", (dim,))
+        for n in ("attn_q", "attn_k", "attn_v", "attn_output"):
+            q40(p + n + ".weight", dim, dim)
+        f32(p + "ffn_norm.weight", (dim,))
+        q40(p + "ffn_gate.weight", hidden, dim)
+        q40(p + "ffn_up.weight", hidden, dim)
+        q40(p + "ffn_down.weight", dim, hidden)
+    f32("output_norm.weight", (dim,))
+    q40("output.weight", vocab, dim)
+
+    def produce(i):
+        kind, a, b = kinds[i]
+        if kind == "f":
+            sd, mean = (0.01, 1.0) if a <= 65536 else (0.02, 0.0)
+            return (mean + sd * rng.standard_normal(a)).astype(np.float32).tobytes()
+        blocks = rng.integers(0, 256, (a * (b // 32), 18), dtype=np.uint8)
+        blocks[:, 0:2] = np.array([0x1400], np.uint16).view(np.uint8)  # d = 2^-10
+        return blocks.tobytes()
+
+    gw.write_stream(path, meta, specs, produce)
+    return sum(x[3] for x in specs)
+
+
+def decode_bench(n_new=128, layers=32):
+    """Greedy decode on the LLaMA-7B-shaped Q4_0 model of write_llama7b_q4_0
+    through mlq_hip_decoder_generate: every op on the device, the picked token
+    fed back on the device, one recorded step replayed per token."""
+    import tempfile
+
+    fd, path = tempfile.mkstemp(suffix=".gguf")
+    os.close(fd)
+    try:
+        t0 = time.perf_counter()
+        nbytes = write_llama7b_q4_0(path, layers)
+        t_write = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        dec = hip.Decoder(path, max_seq_len=1024)
+        t_load = time.perf_counter() - t0
+    finally:
+        os.unlink(path)
+    prompt = [1, 2, 3, 4]
+    dec.generate(prompt, 8)  # records the step
+    t0 = time.perf_counter()
+    toks = dec.generate(prompt, n_new)
+    dt = time.perf_counter() - t0
+    dec.close()
+    return {"model": "llama7b-shaped q4_0 (synthetic weights)", "layers": layers, "prompt_tokens": len(prompt),
+            "new_tokens": n_new, "s": round(dt, 4), "tokens_per_s": round(n_new / dt, 1),
+            "ms_per_token": round(dt * 1e3 / n_new, 3), "distinct_tokens": len(set(toks)),
+            "file_gb": round(nbytes / 1e9, 3), "s_write_file": round(t_write, 2), "s_load": round(t_load, 2),
+            "note": "wall time of one mlq_hip_decoder_generate call (prompt steps, recorded step replayed per "
+                    "token, one upload, one download); attention over positions 0..131"}
+
+
 PICK_CONFIGS = ([("c2_qwen_lm_head", qt, 151936, 896) for qt in (hip.Q8_0, hip.Q4_0, hip.Q4_1)] +
                 [("c3_llama_lm_head", qt, 32000, 4096) for qt in (hip.Q8_0, hip.Q4_0, hip.Q4_1)])
 
@@ -509,6 +592,12 @@ def main():
                 f"token {r['token']}")
             picks.append(r)
 
+    decode = None
+    if not args.no_shapes:
+        decode = decode_bench()
+        log(f"  decode {decode['model']}: {decode['tokens_per_s']} tokens/s ({decode['ms_per_token']} ms/token), "
+            f"load {decode['s_load']} s")
+
     ingest = None
     if not args.no_shapes:
         ingest = ingest_bench()
@@ -573,6 +662,7 @@ def main():
         "gemv": shapes,
         "lm_head_argmax": picks,
         "gguf_ingest": ingest,
+        "decode": decode,
         "gemm": gemm,
     }
     print(json.dumps(out), flush=True)

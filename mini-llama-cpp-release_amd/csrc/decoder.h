@@ -91,6 +91,8 @@ private:
     };
 
     void linear_group(hipStream_t s, const Linear* const* ws, float* const* ys, int n, const float* x);
+    bool launch_attention_rope(hipStream_t s, int layer);
+    void launch_norm(hipStream_t s, const float* delta, const float* w);
 
     DecoderConfig cfg_;
     int device_ = 0;

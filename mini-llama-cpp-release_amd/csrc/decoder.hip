@@ -26,6 +26,8 @@ namespace {
 
 constexpr int kNormThreads = 1024;
 constexpr int kAttnThreads = 256;
+constexpr int kFlashThreads = 512;
+constexpr int kFlashAhead = 4;
 constexpr int kMaxHeadDim = 256;
 
 // Sum (or max) over a workgroup of `nthreads`; every thread gets the result.
@@ -75,6 +77,49 @@ __global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(float* __rest
     ss = wg_reduce<kNormThreads, false>(ss, part);
     const float scale = 1.0f / sqrtf(ss / static_cast<float>(dim) + eps);
     for (int i = threadIdx.x; i < dim; i += kNormThreads) out[i] = x[i] * scale * w[i];
+}
+
+// The same for dim <= 4 * kNormThreads * VEC (x 16-byte aligned, dim % 4 == 0):
+// every thread loads its float4s of x, delta and w once, keeps them in
+// registers through the reduction and stores the results (one round trip to
+// memory instead of three).
+template <int VEC>
+__global__ __launch_bounds__(kNormThreads) void add_rmsnorm_vec_kernel(float* __restrict__ x,
+                                                                       const float* __restrict__ delta,
+                                                                       const float* __restrict__ w, int dim, float eps,
+                                                                       float* __restrict__ out) {
+    __shared__ float part[kNormThreads / 64];
+    const int n4 = dim / 4;
+    float4 xv[VEC], wv[VEC];
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) {
+        const int i = threadIdx.x + j * kNormThreads;
+        const int ic = min(i, n4 - 1);
+        float4 a = reinterpret_cast<const float4*>(x)[ic];
+        wv[j] = reinterpret_cast<const float4*>(w)[ic];
+        if (delta != nullptr) {
+            const float4 d = reinterpret_cast<const float4*>(delta)[ic];
+            a.x = a.x + d.x;
+            a.y = a.y + d.y;
+            a.z = a.z + d.z;
+            a.w = a.w + d.w;
+        }
+        xv[j] = a;
+        if (i < n4) ss += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w;
+    }
+    ss = wg_reduce<kNormThreads, false>(ss, part);
+    const float scale = 1.0f / sqrtf(ss / static_cast<float>(dim) + eps);
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) {
+        const int i = threadIdx.x + j * kNormThreads;
+        if (i < n4) {
+            const float4 a = xv[j];
+            if (delta != nullptr) reinterpret_cast<float4*>(x)[i] = a;
+            reinterpret_cast<float4*>(out)[i] = make_float4(a.x * scale * wv[j].x, a.y * scale * wv[j].y,
+                                                            a.z * scale * wv[j].z, a.w * scale * wv[j].w);
+        }
+    }
 }
 
 // Optional q/k/v biases, RoPE on q and k (src/ops.cpp:109-175: normal pairs
@@ -184,6 +229,155 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
         float r = 0.0f;
         for (int gg = 0; gg < groups; ++gg) r += acc_part[gg * hd + threadIdx.x];
         out[h * hd + threadIdx.x] = r;
+    }
+}
+
+// Decode attention for one query head per workgroup with the step's RoPE,
+// biases and KV-cache write folded in (head_dim = 4 * LPR, a power of two up
+// to 256).  Each workgroup rotates its q head and its kv head's k (as
+// rope_kv_kernel does), uses this position's k and v from LDS and writes them
+// to the cache when it is the first query head of its kv group; earlier
+// positions come from the cache.  A cache row is read as LPR float4s by LPR
+// lanes, ROWS = 256 / LPR rows at a time, so every load is a coalesced row
+// segment.  The softmax is folded into the same pass (running maximum, sum
+// and weighted v per row group, rescaled when the maximum grows), and the
+// row groups are merged once at the end: sum_t e^(s_t - m) v_t / sum_t
+// e^(s_t - m), the reference's softmax-then-sum to rounding.  The first
+// cache rows are requested before the RoPE math, which hides their latency.
+template <int LPR>
+__global__ __launch_bounds__(kFlashThreads) void attention_rope_kernel(
+    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+    const float* __restrict__ bq, const float* __restrict__ bk, const float* __restrict__ bv, int n_heads, int n_kv,
+    float theta, int neox, int max_seq, int layer, DecodeState* st, float* __restrict__ kc,
+    float* __restrict__ vc, float* __restrict__ out) {
+    constexpr int HD = 4 * LPR;
+    constexpr int ROWS = kFlashThreads / LPR;
+    __shared__ float4 qs4[LPR], ks4[LPR], vs4[LPR];
+    __shared__ float gm[ROWS], gl[ROWS];
+    __shared__ float4 gacc[ROWS][LPR];
+    float* qs = reinterpret_cast<float*>(qs4);
+    float* ks = reinterpret_cast<float*>(ks4);
+    float* vs = reinterpret_cast<float*>(vs4);
+    const int tid = threadIdx.x;
+    const int h = blockIdx.x;
+    const int group = n_heads / n_kv;
+    const int kvh = h / group;
+    const int p0 = st->pos;
+    const bool ok = p0 >= 0 && p0 < max_seq;
+    if (!ok && h == 0 && tid == 0) st->error |= kDecodeErrPos;
+    const int pos = ok ? p0 : 0;
+    const int last = pos > 0 ? pos - 1 : 0;  // rows read from the cache stay below pos
+    const size_t layer_base = static_cast<size_t>(layer) * max_seq * n_kv * HD;
+    const size_t t_stride = static_cast<size_t>(n_kv) * HD;
+    const float* kbase = kc + layer_base + kvh * HD;
+    const float* vbase = vc + layer_base + kvh * HD;
+    const int lr = tid / LPR;
+    const int li = tid % LPR;
+    // This row group's first kFlashAhead cache rows, requested ahead of the
+    // RoPE math (rows past the last cached one re-read it and are not used).
+    float4 kr[kFlashAhead], vr[kFlashAhead];
+#pragma unroll
+    for (int j = 0; j < kFlashAhead; ++j) {
+        const int tj = min(lr + j * ROWS, last);
+        kr[j] = *reinterpret_cast<const float4*>(kbase + tj * t_stride + 4 * li);
+        vr[j] = *reinterpret_cast<const float4*>(vbase + tj * t_stride + 4 * li);
+    }
+    const int half = HD / 2;
+    if (tid < HD) {
+        // Threads 0..half-1 rotate pair tid of q, threads half..HD-1 pair
+        // tid - half of k; every thread adds v's bias for element tid.
+        const bool is_q = tid < half;
+        const int r = is_q ? tid : tid - half;
+        const int i0 = neox ? r : 2 * r;
+        const int i1 = neox ? i0 + half : i0 + 1;
+        const float freq = 1.0f / powf(theta, static_cast<float>(2 * r) / static_cast<float>(HD));
+        const float ang = static_cast<float>(pos) * freq;
+        const float c = cosf(ang);
+        const float s = sinf(ang);
+        const float* src = is_q ? q + h * HD : k + kvh * HD;
+        const float* b = is_q ? (bq ? bq + h * HD : nullptr) : (bk ? bk + kvh * HD : nullptr);
+        float a0 = src[i0];
+        float a1 = src[i1];
+        if (b != nullptr) {
+            a0 = a0 + b[i0];
+            a1 = a1 + b[i1];
+        }
+        float* dst = is_q ? qs : ks;
+        dst[i0] = a0 * c - a1 * s;
+        dst[i1] = a0 * s + a1 * c;
+        vs[tid] = bv != nullptr ? v[kvh * HD + tid] + bv[kvh * HD + tid] : v[kvh * HD + tid];
+    }
+    __syncthreads();
+    if (h % group == 0 && tid < HD) {
+        kc[layer_base + pos * t_stride + kvh * HD + tid] = ks[tid];
+        vc[layer_base + pos * t_stride + kvh * HD + tid] = vs[tid];
+    }
+    const float4 qv = qs4[li];
+    const float scale = 1.0f / sqrtf(static_cast<float>(HD));
+    float m = -INFINITY;
+    float l = 0.0f;
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int t0 = lr; t0 <= pos; t0 += kFlashAhead * ROWS) {
+        float4 kc4[kFlashAhead], vc4[kFlashAhead];
+#pragma unroll
+        for (int j = 0; j < kFlashAhead; ++j) {
+            kc4[j] = kr[j];
+            vc4[j] = vr[j];
+        }
+        // The next kFlashAhead rows, requested before these are used -- only
+        // when another pass follows: requests left outstanding at the loop's
+        // end would be waited for at the merge's barrier.
+        if (t0 + kFlashAhead * ROWS <= pos) {
+#pragma unroll
+            for (int j = 0; j < kFlashAhead; ++j) {
+                const int tj = min(t0 + (kFlashAhead + j) * ROWS, last);
+                kr[j] = *reinterpret_cast<const float4*>(kbase + tj * t_stride + 4 * li);
+                vr[j] = *reinterpret_cast<const float4*>(vbase + tj * t_stride + 4 * li);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < kFlashAhead; ++j) {
+            const int t = t0 + j * ROWS;
+            const float4 kv = t == pos ? ks4[li] : kc4[j];
+            const float4 vv = t == pos ? vs4[li] : vc4[j];
+            float dot = qv.x * kv.x + qv.y * kv.y + qv.z * kv.z + qv.w * kv.w;
+#pragma unroll
+            for (int o = LPR / 2; o > 0; o >>= 1) dot += __shfl_xor(dot, o, 64);
+            if (t <= pos) {
+                const float sc = dot * scale;
+                const float mn = fmaxf(m, sc);
+                const float c_old = expf(m - mn);
+                const float p = expf(sc - mn);
+                l = l * c_old + p;
+                acc.x = acc.x * c_old + p * vv.x;
+                acc.y = acc.y * c_old + p * vv.y;
+                acc.z = acc.z * c_old + p * vv.z;
+                acc.w = acc.w * c_old + p * vv.w;
+                m = mn;
+            }
+        }
+    }
+    if (li == 0) {
+        gm[lr] = m;
+        gl[lr] = l;
+    }
+    gacc[lr][li] = acc;
+    __syncthreads();
+    if (tid < HD) {
+        float mx = -INFINITY;
+        for (int g = 0; g < ROWS; ++g) mx = fmaxf(mx, gm[g]);
+        const int c4 = tid / 4;
+        const int e = tid % 4;
+        float num = 0.0f;
+        float den = 0.0f;
+        for (int g = 0; g < ROWS; ++g) {
+            if (gm[g] == -INFINITY) continue;  // a group without rows (pos + 1 < ROWS)
+            const float w = expf(gm[g] - mx);
+            const float4 a = gacc[g][c4];
+            num += w * (e == 0 ? a.x : e == 1 ? a.y : e == 2 ? a.z : a.w);
+            den += w * gl[g];
+        }
+        out[h * HD + tid] = num / den;
     }
 }
 
@@ -587,6 +781,43 @@ void Decoder::linear_group(hipStream_t s, const Linear* const* ws, float* const*
     }
 }
 
+void Decoder::launch_norm(hipStream_t s, const float* delta, const float* w) {
+    const int dim = cfg_.dim;
+    if (dim % 4 == 0 && dim <= 4 * kNormThreads * 2) {
+        if (dim <= 4 * kNormThreads) {
+            hipLaunchKernelGGL(add_rmsnorm_vec_kernel<1>, dim3(1), dim3(kNormThreads), 0, s, x_, delta, w, dim,
+                               cfg_.rms_norm_eps, h_);
+        } else {
+            hipLaunchKernelGGL(add_rmsnorm_vec_kernel<2>, dim3(1), dim3(kNormThreads), 0, s, x_, delta, w, dim,
+                               cfg_.rms_norm_eps, h_);
+        }
+    } else {
+        hipLaunchKernelGGL(add_rmsnorm_kernel, dim3(1), dim3(kNormThreads), 0, s, x_, delta, w, dim, cfg_.rms_norm_eps,
+                           h_);
+    }
+    check(hipGetLastError(), "add_rmsnorm_kernel");
+}
+
+bool Decoder::launch_attention_rope(hipStream_t s, int l) {
+    const DecoderConfig& c = cfg_;
+    const Layer& L = layers_[l];
+#define MLQ_ATTN(LPR)                                                                                            \
+    hipLaunchKernelGGL((attention_rope_kernel<LPR>), dim3(c.n_heads), dim3(kFlashThreads), 0, s, q_, k_, v_, L.bq, \
+                       L.bk, L.bv, c.n_heads, c.n_kv_heads, c.rope_theta, c.rope_neox, c.max_seq_len, l, state_,    \
+                       kcache_, vcache_, att_)
+    switch (c.head_dim) {
+        case 16: MLQ_ATTN(4); break;
+        case 32: MLQ_ATTN(8); break;
+        case 64: MLQ_ATTN(16); break;
+        case 128: MLQ_ATTN(32); break;
+        case 256: MLQ_ATTN(64); break;
+        default: return false;
+    }
+#undef MLQ_ATTN
+    check(hipGetLastError(), "attention_rope_kernel");
+    return true;
+}
+
 void Decoder::enqueue_step(hipStream_t s, bool pick, bool advance) {
     const DecoderConfig& c = cfg_;
     const int q_dim = c.n_heads * c.head_dim;
@@ -596,26 +827,24 @@ void Decoder::enqueue_step(hipStream_t s, bool pick, bool advance) {
     check(hipGetLastError(), "embed_kernel");
     for (int l = 0; l < c.n_layers; ++l) {
         const Layer& L = layers_[l];
-        hipLaunchKernelGGL(add_rmsnorm_kernel, dim3(1), dim3(kNormThreads), 0, s, x_, l == 0 ? nullptr : ff_,
-                           L.attn_norm, c.dim, c.rms_norm_eps, h_);
-        check(hipGetLastError(), "add_rmsnorm_kernel");
+        launch_norm(s, l == 0 ? nullptr : ff_, L.attn_norm);
         const Linear* qkv[3] = {&L.wq, &L.wk, &L.wv};
         float* qkv_y[3] = {q_, k_, v_};
         linear_group(s, qkv, qkv_y, 3, h_);
-        const int rope_threads = q_dim / 2 + kv_dim / 2 + kv_dim;
-        hipLaunchKernelGGL(rope_kv_kernel, dim3((rope_threads + 255) / 256), dim3(256), 0, s, q_, k_, v_, L.bq,
-                           L.bk, L.bv, c.n_heads, c.n_kv_heads, c.head_dim, c.rope_theta, c.rope_neox,
-                           c.max_seq_len, l, state_, kcache_, vcache_);
-        check(hipGetLastError(), "rope_kv_kernel");
-        hipLaunchKernelGGL(attention_kernel, dim3(c.n_heads), dim3(kAttnThreads), 0, s, q_, kcache_, vcache_,
-                           scores_, att_, c.n_heads, c.n_kv_heads, c.head_dim, c.max_seq_len, l, state_);
-        check(hipGetLastError(), "attention_kernel");
+        if (!launch_attention_rope(s, l)) {
+            const int rope_threads = q_dim / 2 + kv_dim / 2 + kv_dim;
+            hipLaunchKernelGGL(rope_kv_kernel, dim3((rope_threads + 255) / 256), dim3(256), 0, s, q_, k_, v_, L.bq,
+                               L.bk, L.bv, c.n_heads, c.n_kv_heads, c.head_dim, c.rope_theta, c.rope_neox,
+                               c.max_seq_len, l, state_, kcache_, vcache_);
+            check(hipGetLastError(), "rope_kv_kernel");
+            hipLaunchKernelGGL(attention_kernel, dim3(c.n_heads), dim3(kAttnThreads), 0, s, q_, kcache_, vcache_,
+                               scores_, att_, c.n_heads, c.n_kv_heads, c.head_dim, c.max_seq_len, l, state_);
+            check(hipGetLastError(), "attention_kernel");
+        }
         const Linear* wo[1] = {&L.wo};
         float* wo_y[1] = {proj_};
         linear_group(s, wo, wo_y, 1, att_);
-        hipLaunchKernelGGL(add_rmsnorm_kernel, dim3(1), dim3(kNormThreads), 0, s, x_, proj_, L.ffn_norm, c.dim,
-                           c.rms_norm_eps, h_);
-        check(hipGetLastError(), "add_rmsnorm_kernel");
+        launch_norm(s, proj_, L.ffn_norm);
         const Linear* gu[2] = {&L.w_gate, &L.w_up};
         float* gu_y[2] = {gate_, up_};
         linear_group(s, gu, gu_y, 2, h_);
@@ -631,9 +860,7 @@ void Decoder::enqueue_step(hipStream_t s, bool pick, bool advance) {
         check(hipGetLastError(), "advance_kernel");
         return;
     }
-    hipLaunchKernelGGL(add_rmsnorm_kernel, dim3(1), dim3(kNormThreads), 0, s, x_, ff_, final_norm_, c.dim,
-                       c.rms_norm_eps, h_);
-    check(hipGetLastError(), "add_rmsnorm_kernel");
+    launch_norm(s, ff_, final_norm_);
     if (pick && lm_head_.qtype != 0) {
         const LinearShape shape{lm_head_.qtype, lm_head_.M, lm_head_.K, (lm_head_.K + 31) / 32, 1};
         check(launch_gemv_pick(shape, lm_head_.data, h_, nullptr, static_cast<PickState*>(pick_), &state_->next, s),
@@ -695,18 +922,10 @@ void Decoder::generate(const int* prompt, int n_prompt, int n_new, int* out) {
         io_ = static_cast<int32_t*>(p);
         io_cap_ = need;
     }
-    DecodeState st{};
-    st.pos = 0;
-    st.token = prompt[0];
-    st.n_prompt = n_prompt;
-    st.n_out = n_new;
-    check(hipMemcpyAsync(state_, &st, sizeof st, hipMemcpyHostToDevice, stream_), "hipMemcpyAsync");
-    check(hipMemcpyAsync(io_, prompt, static_cast<size_t>(n_prompt) * 4, hipMemcpyHostToDevice, stream_),
-          "hipMemcpyAsync");
-    // Prompt steps before the last run without the lm_head; every later step
-    // picks and feeds the token back.  The decode step is recorded once.
-    for (int i = 0; i + 1 < n_prompt; ++i) enqueue_step(stream_, false, true);
+    // The decode step (pick, feed back, advance) is recorded once, on an idle
+    // stream, before anything of this call is queued.
     if (graph_ == nullptr) {
+        check(hipStreamSynchronize(stream_), "hipStreamSynchronize");
         hipGraph_t gr = nullptr;
         check(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
         try {
@@ -721,6 +940,17 @@ void Decoder::generate(const int* prompt, int n_prompt, int n_new, int* out) {
         (void)hipGraphDestroy(gr);
         check(e, "hipGraphInstantiate");
     }
+    DecodeState st{};
+    st.pos = 0;
+    st.token = prompt[0];
+    st.n_prompt = n_prompt;
+    st.n_out = n_new;
+    check(hipMemcpyAsync(state_, &st, sizeof st, hipMemcpyHostToDevice, stream_), "hipMemcpyAsync");
+    check(hipMemcpyAsync(io_, prompt, static_cast<size_t>(n_prompt) * 4, hipMemcpyHostToDevice, stream_),
+          "hipMemcpyAsync");
+    // Prompt steps before the last run without the lm_head; every later step
+    // picks and feeds the token back.
+    for (int i = 0; i + 1 < n_prompt; ++i) enqueue_step(stream_, false, true);
     for (int i = 0; i < n_new; ++i) check(hipGraphLaunch(graph_, stream_), "hipGraphLaunch");
     check(hipMemcpyAsync(out, io_ + n_prompt, static_cast<size_t>(n_new) * 4, hipMemcpyDeviceToHost, stream_),
           "hipMemcpyAsync");

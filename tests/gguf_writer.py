@@ -80,3 +80,33 @@ def f32_tensor(name: str, a: np.ndarray):
     a = np.ascontiguousarray(a, np.float32)
     dims = [a.shape[1], a.shape[0]] if a.ndim == 2 else list(a.shape)
     return (name, dims, GGML_F32, a.tobytes())
+
+
+def write_stream(path: str, metadata, specs, produce, alignment: int = 32) -> None:
+    """Writes a GGUF file tensor by tensor without holding it in memory:
+    specs = [(name, dims ne0-first, ggml type, nbytes)], produce(i) returns
+    tensor i's bytes (exactly nbytes)."""
+    meta = list(metadata)
+    if alignment != 32 and not any(k == "general.alignment" for k, _, _ in meta):
+        meta.append(("general.alignment", U32, alignment))
+    out = [b"GGUF", struct.pack("<IQQ", 3, len(specs), len(meta))]
+    for key, vtype, value in meta:
+        out.append(_str(key) + struct.pack("<I", vtype) + value_bytes(vtype, value))
+    offsets, pos = [], 0
+    for _, _, _, n in specs:
+        pos = (pos + alignment - 1) // alignment * alignment
+        offsets.append(pos)
+        pos += n
+    for (name, dims, gtype, _), off in zip(specs, offsets):
+        out.append(_str(name) + struct.pack("<I", len(dims)) + b"".join(struct.pack("<Q", d) for d in dims) +
+                   struct.pack("<IQ", gtype, off))
+    head = b"".join(out)
+    with open(path, "wb") as f:
+        f.write(head + b"\0" * ((alignment - len(head) % alignment) % alignment))
+        written = 0
+        for i, ((_, _, _, n), off) in enumerate(zip(specs, offsets)):
+            f.write(b"\0" * (off - written))
+            raw = produce(i)
+            assert len(raw) == n
+            f.write(raw)
+            written = off + n
