@@ -386,10 +386,19 @@ def decode_bench(n_new=128, layers=32):
     t0 = time.perf_counter()
     toks = dec.generate(prompt, n_new)
     dt = time.perf_counter() - t0
+    # Batched prefill of a 512-token prompt (two passes of 256 rows: MFMA
+    # GEMMs for the linears, causal attention per row).
+    long_prompt = (np.arange(512) * 7 % 32000).tolist()
+    dec.prefill(long_prompt[:256])  # warm-up (GEMM workspace, kernels)
+    t0 = time.perf_counter()
+    dec.prefill(long_prompt)
+    dt_pre = time.perf_counter() - t0
     dec.close()
     return {"model": "llama7b-shaped q4_0 (synthetic weights)", "layers": layers, "prompt_tokens": len(prompt),
             "new_tokens": n_new, "s": round(dt, 4), "tokens_per_s": round(n_new / dt, 1),
             "ms_per_token": round(dt * 1e3 / n_new, 3), "distinct_tokens": len(set(toks)),
+            "prefill_tokens": len(long_prompt), "prefill_s": round(dt_pre, 4),
+            "prefill_tokens_per_s": round(len(long_prompt) / dt_pre, 1),
             "file_gb": round(nbytes / 1e9, 3), "s_write_file": round(t_write, 2), "s_load": round(t_load, 2),
             "note": "wall time of one mlq_hip_decoder_generate call (prompt steps, recorded step replayed per "
                     "token, one upload, one download); attention over positions 0..131"}
@@ -596,7 +605,7 @@ def main():
     if not args.no_shapes:
         decode = decode_bench()
         log(f"  decode {decode['model']}: {decode['tokens_per_s']} tokens/s ({decode['ms_per_token']} ms/token), "
-            f"load {decode['s_load']} s")
+            f"batched prefill {decode['prefill_tokens_per_s']} tokens/s, load {decode['s_load']} s")
 
     ingest = None
     if not args.no_shapes:

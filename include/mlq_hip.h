@@ -304,9 +304,15 @@ int mlq_hip_decoder_config(mlq_decoder_t d, mlq_decoder_config* out);
  * [vocab_size] to host memory.  Positions below pos hold what earlier calls
  * wrote (zeros otherwise), as the reference's KV cache. */
 int mlq_hip_decoder_forward(mlq_decoder_t d, int token, int pos, float* logits);
+/* forward_batch (src/batch.cpp:33-52) over n tokens at positions
+ * start_pos..start_pos+n-1, batched: every layer runs on all rows at once,
+ * the linears as MFMA GEMMs (the reference runs the tokens one by one).
+ * Logits of the last token to host memory when `logits` is not NULL. */
+int mlq_hip_decoder_prefill(mlq_decoder_t d, const int* tokens, int n, int start_pos, float* logits);
 /* Greedy generation: the prompt at positions 0..n_prompt-1 (forward_batch,
- * src/batch.cpp:33-52), then n_new tokens, each the first maximum of the
- * previous step's logits (MiniSampler::sample_greedy), into out_tokens.
+ * src/batch.cpp:33-52; batched as mlq_hip_decoder_prefill), then n_new
+ * tokens, each the first maximum of the previous step's logits
+ * (MiniSampler::sample_greedy), into out_tokens.
  * Fails with "sampler: logits must be finite" as the sampler does. */
 int mlq_hip_decoder_generate(mlq_decoder_t d, const int* prompt, int n_prompt, int n_new, int* out_tokens);
 int mlq_hip_decoder_close(mlq_decoder_t d);

@@ -69,6 +69,12 @@ public:
     // token.  Throws on a device-side error (bad prompt token, position past
     // the cache, non-finite logits).
     void generate(const int* prompt, int n_prompt, int n_new, int* out);
+    // forward_batch (src/batch.cpp:33-52) over tokens at positions
+    // start..start+n-1, all rows of a layer at once (the MFMA GEMM for the
+    // linears); logits of the last token to host memory (when not null).
+    void prefill(const int* tokens, int n, int start, float* logits_host);
+
+    static constexpr int kPrefillRows = 256;  // rows per batched pass
 
 private:
     Decoder() = default;
@@ -93,6 +99,11 @@ private:
     void linear_group(hipStream_t s, const Linear* const* ws, float* const* ys, int n, const float* x);
     bool launch_attention_rope(hipStream_t s, int layer);
     void launch_norm(hipStream_t s, const float* delta, const float* w);
+    void linear_rows(hipStream_t s, const Linear& w, const float* X, float* Y, int rows);
+    void enqueue_prefill(hipStream_t s, const int32_t* tokens, int n, int start);
+    bool prefill_batched() const;
+    void ensure_prefill();
+    void ensure_io(size_t need);
 
     DecoderConfig cfg_;
     int device_ = 0;
@@ -113,6 +124,11 @@ private:
     int32_t* io_ = nullptr;      // prompt tokens then generated tokens
     size_t io_cap_ = 0;
     void* pick_ = nullptr;       // PickState
+    // Batched prefill: activations of kPrefillRows rows and the GEMM workspace.
+    float *X_ = nullptr, *H_ = nullptr, *Q_ = nullptr, *K_ = nullptr, *V_ = nullptr, *ATT_ = nullptr;
+    float *PROJ_ = nullptr, *GATE_ = nullptr, *UP_ = nullptr, *ACT_ = nullptr, *FF_ = nullptr;
+    void* ws_ = nullptr;
+    size_t ws_bytes_ = 0;
     hipGraphExec_t graph_ = nullptr;
 };
 

@@ -15,6 +15,7 @@
 
 #include "../../include/mlq_hip.h"
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <stdexcept>
@@ -379,6 +380,206 @@ __global__ __launch_bounds__(kFlashThreads) void attention_rope_kernel(
         }
         out[h * HD + tid] = num / den;
     }
+}
+
+// ---- Batched prefill (rows r = 0..n-1 at positions start + r) ----
+
+// X[r] = embedding[tokens[r]].
+__global__ __launch_bounds__(256) void embed_rows_kernel(const float* __restrict__ emb, int vocab, int dim,
+                                                         const int32_t* __restrict__ tokens, DecodeState* st,
+                                                         float* __restrict__ X) {
+    const int r = blockIdx.y;
+    const int t = tokens[r];
+    const bool ok = t >= 0 && t < vocab;
+    if (!ok && blockIdx.x == 0 && threadIdx.x == 0) st->error |= kDecodeErrToken;
+    const size_t row = static_cast<size_t>(ok ? t : 0) * dim;
+    float* x = X + static_cast<size_t>(r) * dim;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < dim; i += gridDim.x * blockDim.x) x[i] = emb[row + i];
+}
+
+// One workgroup per row: X[r] += D[r] (when given), H[r] = rmsnorm(X[r]) * w.
+__global__ __launch_bounds__(kNormThreads) void add_rmsnorm_rows_kernel(float* __restrict__ X,
+                                                                        const float* __restrict__ D,
+                                                                        const float* __restrict__ w, int dim,
+                                                                        float eps, float* __restrict__ H) {
+    __shared__ float part[kNormThreads / 64];
+    const size_t off = static_cast<size_t>(blockIdx.x) * dim;
+    float* x = X + off;
+    float ss = 0.0f;
+    for (int i = threadIdx.x; i < dim; i += kNormThreads) {
+        float v = x[i];
+        if (D != nullptr) {
+            v = v + D[off + i];
+            x[i] = v;
+        }
+        ss += v * v;
+    }
+    ss = wg_reduce<kNormThreads, false>(ss, part);
+    const float scale = 1.0f / sqrtf(ss / static_cast<float>(dim) + eps);
+    for (int i = threadIdx.x; i < dim; i += kNormThreads) H[off + i] = x[i] * scale * w[i];
+}
+
+// rope_kv_kernel for every row (position start + r).
+__global__ __launch_bounds__(256) void rope_kv_rows_kernel(float* __restrict__ Q, float* __restrict__ K,
+                                                           const float* __restrict__ V, const float* __restrict__ bq,
+                                                           const float* __restrict__ bk, const float* __restrict__ bv,
+                                                           int n_heads, int n_kv, int hd, float theta, int neox,
+                                                           int max_seq, int layer, int start, float* __restrict__ kc,
+                                                           float* __restrict__ vc) {
+    const int row = blockIdx.y;
+    const int pos = start + row;
+    const int half = hd / 2;
+    const int nq = n_heads * half;
+    const int nk = n_kv * half;
+    const int nv = n_kv * hd;
+    float* q = Q + static_cast<size_t>(row) * n_heads * hd;
+    float* k = K + static_cast<size_t>(row) * nv;
+    const float* v = V + static_cast<size_t>(row) * nv;
+    const size_t cache_row = (static_cast<size_t>(layer) * max_seq + pos) * nv;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < nq + nk) {
+        const bool is_q = i < nq;
+        const int j = is_q ? i : i - nq;
+        const int h = j / half;
+        const int r = j % half;
+        const int i0 = h * hd + (neox ? r : 2 * r);
+        const int i1 = neox ? i0 + half : i0 + 1;
+        const float freq = 1.0f / powf(theta, static_cast<float>(2 * r) / static_cast<float>(hd));
+        const float ang = static_cast<float>(pos) * freq;
+        const float c = cosf(ang);
+        const float s = sinf(ang);
+        float* t = is_q ? q : k;
+        const float* b = is_q ? bq : bk;
+        float a0 = t[i0];
+        float a1 = t[i1];
+        if (b != nullptr) {
+            a0 = a0 + b[i0];
+            a1 = a1 + b[i1];
+        }
+        const float r0 = a0 * c - a1 * s;
+        const float r1 = a0 * s + a1 * c;
+        t[i0] = r0;
+        t[i1] = r1;
+        if (!is_q) {
+            kc[cache_row + i0] = r0;
+            kc[cache_row + i1] = r1;
+        }
+    } else if (i < nq + nk + nv) {
+        const int e = i - nq - nk;
+        vc[cache_row + e] = bv != nullptr ? v[e] + bv[e] : v[e];
+    }
+}
+
+// Causal attention of prefill rows: workgroup (head h, row r) attends from
+// position start + r over cache rows 0..start + r (all written before), with
+// the same coalesced reads and online softmax as attention_rope_kernel.
+template <int LPR>
+__global__ __launch_bounds__(kFlashThreads) void attention_rows_kernel(const float* __restrict__ Q,
+                                                                       const float* __restrict__ kc,
+                                                                       const float* __restrict__ vc, int n_heads,
+                                                                       int n_kv, int max_seq, int layer, int start,
+                                                                       float* __restrict__ out) {
+    constexpr int HD = 4 * LPR;
+    constexpr int ROWS = kFlashThreads / LPR;
+    __shared__ float gm[ROWS], gl[ROWS];
+    __shared__ float4 gacc[ROWS][LPR];
+    const int tid = threadIdx.x;
+    const int h = blockIdx.x;
+    const int row = blockIdx.y;
+    const int pos = start + row;
+    const int kvh = h / (n_heads / n_kv);
+    const size_t layer_base = static_cast<size_t>(layer) * max_seq * n_kv * HD;
+    const size_t t_stride = static_cast<size_t>(n_kv) * HD;
+    const float* kbase = kc + layer_base + kvh * HD;
+    const float* vbase = vc + layer_base + kvh * HD;
+    const int lr = tid / LPR;
+    const int li = tid % LPR;
+    const float4 qv = *reinterpret_cast<const float4*>(Q + static_cast<size_t>(row) * n_heads * HD + h * HD + 4 * li);
+    const float scale = 1.0f / sqrtf(static_cast<float>(HD));
+    float m = -INFINITY;
+    float l = 0.0f;
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    float4 kr[kFlashAhead], vr[kFlashAhead];
+#pragma unroll
+    for (int j = 0; j < kFlashAhead; ++j) {
+        const int tj = min(lr + j * ROWS, pos);
+        kr[j] = *reinterpret_cast<const float4*>(kbase + tj * t_stride + 4 * li);
+        vr[j] = *reinterpret_cast<const float4*>(vbase + tj * t_stride + 4 * li);
+    }
+    for (int t0 = lr; t0 <= pos; t0 += kFlashAhead * ROWS) {
+        float4 kc4[kFlashAhead], vc4[kFlashAhead];
+#pragma unroll
+        for (int j = 0; j < kFlashAhead; ++j) {
+            kc4[j] = kr[j];
+            vc4[j] = vr[j];
+        }
+        if (t0 + kFlashAhead * ROWS <= pos) {
+#pragma unroll
+            for (int j = 0; j < kFlashAhead; ++j) {
+                const int tj = min(t0 + (kFlashAhead + j) * ROWS, pos);
+                kr[j] = *reinterpret_cast<const float4*>(kbase + tj * t_stride + 4 * li);
+                vr[j] = *reinterpret_cast<const float4*>(vbase + tj * t_stride + 4 * li);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < kFlashAhead; ++j) {
+            const int t = t0 + j * ROWS;
+            const float4 kv = kc4[j];
+            const float4 vv = vc4[j];
+            float dot = qv.x * kv.x + qv.y * kv.y + qv.z * kv.z + qv.w * kv.w;
+#pragma unroll
+            for (int o = LPR / 2; o > 0; o >>= 1) dot += __shfl_xor(dot, o, 64);
+            if (t <= pos) {
+                const float sc = dot * scale;
+                const float mn = fmaxf(m, sc);
+                const float c_old = expf(m - mn);
+                const float p = expf(sc - mn);
+                l = l * c_old + p;
+                acc.x = acc.x * c_old + p * vv.x;
+                acc.y = acc.y * c_old + p * vv.y;
+                acc.z = acc.z * c_old + p * vv.z;
+                acc.w = acc.w * c_old + p * vv.w;
+                m = mn;
+            }
+        }
+    }
+    if (li == 0) {
+        gm[lr] = m;
+        gl[lr] = l;
+    }
+    gacc[lr][li] = acc;
+    __syncthreads();
+    if (tid < HD) {
+        float mx = -INFINITY;
+        for (int g = 0; g < ROWS; ++g) mx = fmaxf(mx, gm[g]);
+        const int c4 = tid / 4;
+        const int e = tid % 4;
+        float num = 0.0f;
+        float den = 0.0f;
+        for (int g = 0; g < ROWS; ++g) {
+            if (gm[g] == -INFINITY) continue;
+            const float wgt = expf(gm[g] - mx);
+            const float4 a = gacc[g][c4];
+            num += wgt * (e == 0 ? a.x : e == 1 ? a.y : e == 2 ? a.z : a.w);
+            den += wgt * gl[g];
+        }
+        out[static_cast<size_t>(row) * n_heads * HD + h * HD + tid] = num / den;
+    }
+}
+
+// Y[r][M] = W[M][K] . X[r] for F32 weights: one wave per (row of W, row of X).
+__global__ __launch_bounds__(256) void gemm_f32_kernel(const float* __restrict__ W, const float* __restrict__ X,
+                                                       float* __restrict__ Y, int M, int K) {
+    const int row = blockIdx.x * 4 + static_cast<int>(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= M) return;
+    const float* w = W + static_cast<size_t>(row) * K;
+    const float* x = X + static_cast<size_t>(blockIdx.y) * K;
+    float acc = 0.0f;
+    for (int k = lane; k < K; k += 64) acc += w[k] * x[k];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+    if (lane == 0) Y[static_cast<size_t>(blockIdx.y) * M + row] = acc;
 }
 
 // out = silu(gate) * up (swiglu, src/ops.cpp:95-107).
@@ -880,6 +1081,175 @@ void Decoder::enqueue_step(hipStream_t s, bool pick, bool advance) {
     }
 }
 
+void Decoder::ensure_prefill() {
+    if (X_ != nullptr) return;
+    const DecoderConfig& c = cfg_;
+    const size_t R = kPrefillRows;
+    auto buf = [&](size_t n) {
+        void* p = nullptr;
+        check(hipMalloc(&p, n * 4), "hipMalloc");
+        allocs_.push_back(p);
+        return static_cast<float*>(p);
+    };
+    const int q_dim = c.n_heads * c.head_dim;
+    const int kv_dim = c.n_kv_heads * c.head_dim;
+    X_ = buf(R * c.dim);
+    H_ = buf(R * c.dim);
+    Q_ = buf(R * q_dim);
+    K_ = buf(R * kv_dim);
+    V_ = buf(R * kv_dim);
+    ATT_ = buf(R * q_dim);
+    PROJ_ = buf(R * c.dim);
+    GATE_ = buf(R * c.hidden_dim);
+    UP_ = buf(R * c.hidden_dim);
+    ACT_ = buf(R * c.hidden_dim);
+    FF_ = buf(R * c.dim);
+}
+
+// One linear over `rows` rows of X (row-major [rows][K] in, [rows][M] out):
+// the MFMA GEMM where it applies, else the GEMV kernels over a batch of rows.
+void Decoder::linear_rows(hipStream_t s, const Linear& w, const float* X, float* Y, int rows) {
+    if (w.qtype == 0) {
+        hipLaunchKernelGGL(gemm_f32_kernel, dim3((w.M + 3) / 4, rows), dim3(256), 0, s,
+                           static_cast<const float*>(w.data), X, Y, w.M, w.K);
+        check(hipGetLastError(), "gemm_f32_kernel");
+        return;
+    }
+    const LinearShape shape{w.qtype, w.M, w.K, (w.K + 31) / 32, rows};
+    if (rows > 1 && gemm_supported(shape)) {
+        const size_t need = gemm_workspace_bytes(shape);
+        if (need > ws_bytes_) {
+            check(hipStreamSynchronize(s), "hipStreamSynchronize");
+            void* p = nullptr;
+            check(hipMalloc(&p, need), "hipMalloc");
+            // Split-K counters start at zero: cleared on this stream, ahead of
+            // the GEMM (a plain hipMemset runs on the null stream, which this
+            // non-blocking stream does not wait for).
+            check(hipMemsetAsync(p, 0, need, s), "hipMemsetAsync");
+            allocs_.push_back(p);
+            ws_ = p;
+            ws_bytes_ = need;
+        }
+        check(launch_gemm(shape, w.data, X, Y, ws_, ws_bytes_, s), "launch_gemm");
+        return;
+    }
+    GemvGroup g{};
+    g.W[0] = w.data;
+    g.y[0] = Y;
+    g.ncalls = 1;
+    check(launch_gemv_group(shape, g, X, s), "launch_gemv_group");
+}
+
+bool Decoder::prefill_batched() const {
+    const int hd = cfg_.head_dim;
+    return hd == 16 || hd == 32 || hd == 64 || hd == 128 || hd == 256;
+}
+
+// forward_batch over tokens[0..n) (device pointer) at positions start..:
+// every layer for all rows at once; X_ row n-1 ends as the last token's
+// residual stream (its final norm and lm_head are the caller's).
+void Decoder::enqueue_prefill(hipStream_t s, const int32_t* tokens, int n, int start) {
+    const DecoderConfig& c = cfg_;
+    const int q_dim = c.n_heads * c.head_dim;
+    const int kv_dim = c.n_kv_heads * c.head_dim;
+    hipLaunchKernelGGL(embed_rows_kernel, dim3((c.dim + 255) / 256, n), dim3(256), 0, s, embedding_, c.vocab_size,
+                       c.dim, tokens, state_, X_);
+    check(hipGetLastError(), "embed_rows_kernel");
+    for (int l = 0; l < c.n_layers; ++l) {
+        const Layer& L = layers_[l];
+        hipLaunchKernelGGL(add_rmsnorm_rows_kernel, dim3(n), dim3(kNormThreads), 0, s, X_, l == 0 ? nullptr : FF_,
+                           L.attn_norm, c.dim, c.rms_norm_eps, H_);
+        check(hipGetLastError(), "add_rmsnorm_rows_kernel");
+        linear_rows(s, L.wq, H_, Q_, n);
+        linear_rows(s, L.wk, H_, K_, n);
+        linear_rows(s, L.wv, H_, V_, n);
+        const int rope_threads = q_dim / 2 + kv_dim / 2 + kv_dim;
+        hipLaunchKernelGGL(rope_kv_rows_kernel, dim3((rope_threads + 255) / 256, n), dim3(256), 0, s, Q_, K_, V_,
+                           L.bq, L.bk, L.bv, c.n_heads, c.n_kv_heads, c.head_dim, c.rope_theta, c.rope_neox,
+                           c.max_seq_len, l, start, kcache_, vcache_);
+        check(hipGetLastError(), "rope_kv_rows_kernel");
+#define MLQ_ATTN_ROWS(LPR)                                                                                   \
+    hipLaunchKernelGGL((attention_rows_kernel<LPR>), dim3(c.n_heads, n), dim3(kFlashThreads), 0, s, Q_, kcache_, \
+                       vcache_, c.n_heads, c.n_kv_heads, c.max_seq_len, l, start, ATT_)
+        switch (c.head_dim) {
+            case 16: MLQ_ATTN_ROWS(4); break;
+            case 32: MLQ_ATTN_ROWS(8); break;
+            case 64: MLQ_ATTN_ROWS(16); break;
+            case 128: MLQ_ATTN_ROWS(32); break;
+            default: MLQ_ATTN_ROWS(64); break;
+        }
+#undef MLQ_ATTN_ROWS
+        check(hipGetLastError(), "attention_rows_kernel");
+        linear_rows(s, L.wo, ATT_, PROJ_, n);
+        hipLaunchKernelGGL(add_rmsnorm_rows_kernel, dim3(n), dim3(kNormThreads), 0, s, X_, PROJ_, L.ffn_norm, c.dim,
+                           c.rms_norm_eps, H_);
+        check(hipGetLastError(), "add_rmsnorm_rows_kernel");
+        linear_rows(s, L.w_gate, H_, GATE_, n);
+        linear_rows(s, L.w_up, H_, UP_, n);
+        const int nh = n * c.hidden_dim;
+        hipLaunchKernelGGL(swiglu_kernel, dim3((nh + 255) / 256), dim3(256), 0, s, GATE_, UP_, ACT_, nh);
+        check(hipGetLastError(), "swiglu_kernel");
+        linear_rows(s, L.w_down, ACT_, FF_, n);
+    }
+    // Residual of the last layer into the rows' streams.
+    hipLaunchKernelGGL(add_rmsnorm_rows_kernel, dim3(n), dim3(kNormThreads), 0, s, X_, FF_, final_norm_, c.dim,
+                       c.rms_norm_eps, H_);
+    check(hipGetLastError(), "add_rmsnorm_rows_kernel");
+}
+
+void Decoder::prefill(const int* tokens, int n, int start, float* logits_host) {
+    const DecoderConfig& c = cfg_;
+    if (n <= 0) throw std::runtime_error("forward_batch: empty batch");
+    for (int i = 0; i < n; ++i) {
+        if (tokens[i] < 0 || tokens[i] >= c.vocab_size) throw std::out_of_range("forward_token token id out of range");
+    }
+    if (start < 0 || static_cast<long long>(start) + n > c.max_seq_len) {
+        throw std::out_of_range("forward_token position out of range");
+    }
+    check(hipSetDevice(device_), "hipSetDevice");
+    if (!prefill_batched() || n == 1) {
+        for (int i = 0; i < n; ++i) forward(tokens[i], start + i, logits_host);
+        return;
+    }
+    ensure_io(static_cast<size_t>(n));
+    ensure_prefill();
+    DecodeState st{};
+    check(hipMemcpyAsync(state_, &st, sizeof st, hipMemcpyHostToDevice, stream_), "hipMemcpyAsync");
+    check(hipMemcpyAsync(io_, tokens, static_cast<size_t>(n) * 4, hipMemcpyHostToDevice, stream_), "hipMemcpyAsync");
+    for (int c0 = 0; c0 < n; c0 += kPrefillRows) {
+        const int rows = std::min(kPrefillRows, n - c0);
+        enqueue_prefill(stream_, io_ + c0, rows, start + c0);
+        if (c0 + rows == n) {
+            // Logits of the last token: its normed row through the lm_head.
+            const Linear* lm[1] = {&lm_head_};
+            float* lm_y[1] = {logits_};
+            linear_group(stream_, lm, lm_y, 1, H_ + static_cast<size_t>(rows - 1) * c.dim);
+        }
+    }
+    if (logits_host != nullptr) {
+        check(hipMemcpyAsync(logits_host, logits_, static_cast<size_t>(c.vocab_size) * 4, hipMemcpyDeviceToHost,
+                             stream_),
+              "hipMemcpyAsync");
+    }
+    check(hipMemcpyAsync(&st, state_, sizeof st, hipMemcpyDeviceToHost, stream_), "hipMemcpyAsync");
+    check(hipStreamSynchronize(stream_), "hipStreamSynchronize");
+    if (st.error != 0) throw std::runtime_error("HIP decoder: device step reported error " + std::to_string(st.error));
+}
+
+void Decoder::ensure_io(size_t need) {
+    if (need <= io_cap_) return;
+    check(hipStreamSynchronize(stream_), "hipStreamSynchronize");
+    if (graph_) {
+        (void)hipGraphExecDestroy(graph_);
+        graph_ = nullptr;
+    }
+    void* p = nullptr;
+    check(hipMalloc(&p, need * 4), "hipMalloc");
+    allocs_.push_back(p);
+    io_ = static_cast<int32_t*>(p);
+    io_cap_ = need;
+}
+
 void Decoder::forward(int token, int pos, float* logits_host) {
     const DecoderConfig& c = cfg_;
     if (token < 0 || token >= c.vocab_size) throw std::out_of_range("forward_token token id out of range");
@@ -909,19 +1279,9 @@ void Decoder::generate(const int* prompt, int n_prompt, int n_new, int* out) {
     }
     check(hipSetDevice(device_), "hipSetDevice");
     // One upload: the state, then the prompt; the generated tokens follow it.
-    const size_t need = static_cast<size_t>(n_prompt) + n_new;
-    if (need > io_cap_) {
-        check(hipStreamSynchronize(stream_), "hipStreamSynchronize");
-        if (graph_) {
-            (void)hipGraphExecDestroy(graph_);
-            graph_ = nullptr;
-        }
-        void* p = nullptr;
-        check(hipMalloc(&p, need * 4), "hipMalloc");
-        allocs_.push_back(p);
-        io_ = static_cast<int32_t*>(p);
-        io_cap_ = need;
-    }
+    ensure_io(static_cast<size_t>(n_prompt) + n_new);
+    const bool batched = prefill_batched() && n_prompt > 2;
+    if (batched) ensure_prefill();
     // The decode step (pick, feed back, advance) is recorded once, on an idle
     // stream, before anything of this call is queued.
     if (graph_ == nullptr) {
@@ -940,17 +1300,25 @@ void Decoder::generate(const int* prompt, int n_prompt, int n_new, int* out) {
         (void)hipGraphDestroy(gr);
         check(e, "hipGraphInstantiate");
     }
+    // With a batched prefill of prompt tokens 0..n_prompt-2 the first
+    // recorded step starts at the last prompt token.
     DecodeState st{};
-    st.pos = 0;
-    st.token = prompt[0];
+    st.pos = batched ? n_prompt - 1 : 0;
+    st.token = batched ? prompt[n_prompt - 1] : prompt[0];
     st.n_prompt = n_prompt;
     st.n_out = n_new;
     check(hipMemcpyAsync(state_, &st, sizeof st, hipMemcpyHostToDevice, stream_), "hipMemcpyAsync");
     check(hipMemcpyAsync(io_, prompt, static_cast<size_t>(n_prompt) * 4, hipMemcpyHostToDevice, stream_),
           "hipMemcpyAsync");
-    // Prompt steps before the last run without the lm_head; every later step
-    // picks and feeds the token back.
-    for (int i = 0; i + 1 < n_prompt; ++i) enqueue_step(stream_, false, true);
+    // Prompt tokens before the last: one batched pass (the MFMA GEMMs), or
+    // steps without the lm_head; every later step picks and feeds back.
+    if (batched) {
+        for (int c0 = 0; c0 < n_prompt - 1; c0 += kPrefillRows) {
+            enqueue_prefill(stream_, io_ + c0, std::min(kPrefillRows, n_prompt - 1 - c0), c0);
+        }
+    } else {
+        for (int i = 0; i + 1 < n_prompt; ++i) enqueue_step(stream_, false, true);
+    }
     for (int i = 0; i < n_new; ++i) check(hipGraphLaunch(graph_, stream_), "hipGraphLaunch");
     check(hipMemcpyAsync(out, io_ + n_prompt, static_cast<size_t>(n_new) * 4, hipMemcpyDeviceToHost, stream_),
           "hipMemcpyAsync");

@@ -1386,6 +1386,18 @@ int mlq_hip_decoder_forward(mlq_decoder_t d, int token, int pos, float* logits) 
     return MLQ_OK;
 }
 
+int mlq_hip_decoder_prefill(mlq_decoder_t d, const int* tokens, int n, int start_pos, float* logits) {
+    if (d == nullptr || tokens == nullptr) return fail(MLQ_ERR_INVALID, "mlq_hip_decoder_prefill: null argument");
+    try {
+        d->dec->prefill(tokens, n, start_pos, logits);
+    } catch (const std::out_of_range& e) {
+        return fail(MLQ_ERR_SHAPE, e.what());
+    } catch (const std::exception& e) {
+        return fail(MLQ_ERR_INVALID, e.what());
+    }
+    return MLQ_OK;
+}
+
 int mlq_hip_decoder_generate(mlq_decoder_t d, const int* prompt, int n_prompt, int n_new, int* out_tokens) {
     if (d == nullptr || prompt == nullptr || (n_new > 0 && out_tokens == nullptr)) {
         return fail(MLQ_ERR_INVALID, "mlq_hip_decoder_generate: null argument");

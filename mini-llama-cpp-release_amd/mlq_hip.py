@@ -103,6 +103,7 @@ _SIGS = {
     "mlq_hip_decoder_config": (ctypes.c_int, [_vp, ctypes.POINTER(DecoderConfig)]),
     "mlq_hip_decoder_forward": (ctypes.c_int, [_vp, ctypes.c_int, ctypes.c_int, _vp]),
     "mlq_hip_decoder_generate": (ctypes.c_int, [_vp, _vp, ctypes.c_int, ctypes.c_int, _vp]),
+    "mlq_hip_decoder_prefill": (ctypes.c_int, [_vp, _vp, ctypes.c_int, ctypes.c_int, _vp]),
     "mlq_hip_decoder_close": (ctypes.c_int, [_vp]),
     "mlq_hip_graph_begin": (ctypes.c_int, [ctypes.c_int, _vp]),
     "mlq_hip_graph_end": (ctypes.c_int, [ctypes.c_int, _vp, ctypes.POINTER(_vp)]),
@@ -507,6 +508,13 @@ class Decoder:
     def forward(self, token: int, pos: int) -> np.ndarray:
         logits = np.empty(self.config["vocab_size"], np.float32)
         _check(_LIB.mlq_hip_decoder_forward(self.h, token, pos, logits.ctypes.data))
+        return logits
+
+    def prefill(self, tokens, start: int = 0) -> np.ndarray:
+        """Batched forward_batch; logits of the last token."""
+        t = np.ascontiguousarray(tokens, np.int32)
+        logits = np.empty(self.config["vocab_size"], np.float32)
+        _check(_LIB.mlq_hip_decoder_prefill(self.h, t.ctypes.data, t.size, start, logits.ctypes.data))
         return logits
 
     def generate(self, prompt, n_new: int) -> list:

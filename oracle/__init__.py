@@ -336,6 +336,9 @@ class RefDecoder:
         self._cfg = ref._fn("decoder_config", None, [vp, ctypes.POINTER(ctypes.c_int)])
         self._fwd = ref._fn("decoder_forward", ctypes.c_int,
                             [vp, ctypes.c_int, ctypes.c_int, _f32p, ctypes.c_char_p, ctypes.c_size_t])
+        self._batch = ref._fn("decoder_batch", ctypes.c_int,
+                              [vp, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, _f32p, ctypes.c_char_p,
+                               ctypes.c_size_t])
         self._gen = ref._fn("decoder_generate", ctypes.c_int,
                             [vp, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_char_p,
                              ctypes.c_size_t])
@@ -355,6 +358,14 @@ class RefDecoder:
         out = np.empty(self.config["vocab_size"], np.float32)
         err = ctypes.create_string_buffer(512)
         if self._fwd(self.h, token, pos, _ptr(out, _f32p), err, 512) != 0:
+            raise RuntimeError(err.value.decode())
+        return out
+
+    def batch(self, tokens, start: int = 0) -> np.ndarray:
+        t = np.ascontiguousarray(tokens, np.int32)
+        out = np.empty(self.config["vocab_size"], np.float32)
+        err = ctypes.create_string_buffer(512)
+        if self._batch(self.h, _ptr(t), t.size, start, _ptr(out, _f32p), err, 512) != 0:
             raise RuntimeError(err.value.decode())
         return out
 

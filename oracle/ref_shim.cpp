@@ -333,6 +333,20 @@ int mlq_ref_decoder_forward(void* h, int token, int pos, float* out, char* err, 
     }
 }
 
+// forward_batch over tokens at positions start..; logits of the last token.
+int mlq_ref_decoder_batch(void* h, const int* tokens, int n, int start, float* out, char* err, size_t err_len) {
+    RefDecoder* d = static_cast<RefDecoder*>(h);
+    try {
+        std::vector<int> toks(tokens, tokens + n);
+        Tensor logits = forward_batch(d->model, *d->ctx, MiniBatch::from_tokens(toks, start));
+        std::memcpy(out, logits.data.data(), logits.data.size() * sizeof(float));
+        return 0;
+    } catch (const std::exception& e) {
+        std::snprintf(err, err_len, "%s", e.what());
+        return -1;
+    }
+}
+
 // Greedy generation as forward_batch over the prompt, then sample_greedy and
 // forward_token per new token.
 int mlq_ref_decoder_generate(void* h, const int* prompt, int n_prompt, int n_new, int* out, char* err,

@@ -158,3 +158,34 @@ def test_loader_errors_match_reference(hip, orc, ref, tmp_path, case):
     with pytest.raises(hip.MlqError) as got:
         hip.Decoder(path)
     assert got.value.msg == str(want.value)
+
+
+@pytest.mark.parametrize("name", list(VARIANTS))
+def test_batched_prefill_matches_reference(hip, orc, ref, tmp_path, name):
+    """mlq_hip_decoder_prefill (every layer over all rows, MFMA GEMMs for the
+    linears) against the reference's token-by-token forward_batch: the last
+    token's logits, then a continuation step that reads the cache the batch
+    wrote, and a second batch at a later start."""
+    path = model(orc, tmp_path, name)
+    dec = hip.Decoder(path)
+    rd = ref.decoder(path)
+    rng = np.random.default_rng(11)
+    v = dec.config["vocab_size"]
+    toks = rng.integers(0, v, 37).tolist()
+    worst = close(dec.prefill(toks[:20]), rd.batch(toks[:20]), f"{name} batch 0..19")
+    worst = max(worst, close(dec.forward(toks[20], 20), rd.forward(toks[20], 20), f"{name} step 20"))
+    worst = max(worst, close(dec.prefill(toks[21:37], 21), rd.batch(toks[21:37], 21), f"{name} batch 21..36"))
+    say(f"  worst relative logit difference {worst:.2e}")
+    dec.close()
+
+
+def test_batched_prefill_longer_than_one_pass(hip, orc, ref, tmp_path):
+    """A prompt of more rows than one batched pass holds (chunks of 256)."""
+    path = mf.write_model(orc, str(tmp_path / "long.gguf"), ctx=640, vocab=300, layers=2, seed=9)
+    dec = hip.Decoder(path)
+    rd = ref.decoder(path)
+    toks = np.random.default_rng(3).integers(0, 300, 600).tolist()
+    close(dec.prefill(toks), rd.batch(toks), "600-token batch")
+    got = dec.generate(toks[:300], 8)
+    assert got == ref.decoder(path).generate(toks[:300], 8)
+    dec.close()
