@@ -404,6 +404,28 @@ def decode_bench(n_new=128, layers=32):
                     "token, one upload, one download); attention over positions 0..131"}
 
 
+def decode_steps_bench(steps):
+    """forward() steps (forward_token: logits to the host each step) on the
+    model of decode_bench, positions 0..steps-1."""
+    import tempfile
+
+    fd, path = tempfile.mkstemp(suffix=".gguf")
+    os.close(fd)
+    try:
+        write_llama7b_q4_0(path)
+        dec = hip.Decoder(path, max_seq_len=max(256, steps))
+    finally:
+        os.unlink(path)
+    dec.forward(1, 0)
+    t0 = time.perf_counter()
+    for pos in range(steps):
+        dec.forward(pos % 100 + 1, pos)
+    dt = time.perf_counter() - t0
+    dec.close()
+    return {"forward_steps": steps, "s": round(dt, 4), "ms_per_step": round(dt * 1e3 / steps, 3),
+            "note": "each step synchronizes and downloads the logits (forward_token)"}
+
+
 PICK_CONFIGS = ([("c2_qwen_lm_head", qt, 151936, 896) for qt in (hip.Q8_0, hip.Q4_0, hip.Q4_1)] +
                 [("c3_llama_lm_head", qt, 32000, 4096) for qt in (hip.Q8_0, hip.Q4_0, hip.Q4_1)])
 
@@ -512,7 +534,20 @@ def main():
     ap.add_argument("--calibration-copy-mb", type=int, default=0,
                     help="before timing, run one device-to-device copy of this many MiB: a kernel of "
                          "known traffic that scales the rocprofv3 FETCH_SIZE / WRITE_SIZE counters")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="run only the device-resident decode leg and print its JSON")
+    ap.add_argument("--decode-steps", type=int, default=0,
+                    help="with --decode-only: instead run this many single forward() steps (one launch "
+                         "sequence per token, no recorded graph) on the same model, for kernel profiles")
     args = ap.parse_args()
+    if args.decode_only:
+        hip.load()
+        hip.init(0)
+        if args.decode_steps > 0:
+            print(json.dumps(decode_steps_bench(args.decode_steps)), flush=True)
+        else:
+            print(json.dumps(decode_bench()), flush=True)
+        return
 
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only; --gpus {args.gpus} is not supported "
