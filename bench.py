@@ -364,7 +364,7 @@ def write_llama7b_q4_0(path, layers=32):
     return sum(x[3] for x in specs)
 
 
-def decode_bench(n_new=128, layers=32):
+def decode_bench(n_new=128, layers=32, cpu=False):
     """Greedy decode on the LLaMA-7B-shaped Q4_0 model of write_llama7b_q4_0
     through mlq_hip_decoder_generate: every op on the device, the picked token
     fed back on the device, one recorded step replayed per token."""
@@ -372,6 +372,7 @@ def decode_bench(n_new=128, layers=32):
 
     fd, path = tempfile.mkstemp(suffix=".gguf")
     os.close(fd)
+    cpu_leg = None
     try:
         t0 = time.perf_counter()
         nbytes = write_llama7b_q4_0(path, layers)
@@ -379,6 +380,8 @@ def decode_bench(n_new=128, layers=32):
         t0 = time.perf_counter()
         dec = hip.Decoder(path, max_seq_len=1024)
         t_load = time.perf_counter() - t0
+        if cpu:
+            cpu_leg = decode_cpu_baseline(path, dec)
     finally:
         os.unlink(path)
     prompt = [1, 2, 3, 4]
@@ -400,8 +403,39 @@ def decode_bench(n_new=128, layers=32):
             "prefill_tokens": len(long_prompt), "prefill_s": round(dt_pre, 4),
             "prefill_tokens_per_s": round(len(long_prompt) / dt_pre, 1),
             "file_gb": round(nbytes / 1e9, 3), "s_write_file": round(t_write, 2), "s_load": round(t_load, 2),
+            "cpu_baseline": cpu_leg,
             "note": "wall time of one mlq_hip_decoder_generate call (prompt steps, recorded step replayed per "
                     "token, one upload, one download); attention over positions 0..131"}
+
+
+def decode_cpu_baseline(path, dec, tokens=(11, 22, 33)):
+    """The reference's own load_gguf_model + forward_token (oracle/_ref, the
+    threaded CPU path) on the same model file, a bounded sample of tokens;
+    its logits also check the device decoder's at full size."""
+    import oracle
+
+    ref = oracle.reference()
+    if ref is None:
+        return None
+    threads = os.cpu_count() or 1
+    t0 = time.perf_counter()
+    rd = ref.decoder(path, threads)
+    t_load = time.perf_counter() - t0
+    times, worst = [], 0.0
+    for pos, t in enumerate(tokens):
+        t0 = time.perf_counter()
+        want = rd.forward(t, pos)
+        times.append(time.perf_counter() - t0)
+        got = dec.forward(t, pos)
+        worst = max(worst, float(np.abs(got.astype(np.float64) - want).max()) / max(1.0, float(np.abs(want).max())))
+    del rd
+    per_token = sum(times[1:]) / max(1, len(times) - 1)
+    if worst > 1e-3:
+        raise SystemExit(f"decoder logits differ from the reference's by {worst:.2e} of max |logit|")
+    return {"kind": "reference", "cores": threads, "tokens_per_s": round(1.0 / per_token, 3),
+            "ms_per_token": round(per_token * 1e3, 1), "s_load": round(t_load, 2),
+            "sample": f"forward_token at positions 0..{len(tokens) - 1} (first excluded from the rate)",
+            "gpu_vs_reference_max_rel_logit_diff": worst}
 
 
 def decode_steps_bench(steps):
@@ -638,7 +672,7 @@ def main():
 
     decode = None
     if not args.no_shapes:
-        decode = decode_bench()
+        decode = decode_bench(cpu=not args.no_cpu)
         log(f"  decode {decode['model']}: {decode['tokens_per_s']} tokens/s ({decode['ms_per_token']} ms/token), "
             f"batched prefill {decode['prefill_tokens_per_s']} tokens/s, load {decode['s_load']} s")
 

@@ -257,8 +257,8 @@ class Reference(_Lib):
         finally:
             free(h)
 
-    def decoder(self, path: str) -> "RefDecoder":
-        return RefDecoder(self, path)
+    def decoder(self, path: str, threads: int = 0) -> "RefDecoder":
+        return RefDecoder(self, path, threads)
 
     def fp16_probe_q4_1(self, v: float) -> int:
         return int(self._p41(float(v)))
@@ -328,9 +328,9 @@ class RefWeight:
 class RefDecoder:
     """load_gguf_model + forward_token of the reference (CPU, f32)."""
 
-    def __init__(self, ref: Reference, path: str):
+    def __init__(self, ref: Reference, path: str, threads: int = 0):
         vp, cp = ctypes.c_void_p, ctypes.c_char_p
-        self._open = ref._fn("decoder_open", vp, [cp, ctypes.POINTER(ctypes.c_int)])
+        self._open = ref._fn("decoder_open", vp, [cp, ctypes.c_int, ctypes.POINTER(ctypes.c_int)])
         self._err = ref._fn("decoder_error", cp, [vp])
         self._free = ref._fn("decoder_free", None, [vp])
         self._cfg = ref._fn("decoder_config", None, [vp, ctypes.POINTER(ctypes.c_int)])
@@ -343,7 +343,7 @@ class RefDecoder:
                             [vp, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_char_p,
                              ctypes.c_size_t])
         ok = ctypes.c_int(0)
-        self.h = self._open(os.fsencode(path), ctypes.byref(ok))
+        self.h = self._open(os.fsencode(path), threads, ctypes.byref(ok))
         if not ok.value:
             msg = self._err(self.h).decode()
             self._free(self.h)

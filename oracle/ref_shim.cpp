@@ -299,7 +299,8 @@ struct RefDecoder {
     std::unique_ptr<MiniLlamaContext> ctx;
 };
 
-void* mlq_ref_decoder_open(const char* path, int* ok) {
+void* mlq_ref_decoder_open(const char* path, int threads, int* ok) {
+    set_thread_count(threads);
     RefDecoder* d = new RefDecoder;
     d->model = load_gguf_model(path);
     *ok = d->model.loaded ? 1 : 0;
