@@ -100,6 +100,8 @@ private:
     bool launch_attention_rope(hipStream_t s, int layer);
     void launch_norm(hipStream_t s, const float* delta, const float* w);
     void linear_rows(hipStream_t s, const Linear& w, const float* X, float* Y, int rows);
+    void linear_fused(hipStream_t s, const Linear* const* ws, float* const* ys, int n, const float* x,
+                      const float* norm_w, bool acc);
     void enqueue_prefill(hipStream_t s, const int32_t* tokens, int n, int start);
     bool prefill_batched() const;
     void ensure_prefill();

@@ -1019,20 +1019,60 @@ bool Decoder::launch_attention_rope(hipStream_t s, int l) {
     return true;
 }
 
+// Quantized weights of one (grouped) launch: consecutive ones of one format
+// and width share it.  `norm`: stage rmsnorm(x) * norm_w instead of x;
+// `acc`: add the rows into y.  F32 weights are not allowed here.
+void Decoder::linear_fused(hipStream_t s, const Linear* const* ws, float* const* ys, int n, const float* x,
+                           const float* norm_w, bool acc) {
+    int i = 0;
+    while (i < n) {
+        const Linear& w = *ws[i];
+        GemvGroup g{};
+        int rows = 0;
+        int j = i;
+        while (j < n && j - i < kGroupMaxCalls && ws[j]->qtype == w.qtype && ws[j]->K == w.K) {
+            g.W[j - i] = ws[j]->data;
+            g.y[j - i] = ys[j];
+            g.row_begin[j - i] = rows;
+            rows += ws[j]->M;
+            ++j;
+        }
+        g.ncalls = j - i;
+        g.norm_w = norm_w;
+        g.norm_eps = cfg_.rms_norm_eps;
+        const LinearShape shape{w.qtype, rows, w.K, (w.K + 31) / 32, 1};
+        check(launch_gemv_decode(shape, g, x, norm_w != nullptr, acc, s), "launch_gemv_decode");
+        i = j;
+    }
+}
+
+// One decode step.  Where a layer's linears are quantized, the RMSNorm is
+// done by the consuming GEMVs (norm mode, reading the residual stream x_) and
+// the residual add by the producing ones (o and down accumulate into x_):
+// per layer q/k/v -> attention -> o -> gate/up -> SwiGLU -> down.  Otherwise
+// (F32 weights) the separate add + RMSNorm kernel runs, with `pending` the
+// residual delta it still has to add.
 void Decoder::enqueue_step(hipStream_t s, bool pick, bool advance) {
     const DecoderConfig& c = cfg_;
-    const int q_dim = c.n_heads * c.head_dim;
-    const int kv_dim = c.n_kv_heads * c.head_dim;
+    auto quant = [](const Linear& w) { return w.qtype != 0; };
     hipLaunchKernelGGL(embed_kernel, dim3((c.dim + 255) / 256), dim3(256), 0, s, embedding_, c.vocab_size, c.dim,
                        state_, x_);
     check(hipGetLastError(), "embed_kernel");
+    const float* pending = nullptr;
     for (int l = 0; l < c.n_layers; ++l) {
         const Layer& L = layers_[l];
-        launch_norm(s, l == 0 ? nullptr : ff_, L.attn_norm);
         const Linear* qkv[3] = {&L.wq, &L.wk, &L.wv};
         float* qkv_y[3] = {q_, k_, v_};
-        linear_group(s, qkv, qkv_y, 3, h_);
+        if (pending == nullptr && quant(L.wq) && quant(L.wk) && quant(L.wv)) {
+            linear_fused(s, qkv, qkv_y, 3, x_, L.attn_norm, false);
+        } else {
+            launch_norm(s, pending, L.attn_norm);
+            pending = nullptr;
+            linear_group(s, qkv, qkv_y, 3, h_);
+        }
         if (!launch_attention_rope(s, l)) {
+            const int q_dim = c.n_heads * c.head_dim;
+            const int kv_dim = c.n_kv_heads * c.head_dim;
             const int rope_threads = q_dim / 2 + kv_dim / 2 + kv_dim;
             hipLaunchKernelGGL(rope_kv_kernel, dim3((rope_threads + 255) / 256), dim3(256), 0, s, q_, k_, v_, L.bq,
                                L.bk, L.bv, c.n_heads, c.n_kv_heads, c.head_dim, c.rope_theta, c.rope_neox,
@@ -1043,36 +1083,64 @@ void Decoder::enqueue_step(hipStream_t s, bool pick, bool advance) {
             check(hipGetLastError(), "attention_kernel");
         }
         const Linear* wo[1] = {&L.wo};
-        float* wo_y[1] = {proj_};
-        linear_group(s, wo, wo_y, 1, att_);
-        launch_norm(s, proj_, L.ffn_norm);
+        if (quant(L.wo)) {
+            float* wo_y[1] = {x_};
+            linear_fused(s, wo, wo_y, 1, att_, nullptr, true);
+        } else {
+            float* wo_y[1] = {proj_};
+            linear_group(s, wo, wo_y, 1, att_);
+            pending = proj_;
+        }
         const Linear* gu[2] = {&L.w_gate, &L.w_up};
         float* gu_y[2] = {gate_, up_};
-        linear_group(s, gu, gu_y, 2, h_);
+        if (pending == nullptr && quant(L.w_gate) && quant(L.w_up)) {
+            linear_fused(s, gu, gu_y, 2, x_, L.ffn_norm, false);
+        } else {
+            launch_norm(s, pending, L.ffn_norm);
+            pending = nullptr;
+            linear_group(s, gu, gu_y, 2, h_);
+        }
         hipLaunchKernelGGL(swiglu_kernel, dim3((c.hidden_dim + 255) / 256), dim3(256), 0, s, gate_, up_, act_,
                            c.hidden_dim);
         check(hipGetLastError(), "swiglu_kernel");
         const Linear* wd[1] = {&L.w_down};
-        float* wd_y[1] = {ff_};
-        linear_group(s, wd, wd_y, 1, act_);
+        if (quant(L.w_down)) {
+            float* wd_y[1] = {x_};
+            linear_fused(s, wd, wd_y, 1, act_, nullptr, true);
+        } else {
+            float* wd_y[1] = {ff_};
+            linear_group(s, wd, wd_y, 1, act_);
+            pending = ff_;
+        }
     }
     if (!pick && advance) {  // a prompt step before the last: no logits needed
         hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(64), 0, s, state_, io_);
         check(hipGetLastError(), "advance_kernel");
         return;
     }
-    launch_norm(s, ff_, final_norm_);
-    if (pick && lm_head_.qtype != 0) {
-        const LinearShape shape{lm_head_.qtype, lm_head_.M, lm_head_.K, (lm_head_.K + 31) / 32, 1};
-        check(launch_gemv_pick(shape, lm_head_.data, h_, nullptr, static_cast<PickState*>(pick_), &state_->next, s),
-              "launch_gemv_pick");
-    } else {
+    const bool fused_head = pending == nullptr && quant(lm_head_);
+    const LinearShape head{lm_head_.qtype, lm_head_.M, lm_head_.K, (lm_head_.K + 31) / 32, 1};
+    if (pick && fused_head) {
+        check(launch_gemv_pick_norm(head, lm_head_.data, x_, final_norm_, c.rms_norm_eps, nullptr,
+                                    static_cast<PickState*>(pick_), &state_->next, s),
+              "launch_gemv_pick_norm");
+    } else if (fused_head) {
         const Linear* lm[1] = {&lm_head_};
         float* lm_y[1] = {logits_};
-        linear_group(s, lm, lm_y, 1, h_);
-        if (pick) {
-            hipLaunchKernelGGL(pick_f32_kernel, dim3(1), dim3(1024), 0, s, logits_, c.vocab_size, state_);
-            check(hipGetLastError(), "pick_f32_kernel");
+        linear_fused(s, lm, lm_y, 1, x_, final_norm_, false);
+    } else {
+        launch_norm(s, pending, final_norm_);
+        if (pick && quant(lm_head_)) {
+            check(launch_gemv_pick(head, lm_head_.data, h_, nullptr, static_cast<PickState*>(pick_), &state_->next, s),
+                  "launch_gemv_pick");
+        } else {
+            const Linear* lm[1] = {&lm_head_};
+            float* lm_y[1] = {logits_};
+            linear_group(s, lm, lm_y, 1, h_);
+            if (pick) {
+                hipLaunchKernelGGL(pick_f32_kernel, dim3(1), dim3(1024), 0, s, logits_, c.vocab_size, state_);
+                check(hipGetLastError(), "pick_f32_kernel");
+            }
         }
     }
     if (advance) {

@@ -145,13 +145,30 @@ __device__ __forceinline__ void pick_finish(PickState* ps, int32_t* token, unsig
     *token = pick_token(k);
 }
 
+// Launch modes of the GEMV kernels.  The plain mode stores y = W x; the pick
+// modes also fold the greedy pick over y (y may be null); the norm modes
+// stage rmsnorm(x) * norm_w instead of x (the decode step's RMSNorm, done by
+// each workgroup on its own copy of x); the accumulate mode adds the rows into
+// y (the decode step's residual add: y is the residual stream, x another
+// buffer).
+constexpr int kModePlain = 0;
+constexpr int kModePick = 1;
+constexpr int kModeNorm = 2;
+constexpr int kModeNormPick = 3;
+constexpr int kModeAcc = 4;
+template <int MODE> struct Mode {
+    static constexpr bool pick = MODE == kModePick || MODE == kModeNormPick;
+    static constexpr bool norm = MODE == kModeNorm || MODE == kModeNormPick;
+    static constexpr bool acc = MODE == kModeAcc;
+};
+
 // Waves per SIMD the single kernel's registers are bounded for: four (two
 // workgroups per CU) except Q8_0 with two rows per slot, whose 2 x 17 pair
 // dwords in flight do not fit 128 VGPRs without spilling.
 template <int QT, int R> struct SingleOcc { static constexpr int waves_per_simd = (QT == 1 && R == 2) ? 2 : 4; };
 
 // Rows of at most LPR pairs: x in VGPRs, persistent over row groups.
-template <int QT, int LPR, int R, int WAVES, bool PICK>
+template <int QT, int LPR, int R, int WAVES, int MODE>
 __global__ __launch_bounds__(WAVES * 64, (SingleOcc<QT, R>::waves_per_simd)) void gemv_single_kernel(
     const GemvGroup g, const float* __restrict__ x, int M, int K, int nb, int groups) {
     constexpr int DW = Fmt<QT>::DW;
@@ -174,9 +191,17 @@ __global__ __launch_bounds__(WAVES * 64, (SingleOcc<QT, R>::waves_per_simd)) voi
     // Every weight request is unconditional (a group past the end re-reads the
     // last one; its result is dropped): a guarded request makes the compiler
     // wait for it right away, which serialises the prefetch.
+    constexpr bool PICK = Mode<MODE>::pick;
+    constexpr bool ACC = Mode<MODE>::acc;
     uint32_t wc[R][DW];
+    float rc[R];  // accumulate mode: the residual of the rows, requested with their weights
     load_rows<R, DW>(g, row_dw, min(gi, groups - 1) * (SUB * R) + slot * R, M, p, wc);
-    stage_x<QT>(x, K, nb, xs4, cb);
+    if (ACC) {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            rc[r] = *group_y(g, min(min(gi, groups - 1) * (SUB * R) + slot * R + r, M - 1), M, blockIdx.y);
+    }
+    stage_x<QT, false, Mode<MODE>::norm>(x, K, nb, xs4, cb, g.norm_w, g.norm_eps);
     __syncthreads();
     float xv[64];
     load_xv(xs4, p, xv);
@@ -188,8 +213,13 @@ __global__ __launch_bounds__(WAVES * 64, (SingleOcc<QT, R>::waves_per_simd)) voi
 
     for (; gi < groups; gi += gstride) {
         uint32_t wn[R][DW];
+        float rn[R];
         const int gn = min(gi + gstride, groups - 1);
         load_rows<R, DW>(g, row_dw, gn * (SUB * R) + slot * R, M, p, wn);
+        if (ACC) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) rn[r] = *group_y(g, min(gn * (SUB * R) + slot * R + r, M - 1), M, blockIdx.y);
+        }
         __builtin_amdgcn_sched_barrier(0);  // the request stays ahead of this group's compute
         float acc[R];
 #pragma unroll
@@ -202,7 +232,7 @@ __global__ __launch_bounds__(WAVES * 64, (SingleOcc<QT, R>::waves_per_simd)) voi
 #pragma unroll
             for (int r = 0; r < R; ++r) {
                 if (row0 + r < M) {
-                    if (store_y) *group_y(g, row0 + r, M, blockIdx.y) = acc[r];
+                    if (store_y) *group_y(g, row0 + r, M, blockIdx.y) = ACC ? rc[r] + acc[r] : acc[r];
                     if (PICK) {
                         const unsigned long long k = pick_key(acc[r], row0 + r);
                         best = k > best ? k : best;
@@ -211,15 +241,17 @@ __global__ __launch_bounds__(WAVES * 64, (SingleOcc<QT, R>::waves_per_simd)) voi
             }
         }
 #pragma unroll
-        for (int r = 0; r < R; ++r)
+        for (int r = 0; r < R; ++r) {
 #pragma unroll
             for (int i = 0; i < DW; ++i) wc[r][i] = wn[r][i];
+            if (ACC) rc[r] = rn[r];
+        }
     }
     if (PICK) pick_finish<WAVES>(g.pick, g.token, best);
 }
 
 // Rows of more than LPR pairs: one row group per wave, x from LDS per pair.
-template <int QT, int LPR, int R, int WAVES, bool PICK>
+template <int QT, int LPR, int R, int WAVES, int MODE>
 __global__ __launch_bounds__(WAVES * 64) void gemv_multi_kernel(
     const GemvGroup g, const float* __restrict__ x, int M, int K, int nb) {
     constexpr int DW = Fmt<QT>::DW;
@@ -239,10 +271,17 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_multi_kernel(
     // Chunks c = 0 .. nch-1 (pair c * LPR + pl of every lane) in a uniform loop;
     // lanes past the row keep their sum.  Requests are unconditional (past the
     // row: re-read the last pair) so the prefetch is never waited for early.
+    constexpr bool PICK = Mode<MODE>::pick;
+    constexpr bool ACC = Mode<MODE>::acc;
     const int nch = (np + LPR - 1) / LPR;
     uint32_t wc[R][DW];
     load_rows<R, DW>(g, row_dw, row0, M, min(pl, np - 1), wc);
-    stage_x<QT>(x, K, nb, xs4, cb);
+    float res[R];  // accumulate mode: the rows' residual, requested up front
+    if (ACC) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) res[r] = *group_y(g, min(row0 + r, M - 1), M, blockIdx.y);
+    }
+    stage_x<QT, false, Mode<MODE>::norm>(x, K, nb, xs4, cb, g.norm_w, g.norm_eps);
     __syncthreads();
     const NibConsts nk = NibConsts::make();
     float acc[R];
@@ -275,7 +314,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_multi_kernel(
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             if (row0 + r < M) {
-                if (!PICK || g.y[0] != nullptr) *group_y(g, row0 + r, M, blockIdx.y) = acc[r];
+                if (!PICK || g.y[0] != nullptr) *group_y(g, row0 + r, M, blockIdx.y) = ACC ? res[r] + acc[r] : acc[r];
                 if (PICK) {
                     const unsigned long long k = pick_key(acc[r], row0 + r);
                     best = k > best ? k : best;
@@ -289,9 +328,12 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_multi_kernel(
 // ---------------------------------------------------------------------------
 // Generic kernel: one wave per output row, lanes over blocks, byte loads.
 // Handles every shape (odd block counts, K beyond the LDS budget).
-template <int QT, bool PICK>
+template <int QT, int MODE>
 __global__ __launch_bounds__(256) void gemv_generic_kernel(const GemvGroup g, const float* __restrict__ x,
                                                            int M, int K, int nb) {
+    constexpr bool PICK = Mode<MODE>::pick;
+    constexpr bool NORM = Mode<MODE>::norm;
+    constexpr bool ACC = Mode<MODE>::acc;
     constexpr int BB = Fmt<QT>::BB;
     const int lane = threadIdx.x & 63;
     const int wave_row = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -303,6 +345,18 @@ __global__ __launch_bounds__(256) void gemv_generic_kernel(const GemvGroup g, co
     const int k = group_call(g, row);
     const uint8_t* W = static_cast<const uint8_t*>(g.W[k]) +
                        static_cast<size_t>(row - g.row_begin[k]) * nb * BB;
+    const float res = ACC ? *group_y(g, row, M, blockIdx.y) : 0.0f;
+    // Norm mode: each wave reduces the squares of x itself and reads
+    // x * scale * w on the fly.
+    float scale = 1.0f;
+    if (NORM) {
+        float ss = 0.0f;
+        for (int i = lane; i < K; i += 64) ss += x[i] * x[i];
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+        scale = 1.0f / sqrtf(ss / static_cast<float>(K) + g.norm_eps);
+    }
+    auto xat = [&](int i) { return NORM ? x[i] * scale * g.norm_w[i] : x[i]; };
     float acc = 0.0f;
     for (int b = lane; b < nb; b += 64) {
         const uint8_t* blk = W + static_cast<size_t>(b) * BB;
@@ -322,8 +376,9 @@ __global__ __launch_bounds__(256) void gemv_generic_kernel(const GemvGroup g, co
                 const int nib = (i < 16) ? (byte & 15) : (byte >> 4);
                 q = static_cast<float>(QT == 2 ? nib - 8 : nib);
             }
-            s = __builtin_fmaf(q, x[k0 + i], s);
-            sx += x[k0 + i];
+            const float xi = xat(k0 + i);
+            s = __builtin_fmaf(q, xi, s);
+            sx += xi;
         }
         acc = __builtin_fmaf(d, s, acc);
         if (QT == 3) {
@@ -333,7 +388,7 @@ __global__ __launch_bounds__(256) void gemv_generic_kernel(const GemvGroup g, co
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
-    if (lane == 0 && live && (!PICK || g.y[0] != nullptr)) *group_y(g, row, M, blockIdx.y) = acc;
+    if (lane == 0 && live && (!PICK || g.y[0] != nullptr)) *group_y(g, row, M, blockIdx.y) = ACC ? res + acc : acc;
     if (PICK) pick_finish<4>(g.pick, g.token, lane == 0 && live ? pick_key(acc, row) : 0ull);
 }
 
@@ -362,55 +417,69 @@ PairCfg choose_pair(const LinearShape& s) {
     return PairCfg{Kind::Multi, 16, 1};
 }
 
-template <int QT, int LPR, int R, bool PICK>
+template <int QT, int LPR, int R, int MODE>
 hipError_t launch_single_t(const LinearShape& s, const GemvGroup& g, const float* x, hipStream_t stream) {
     constexpr int rows_per_group = (64 / LPR) * R;
     const int groups = (s.M + rows_per_group - 1) / rows_per_group;
     int grid = (groups + kWaves - 1) / kWaves;
     if (grid > kPersistentWgs) grid = kPersistentWgs;
-    hipLaunchKernelGGL((gemv_single_kernel<QT, LPR, R, kWaves, PICK>), dim3(grid, s.rows), dim3(kWaves * 64),
+    hipLaunchKernelGGL((gemv_single_kernel<QT, LPR, R, kWaves, MODE>), dim3(grid, s.rows), dim3(kWaves * 64),
                        pair_lds_bytes(s.nb), stream, g, x, s.M, s.K, s.nb, groups);
     return hipGetLastError();
 }
 
-template <int QT, int LPR, bool PICK>
+template <int QT, int LPR, int MODE>
 hipError_t launch_multi_t(const LinearShape& s, const GemvGroup& g, const float* x, hipStream_t stream) {
     constexpr int rows_per_wg = kWaves * (64 / LPR);
     dim3 grid((s.M + rows_per_wg - 1) / rows_per_wg, s.rows);
-    hipLaunchKernelGGL((gemv_multi_kernel<QT, LPR, 1, kWaves, PICK>), grid, dim3(kWaves * 64), pair_lds_bytes(s.nb),
+    hipLaunchKernelGGL((gemv_multi_kernel<QT, LPR, 1, kWaves, MODE>), grid, dim3(kWaves * 64), pair_lds_bytes(s.nb),
                        stream, g, x, s.M, s.K, s.nb);
     return hipGetLastError();
 }
 
-template <int QT, bool PICK>
+template <int QT, int MODE>
 hipError_t launch_q(const LinearShape& s, const PairCfg& c, const GemvGroup& g, const float* x,
                     hipStream_t stream) {
     if (c.kind == Kind::Single) {
-        if (c.lpr == 16) return launch_single_t<QT, 16, 1, PICK>(s, g, x, stream);
-        if (c.r == 2) return launch_single_t<QT, 64, 2, PICK>(s, g, x, stream);
-        return launch_single_t<QT, 64, 1, PICK>(s, g, x, stream);
+        if (c.lpr == 16) return launch_single_t<QT, 16, 1, MODE>(s, g, x, stream);
+        if (c.r == 2) return launch_single_t<QT, 64, 2, MODE>(s, g, x, stream);
+        return launch_single_t<QT, 64, 1, MODE>(s, g, x, stream);
     }
     if (c.kind == Kind::Multi) {
-        if (c.lpr == 64) return launch_multi_t<QT, 64, PICK>(s, g, x, stream);
-        if (c.lpr == 32) return launch_multi_t<QT, 32, PICK>(s, g, x, stream);
-        return launch_multi_t<QT, 16, PICK>(s, g, x, stream);
+        if (c.lpr == 64) return launch_multi_t<QT, 64, MODE>(s, g, x, stream);
+        if (c.lpr == 32) return launch_multi_t<QT, 32, MODE>(s, g, x, stream);
+        return launch_multi_t<QT, 16, MODE>(s, g, x, stream);
     }
     dim3 grid((s.M + 3) / 4, s.rows);
-    hipLaunchKernelGGL((gemv_generic_kernel<QT, PICK>), grid, dim3(256), 0, stream, g, x, s.M, s.K, s.nb);
+    hipLaunchKernelGGL((gemv_generic_kernel<QT, MODE>), grid, dim3(256), 0, stream, g, x, s.M, s.K, s.nb);
     return hipGetLastError();
+}
+
+template <int MODE>
+hipError_t launch_mode(const LinearShape& s, const GemvGroup& g, const float* x, hipStream_t stream) {
+    const PairCfg c = choose_pair(s);
+    switch (s.qtype) {
+        case 1: return launch_q<1, MODE>(s, c, g, x, stream);
+        case 2: return launch_q<2, MODE>(s, c, g, x, stream);
+        case 3: return launch_q<3, MODE>(s, c, g, x, stream);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 }  // namespace
 
 hipError_t launch_gemv_group(const LinearShape& s, const GemvGroup& g, const float* x, hipStream_t stream) {
     if (g.ncalls < 1 || g.ncalls > kGroupMaxCalls) return hipErrorInvalidValue;
-    const PairCfg c = choose_pair(s);
-    switch (s.qtype) {
-        case 1: return launch_q<1, false>(s, c, g, x, stream);
-        case 2: return launch_q<2, false>(s, c, g, x, stream);
-        case 3: return launch_q<3, false>(s, c, g, x, stream);
-        default: return hipErrorInvalidValue;
-    }
+    return launch_mode<kModePlain>(s, g, x, stream);
+}
+
+hipError_t launch_gemv_decode(const LinearShape& s, const GemvGroup& g, const float* x, bool norm, bool accumulate,
+                              hipStream_t stream) {
+    if (g.ncalls < 1 || g.ncalls > kGroupMaxCalls || (norm && accumulate)) return hipErrorInvalidValue;
+    if (norm && g.norm_w == nullptr) return hipErrorInvalidValue;
+    if (accumulate) return launch_mode<kModeAcc>(s, g, x, stream);
+    if (norm) return launch_mode<kModeNorm>(s, g, x, stream);
+    return launch_mode<kModePlain>(s, g, x, stream);
 }
 
 hipError_t launch_gemv_pick(const LinearShape& s, const void* w, const float* x, float* y, PickState* ps,
@@ -422,13 +491,21 @@ hipError_t launch_gemv_pick(const LinearShape& s, const void* w, const float* x,
     g.ncalls = 1;
     g.pick = ps;
     g.token = token;
-    const PairCfg c = choose_pair(s);
-    switch (s.qtype) {
-        case 1: return launch_q<1, true>(s, c, g, x, stream);
-        case 2: return launch_q<2, true>(s, c, g, x, stream);
-        case 3: return launch_q<3, true>(s, c, g, x, stream);
-        default: return hipErrorInvalidValue;
-    }
+    return launch_mode<kModePick>(s, g, x, stream);
+}
+
+hipError_t launch_gemv_pick_norm(const LinearShape& s, const void* w, const float* x, const float* norm_w,
+                                 float norm_eps, float* y, PickState* ps, int32_t* token, hipStream_t stream) {
+    if (s.rows != 1 || ps == nullptr || token == nullptr || norm_w == nullptr) return hipErrorInvalidValue;
+    GemvGroup g{};
+    g.W[0] = w;
+    g.y[0] = y;
+    g.ncalls = 1;
+    g.pick = ps;
+    g.token = token;
+    g.norm_w = norm_w;
+    g.norm_eps = norm_eps;
+    return launch_mode<kModeNormPick>(s, g, x, stream);
 }
 
 hipError_t launch_gemv(const LinearShape& s, const void* w, const float* x, float* y,

@@ -60,9 +60,16 @@ inline int pair_lds_bytes(int nb) { return (nb / 2) * 256 + nb * 8; }
 // its block from LDS.  A block's two pair partners (g, g ^ 1) are neighbouring
 // lanes of one wave, so every read of the region happens before any write
 // that permutes it.
-template <int QT, bool COHERENT = false>
+// NORM stages rmsnorm(x) * w instead of x (src/ops.cpp:18-41: mean of
+// squares over the K elements, scale = 1 / sqrt(ms + eps), x * scale * w):
+// every workgroup normalises its own copy.  Each thread loads its block's x
+// and w together, the squares are reduced over the workgroup once (every
+// thread of the block takes part; NORM needs nb <= blockDim, one block per
+// thread), and the values are scaled from registers -- x is read once.
+template <int QT, bool COHERENT = false, bool NORM = false>
 __device__ __forceinline__ void stage_x(const float* __restrict__ x, int K, int nb,
-                                        float4* __restrict__ xs4, float2* __restrict__ cb) {
+                                        float4* __restrict__ xs4, float2* __restrict__ cb,
+                                        const float* __restrict__ norm_w = nullptr, float norm_eps = 0.0f) {
     if (COHERENT) {
         constexpr int kAgentScope = 16;  // sc1 cache policy
         const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
@@ -83,7 +90,9 @@ __device__ __forceinline__ void stage_x(const float* __restrict__ x, int K, int 
         }
         __syncthreads();
     }
-    for (int g = threadIdx.x; g < nb; g += blockDim.x) {
+    for (int g0 = 0; g0 < nb; g0 += blockDim.x) {
+        const int g = NORM ? min(static_cast<int>(threadIdx.x), nb - 1) : g0 + static_cast<int>(threadIdx.x);
+        if (!NORM && g >= nb) break;
         float v[32];
         const int k0 = g * kQK;
         if (COHERENT) {
@@ -109,6 +118,39 @@ __device__ __forceinline__ void stage_x(const float* __restrict__ x, int K, int 
         } else {
 #pragma unroll
             for (int i = 0; i < 32; ++i) v[i] = (k0 + i < K) ? as_global(x)[k0 + i] : 0.0f;
+        }
+        if (NORM) {
+            float w[32];
+            if (k0 + kQK <= K && (reinterpret_cast<uintptr_t>(norm_w + k0) & 15u) == 0) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const f32x4_t fv = ((g_f4*)(norm_w + k0))[i];
+                    w[4 * i] = fv.x;
+                    w[4 * i + 1] = fv.y;
+                    w[4 * i + 2] = fv.z;
+                    w[4 * i + 3] = fv.w;
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 32; ++i) w[i] = (k0 + i < K) ? as_global(norm_w)[k0 + i] : 0.0f;
+            }
+            // Squares of this thread's block (a repeated last block counts 0).
+            float ss = 0.0f;
+            if (static_cast<int>(threadIdx.x) < nb) {
+#pragma unroll
+                for (int i = 0; i < 32; ++i) ss += v[i] * v[i];
+            }
+            __shared__ float part[16];
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+            if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+            __syncthreads();
+            float t = part[0];
+            for (int i = 1; i < static_cast<int>(blockDim.x >> 6); ++i) t += part[i];
+            const float scale = 1.0f / sqrtf(t / static_cast<float>(K) + norm_eps);
+#pragma unroll
+            for (int i = 0; i < 32; ++i) v[i] = v[i] * scale * w[i];
+            if (static_cast<int>(threadIdx.x) >= nb) break;
         }
         float X = 0.0f;
         float S = 0.0f;

@@ -50,6 +50,8 @@ struct GemvGroup {
     int ncalls;
     PickState* pick;  // greedy-pick launches only (launch_gemv_pick)
     int32_t* token;
+    const float* norm_w;  // norm launches only: RMSNorm weights [K]
+    float norm_eps;
 };
 
 hipError_t launch_gemv_group(const LinearShape& s, const GemvGroup& g, const float* x, hipStream_t stream);
@@ -71,6 +73,17 @@ struct PickState {
 
 hipError_t launch_gemv_pick(const LinearShape& s, const void* w, const float* x, float* y, PickState* ps,
                             int32_t* token, hipStream_t stream);
+
+// Decode-step forms of a (grouped) GEMV, rows == 1 or a batch:
+//  norm:       stage rmsnorm(x) * g.norm_w (eps g.norm_eps) instead of x
+//              (src/ops.cpp:18-41) -- each workgroup normalises its own copy;
+//  accumulate: y += W x (the residual add; y must not overlap x).
+hipError_t launch_gemv_decode(const LinearShape& s, const GemvGroup& g, const float* x, bool norm, bool accumulate,
+                              hipStream_t stream);
+// The greedy pick over W . (rmsnorm(x) * norm_w): the final norm and lm_head
+// of a decode step in one launch.
+hipError_t launch_gemv_pick_norm(const LinearShape& s, const void* w, const float* x, const float* norm_w,
+                                 float norm_eps, float* y, PickState* ps, int32_t* token, hipStream_t stream);
 
 // Batched prefill GEMM for rows > 1 (MFMA).  Needs a device workspace of
 // gemm_workspace_bytes(s) bytes (split x, scales, split-K partials) that no
