@@ -12,13 +12,14 @@
 //    row: coalesced, with the stored format untouched.
 //  * LPR lanes ("a slot") share R rows; lane l of a slot owns pairs
 //    l, l + LPR, ... of those rows.  A wave holds 64 / LPR slots.
-//  * x is staged once per workgroup in LDS as f32 with per-block constants
-//    (one thread per block, whole-block vector loads); 16-byte LDS slots are
+//  * x is staged once per workgroup in LDS as block-scaled integer limbs
+//    with per-block constants (four threads per block, buffer loads whose
+//    range check reads elements past K as 0); 16-byte LDS slots are
 //    XOR-swizzled by pair so a wave's reads spread over the banks.
 //  * Every lane requests its first W pair(s) before staging x, so the W
 //    latency overlaps the staging and the barrier.
-//  * "single" kernel (row of at most LPR pairs): each lane keeps its 64 x
-//    values in VGPRs and the workgroups are persistent (at most ~2 per CU),
+//  * "single" kernel (row of at most LPR pairs): each lane keeps its pair's
+//    x limbs in VGPRs and the workgroups are persistent (at most ~2 per CU),
 //    walking row groups with the next group's W requested before the current
 //    one is computed.  "multi" kernel (longer rows): one row group per wave,
 //    x read from LDS per pair, next pair's W requested before the current one
@@ -26,23 +27,13 @@
 //  * Row sums are reduced across the slot's lanes with DPP adds (quad_perm,
 //    row mirrors, row_bcast), all VALU, no LDS round trip.
 //
-// Arithmetic (VALU, fp32 accumulate, ~1.7 VALU ops per weight):
-//  * A stored nibble or biased byte becomes an exact fp16 integer with one
-//    AND-OR (or one byte permute) against the fp16 pattern 0x6400 (1024.0):
-//    Q4 low nibble q -> 1024 + q, Q4 high nibble (masked in place) -> 1024 + 16q,
-//    Q8 byte q ^ 0x80 -> 1024 + 128 + q.  Two such values share a dword.
-//  * v_fma_mix_f32 multiplies the fp16 half by the f32 x element and
-//    accumulates in f32; x of high-nibble elements is pre-scaled by 1/16 so
-//    16q * x/16 == q * x.
-//  * Each block is summed in two chains (ILP) starting at -bias, where
-//    bias = 1024 * sum(x') + 8 * sum(x) (Q4_0), 1024 * sum(x') (Q4_1),
-//    1152 * sum(x) (Q8_0) is computed once per workgroup; the chains end at
-//    sum(q_signed * x) for the block, then y += d * sum (+ m * sum(x) for Q4_1)
-//    with d and m read as fp16 operands of the same fma_mix.
-//  Products are exact; only the f32 accumulations round.  The intermediate
-//  magnitude (~1024 * |partial sum of x|) costs ~10 bits of the f32 sum, i.e.
-//  ~1e-4 relative error per block sum, far inside the 1e-3 tolerance.
-//
+// Arithmetic (integer dot products, exact per block; gemv_device.h): x is
+// written per block as s_b * X with X a 16-bit (Q4) or 23-bit (Q8_0) integer
+// in int8 limbs, the stored nibbles / bytes meet the limbs in v_dot4 (4
+// products per instruction, ~1.0 VALU op per Q4 weight and ~0.8 per Q8_0
+// weight including the unpacking), and each block's exact integer sum is
+// scaled by d * s_b into the f32 row sum.
+
 // Rows with an odd block count (pairs would straddle rows) and very long rows
 // go to a simple one-wave-per-row kernel with byte loads.
 
@@ -175,8 +166,8 @@ __global__ __launch_bounds__(WAVES * 64, (SingleOcc<QT, R>::waves_per_simd)) voi
     constexpr int SUB = 64 / LPR;
     extern __shared__ float4 lds4[];
     const int np = nb >> 1;
-    float4* xs4 = lds4;
-    float2* cb = reinterpret_cast<float2*>(lds4 + np * 16);
+    uint32_t* xl = reinterpret_cast<uint32_t*>(lds4);
+    float4* xc = reinterpret_cast<float4*>(xl + np * XLimbs<QT>::PAIR_DW);
     x += static_cast<size_t>(blockIdx.y) * K;
 
     const int lane = threadIdx.x & 63;
@@ -201,13 +192,10 @@ __global__ __launch_bounds__(WAVES * 64, (SingleOcc<QT, R>::waves_per_simd)) voi
         for (int r = 0; r < R; ++r)
             rc[r] = *group_y(g, min(min(gi, groups - 1) * (SUB * R) + slot * R + r, M - 1), M, blockIdx.y);
     }
-    stage_x<QT, false, Mode<MODE>::norm>(x, K, nb, xs4, cb, g.norm_w, g.norm_eps);
-    __syncthreads();
-    float xv[64];
-    load_xv(xs4, p, xv);
-    const float2 c0 = cb[2 * p];
-    const float2 c1 = cb[2 * p + 1];
-    const NibConsts nk = NibConsts::make();
+    stage_x<QT, false, Mode<MODE>::norm>(x, K, nb, xl, xc, g.norm_w, g.norm_eps);
+    uint32_t xq[XLimbs<QT>::PAIR_DW];
+    float4 c0, c1;
+    load_xq<QT>(xl, xc, p, xq, c0, c1);
     const bool store_y = !PICK || g.y[0] != nullptr;
     unsigned long long best = 0;
 
@@ -224,7 +212,7 @@ __global__ __launch_bounds__(WAVES * 64, (SingleOcc<QT, R>::waves_per_simd)) voi
         float acc[R];
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            acc[r] = active ? PairDot<QT>::run(wc[r], xv, c0, c1, 0.0f, nk) : 0.0f;
+            acc[r] = active ? PairDot<QT>::run(wc[r], xq, c0, c1, 0.0f) : 0.0f;
             acc[r] = group_sum<LPR>(acc[r]);
         }
         if (pl == LPR - 1) {
@@ -258,8 +246,8 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_multi_kernel(
     constexpr int SUB = 64 / LPR;
     extern __shared__ float4 lds4[];
     const int np = nb >> 1;
-    float4* xs4 = lds4;
-    float2* cb = reinterpret_cast<float2*>(lds4 + np * 16);
+    uint32_t* xl = reinterpret_cast<uint32_t*>(lds4);
+    float4* xc = reinterpret_cast<float4*>(xl + np * XLimbs<QT>::PAIR_DW);
     x += static_cast<size_t>(blockIdx.y) * K;
 
     const int lane = threadIdx.x & 63;
@@ -281,9 +269,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_multi_kernel(
 #pragma unroll
         for (int r = 0; r < R; ++r) res[r] = *group_y(g, min(row0 + r, M - 1), M, blockIdx.y);
     }
-    stage_x<QT, false, Mode<MODE>::norm>(x, K, nb, xs4, cb, g.norm_w, g.norm_eps);
-    __syncthreads();
-    const NibConsts nk = NibConsts::make();
+    stage_x<QT, false, Mode<MODE>::norm>(x, K, nb, xl, xc, g.norm_w, g.norm_eps);
     float acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = 0.0f;
@@ -293,13 +279,12 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_multi_kernel(
         uint32_t wn[R][DW];
         load_rows<R, DW>(g, row_dw, row0, M, min(p + LPR, np - 1), wn);
         __builtin_amdgcn_sched_barrier(0);  // the request stays ahead of this chunk's compute
-        float xv[64];
-        load_xv(xs4, pc, xv);
-        const float2 c0 = cb[2 * pc];
-        const float2 c1 = cb[2 * pc + 1];
+        uint32_t xq[XLimbs<QT>::PAIR_DW];
+        float4 c0, c1;
+        load_xq<QT>(xl, xc, pc, xq, c0, c1);
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const float a = PairDot<QT>::run(wc[r], xv, c0, c1, acc[r], nk);
+            const float a = PairDot<QT>::run(wc[r], xq, c0, c1, acc[r]);
             acc[r] = p < np ? a : acc[r];
         }
 #pragma unroll
@@ -405,7 +390,7 @@ struct PairCfg {
 };
 
 PairCfg choose_pair(const LinearShape& s) {
-    if (s.nb % 2 != 0 || pair_lds_bytes(s.nb) > kMaxPairLdsBytes) return PairCfg{Kind::Generic, 64, 1};
+    if (s.nb % 2 != 0 || pair_lds_bytes(s.qtype, s.nb) > kMaxPairLdsBytes) return PairCfg{Kind::Generic, 64, 1};
     const int np = s.nb / 2;
     if (np <= 16) return PairCfg{Kind::Single, 16, 1};
     if (np <= 64) return PairCfg{Kind::Single, 64, s.M <= 8192 ? 2 : 1};
@@ -424,7 +409,7 @@ hipError_t launch_single_t(const LinearShape& s, const GemvGroup& g, const float
     int grid = (groups + kWaves - 1) / kWaves;
     if (grid > kPersistentWgs) grid = kPersistentWgs;
     hipLaunchKernelGGL((gemv_single_kernel<QT, LPR, R, kWaves, MODE>), dim3(grid, s.rows), dim3(kWaves * 64),
-                       pair_lds_bytes(s.nb), stream, g, x, s.M, s.K, s.nb, groups);
+                       pair_lds_bytes(QT, s.nb), stream, g, x, s.M, s.K, s.nb, groups);
     return hipGetLastError();
 }
 
@@ -432,7 +417,7 @@ template <int QT, int LPR, int MODE>
 hipError_t launch_multi_t(const LinearShape& s, const GemvGroup& g, const float* x, hipStream_t stream) {
     constexpr int rows_per_wg = kWaves * (64 / LPR);
     dim3 grid((s.M + rows_per_wg - 1) / rows_per_wg, s.rows);
-    hipLaunchKernelGGL((gemv_multi_kernel<QT, LPR, 1, kWaves, MODE>), grid, dim3(kWaves * 64), pair_lds_bytes(s.nb),
+    hipLaunchKernelGGL((gemv_multi_kernel<QT, LPR, 1, kWaves, MODE>), grid, dim3(kWaves * 64), pair_lds_bytes(QT, s.nb),
                        stream, g, x, s.M, s.K, s.nb);
     return hipGetLastError();
 }

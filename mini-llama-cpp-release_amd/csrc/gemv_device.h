@@ -1,8 +1,27 @@
 // Device helpers shared by the decode GEMV kernels (gemv.hip) and the
 // persistent sequence kernel (sequence.hip): block formats, x staging into
-// LDS, the nibble / byte expansion to exact fp16 integers, the per-pair dot
-// product and the DPP row reduction.  Both translation units include this
-// file so a row is summed in exactly the same order by either kernel.
+// LDS as block-scaled integer limbs, the per-pair integer dot product and the
+// DPP row reduction.  Both translation units include this file so a row is
+// summed in exactly the same order by either kernel.
+//
+// Arithmetic.  Per 32-element block b of x, with m_b = max |x_k| over the
+// block, x is written as x_k = s_b * X_k + e_k with s_b = m_b / R and the
+// integer X_k = rint(x_k / s_b), |X_k| <= R, |e_k| <= s_b / 2:
+//   Q4_0 / Q4_1: R = 32639 (two int8 limbs, X = 256 hi + lo),
+//   Q8_0:        R = 4160000 (three limbs, X = 65536 hi + 256 mid + lo).
+// The weights' integers (Q4 nibbles 0..15, Q8 bytes -128..127) meet the limbs
+// in v_dot4 (four int8 products summed into an int32, exact), so per block
+// and row the kernel gets the exact integer T = sum_k q_k X_k and then
+//   Q4_0: y += d * (s_b * (T - 8 sum_k X_k))     (the -8 folded into the start)
+//   Q4_1: y += d * (s_b * T) + m * sum_k x_k
+//   Q8_0: y += d * (s_b * T)
+// (src/quant.cpp:421-447 computes the same sums over d * q (+ m) in f32).
+// Only x's representation (2^-16 or 2^-23 of the block maximum) and the f32
+// steps after T round.  Against the CPU reference's f32 sums this is
+// ~2e-5 (Q4) / ~1e-7 (Q8) relative to |y| on N(0, 1) inputs, and the error on
+// outputs near zero stays ~20x below the 1e-3 * ||x|| * max|d| floor of the
+// tolerance (Q4; Q8's third limb puts it ~5000x below).  A block holding an
+// Inf or NaN gets s_b = NaN, so the rows it feeds come out NaN as in f32.
 #pragma once
 
 #include "mlq_kernels.h"
@@ -19,13 +38,20 @@ typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ float h_lo(uint32_t v) { return (float)__builtin_bit_cast(h2_t, v).x; }
 __device__ __forceinline__ float h_hi(uint32_t v) { return (float)__builtin_bit_cast(h2_t, v).y; }
 
-constexpr uint32_t kF16Magic2 = 0x64006400u;   // {1024.0h, 1024.0h}
-constexpr uint32_t kF16MagicB = 0x64646464u;   // byte source for v_perm
-
 template <int QT> struct Fmt;
 template <> struct Fmt<1> { static constexpr int BB = 34, DW = 17; };  // Q8_0
 template <> struct Fmt<2> { static constexpr int BB = 18, DW = 9; };   // Q4_0
 template <> struct Fmt<3> { static constexpr int BB = 20, DW = 10; };  // Q4_1
+
+// x limbs per format: L int8 limbs per element; a pair's x is 16 L dwords
+// (per block 8 dwords of 4 elements per limb).
+template <int QT> struct XLimbs {
+    static constexpr int L = QT == 1 ? 3 : 2;
+    static constexpr int PAIR_DW = 16 * L;
+    // Largest |X|: balanced digits of X + 128 (+ 32768) must fit a signed
+    // byte each, and 1.5 * 2^23 + X + 32896 must stay below 2^24.
+    static constexpr float RANGE = QT == 1 ? 4160000.0f : 32639.0f;
+};
 
 // Device pointers that the compiler cannot trace to a kernel argument (loaded
 // from a descriptor table) are generic; generic accesses become FLAT
@@ -33,8 +59,6 @@ template <> struct Fmt<3> { static constexpr int BB = 20, DW = 10; };  // Q4_1
 // wait conservative.  These casts state that the memory is global.
 typedef __attribute__((address_space(1))) const uint32_t g_u32;
 typedef __attribute__((address_space(1))) const float g_f32;
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(1))) const f32x4_t g_f4;
 __device__ __forceinline__ g_u32* as_global(const uint32_t* p) { return (g_u32*)p; }
 __device__ __forceinline__ g_f32* as_global(const float* p) { return (g_f32*)p; }
 
@@ -42,280 +66,318 @@ constexpr int kMaxPairLdsBytes = 64 * 1024;
 constexpr int kWaves = 8;             // waves per workgroup
 constexpr int kPersistentWgs = 512;   // ~2 workgroups per CU on a 256-CU MI355X
 
-// LDS of the pair kernels: 256 B of x per pair plus 8 B of constants per block.
-inline int pair_lds_bytes(int nb) { return (nb / 2) * 256 + nb * 8; }
+// LDS of the pair kernels: the x limbs (64 L bytes per pair) and 16 bytes of
+// constants per block.
+inline int pair_lds_bytes(int qtype, int nb) { return (nb / 2) * 64 * (qtype == 1 ? 3 : 2) + nb * 16; }
+
+#define MLQ_DPP_F32(x, ctrl, rmask) \
+    __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, (x)), (ctrl), (rmask), 0xF, false))
+
+__device__ __forceinline__ float quad_sum(float v) {
+    v += MLQ_DPP_F32(v, 0xB1, 0xF);  // quad_perm [1,0,3,2]
+    v += MLQ_DPP_F32(v, 0x4E, 0xF);  // quad_perm [2,3,0,1]
+    return v;
+}
+
+__device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot4(static_cast<int>(a), static_cast<int>(b), c, false);
+}
+
+// Sum over the workgroup (every thread calls it; the result in every thread).
+__device__ __forceinline__ float workgroup_sum(float v) {
+    __shared__ float part[16];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float t = part[0];
+    for (int i = 1; i < static_cast<int>(blockDim.x >> 6); ++i) t += part[i];
+    return t;
+}
 
 // ---------------------------------------------------------------------------
-// x staging: one thread per block.  Writes x' (f32, Q4 high halves scaled by
-// 1/16) into 16-byte slots swizzled by pair, and per-block constants {c0, c1}:
-//   Q8_0: c0 = 1152 * X          Q4_0: c0 = 1024 * S + 8 * X
-//   Q4_1: c0 = 1024 * S, c1 = X  with X = sum(x), S = sum(x') over the block.
-// Elements past K read as 0, so a partial last block contributes nothing
-// (the reference loops only k < K, src/quant.cpp:421-426).
-// COHERENT reads x with agent-scope (sc1) loads, which return what another
-// workgroup of the same launch stored with agent-scope stores even when this
-// XCD's L2 holds an older copy of the line.  Those loads are not cached, so
-// they are issued as coalesced 16-byte buffer loads (the buffer's range check
-// returns 0 past K) into the pair region of LDS first; each thread then takes
-// its block from LDS.  A block's two pair partners (g, g ^ 1) are neighbouring
-// lanes of one wave, so every read of the region happens before any write
-// that permutes it.
-// NORM stages rmsnorm(x) * w instead of x (src/ops.cpp:18-41: mean of
-// squares over the K elements, scale = 1 / sqrt(ms + eps), x * scale * w):
-// every workgroup normalises its own copy.  Each thread loads its block's x
-// and w together, the squares are reduced over the workgroup once (every
-// thread of the block takes part; NORM needs nb <= blockDim, one block per
-// thread), and the values are scaled from registers -- x is read once.
+// x staging.  Four threads per block, each taking two of the block's eight
+// x dwords (four elements each).  The elements of x dword d are those the
+// kernel's weight dword d of the same block holds, in byte order (PairDot
+// below): Q4 x dword d = 2j + h pairs with qs dword j, low nibbles (h = 0,
+// elements E_j) or high nibbles (h = 1, E_j + 16); Q8_0 x dword j pairs with
+// qs dword j.  E_j, as two runs of two elements, is {4j, 4j+2} except in the
+// first block of a pair of the formats whose qs start 2 bytes into a dword
+// (Q4_0 / Q8_0): there the dwords are {qs[0,1], qs[last 2]} (one byte
+// permute) and then the stored dwords, {4j-2, 4j}.
+template <int QT>
+__device__ __forceinline__ int2 x_runs(int blk, int d) {
+    if (QT == 1) {
+        if (blk == 0) return d == 0 ? make_int2(0, 30) : make_int2(4 * d - 2, 4 * d);
+        return make_int2(4 * d, 4 * d + 2);
+    }
+    const int j = d >> 1, h = (d & 1) * 16;
+    if (QT == 2 && blk == 0) return j == 0 ? make_int2(h, 14 + h) : make_int2(4 * j - 2 + h, 4 * j + h);
+    return make_int2(4 * j + h, 4 * j + 2 + h);
+}
+
+// LDS placement of x dword idx (0 .. 16 L - 1) of pair p: 16-byte quads
+// XOR-swizzled by pair so a wave's reads spread over the banks.
+template <int QT>
+__device__ __forceinline__ int x_slot(int p, int idx) {
+    constexpr int L = XLimbs<QT>::L;
+    const int swz = L == 2 ? (p & 7) : (p & 3);
+    return p * (16 * L) + ((((idx >> 2) ^ swz)) << 2) + (idx & 3);
+}
+
+// The eight elements of thread `sub`'s two x dwords of block g; elements past
+// K read as 0 (buffer range check), so a partial last block contributes
+// nothing (the reference loops only k < K, src/quant.cpp:421-426).
+// COHERENT loads with agent scope (sc1): they return what another workgroup
+// of the same launch stored with agent-scope stores even when this XCD's L2
+// holds an older copy of the line.
+template <int QT, bool COHERENT>
+__device__ __forceinline__ void load8(__amdgpu_buffer_rsrc_t rs, int g, int sub, float (&v)[8]) {
+    constexpr int kPolicy = COHERENT ? 16 : 0;
+    const int blk = g & 1;
+#pragma unroll
+    for (int dd = 0; dd < 2; ++dd) {
+        const int2 r = x_runs<QT>(blk, 2 * sub + dd);
+        const int e0 = (g * kQK + r.x) * 4, e1 = (g * kQK + r.y) * 4;
+        v[4 * dd] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, e0, 0, kPolicy));
+        v[4 * dd + 1] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, e0 + 4, 0, kPolicy));
+        v[4 * dd + 2] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, e1, 0, kPolicy));
+        v[4 * dd + 3] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, e1 + 4, 0, kPolicy));
+    }
+}
+
+// Quantizes thread `sub`'s eight elements of block g (the four threads of the
+// block are one aligned lane quad) and stores their limbs and, from sub 0,
+// the block constants {s_b, -8 sum X (Q4_0, as int bits), sum x, 0}.
+// X = rint(x / s_b) comes out of one fma as the low mantissa bits of
+// x * (1 / s_b) + 1.5 * 2^23 (exact: |X| < 2^22, so the sum stays in the
+// binade whose ulp is 1; the pattern is 0x4B400000 + X).  The balanced
+// base-256 digits are then bytes of that integer offset by 128 (and 32896):
+// lo = byte 0 of X, mid (Q8_0) or hi (Q4) = byte 1 of X + 128, hi (Q8_0) =
+// byte 2 of X + 32896, each read as a signed byte; byte permutes gather four
+// elements' digits into a dword.
+template <int QT>
+__device__ __forceinline__ void emit_block(int g, int sub, const float (&v)[8], uint32_t* __restrict__ xl,
+                                           float4* __restrict__ xc) {
+    constexpr int L = XLimbs<QT>::L;
+    constexpr float RANGE = XLimbs<QT>::RANGE;
+    constexpr float kMagic = 12582912.0f;  // 1.5 * 2^23
+    // Largest |x| of the block, NaN if any element is NaN (Inf stays Inf).
+    float m = __builtin_elementwise_maximum(__builtin_fabsf(v[0]), __builtin_fabsf(v[1]));
+#pragma unroll
+    for (int i = 2; i < 8; i += 2)
+        m = __builtin_elementwise_maximum(m, __builtin_elementwise_maximum(__builtin_fabsf(v[i]), __builtin_fabsf(v[i + 1])));
+    m = __builtin_elementwise_maximum(m, MLQ_DPP_F32(m, 0xB1, 0xF));
+    m = __builtin_elementwise_maximum(m, MLQ_DPP_F32(m, 0x4E, 0xF));
+    // Blocks below 2^-100 are scaled by 2^64 first, so RANGE / m stays finite;
+    // m = Inf or NaN gives inv = 0 and s_b = Inf or NaN: the rows come out
+    // non-finite.
+    const float k = m < 0x1p-100f ? 0x1p64f : 1.0f;
+    const float mk = m * k;
+    const float inv = mk > 0.0f && mk <= 3.4e38f ? RANGE / mk : 0.0f;
+    const float s = (mk / RANGE) / k;
+    uint32_t out[L][2];
+    float xs = 0.0f;
+#pragma unroll
+    for (int dd = 0; dd < 2; ++dd) {
+        uint32_t a[4], b[4], c[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float xv = v[4 * dd + e];
+            if (QT == 3) xs += xv;
+            const float f = __builtin_fmaf(xv * k, inv, kMagic);
+            a[e] = __builtin_bit_cast(uint32_t, f);
+            b[e] = __builtin_bit_cast(uint32_t, f + 128.0f);
+            // (byte 2 of 1.5 * 2^23 is 0x40: taken out of the integer first)
+            if (L == 3) c[e] = __builtin_bit_cast(uint32_t, f + 32896.0f) - 0x00400000u;
+        }
+        // perm(hi, lo, sel): result byte i = byte sel_i of {hi:lo} (lo = 0..3).
+        auto gather = [](const uint32_t (&r)[4], uint32_t byte_sel) -> uint32_t {
+            const uint32_t s01 = byte_sel | ((byte_sel + 4) << 8) | 0x0C0C0000u;  // {r0.b, r1.b, 0, 0}
+            const uint32_t s23 = 0x0C0Cu | (byte_sel << 16) | ((byte_sel + 4) << 24);  // {0, 0, r2.b, r3.b}
+            return __builtin_amdgcn_perm(r[1], r[0], s01) | __builtin_amdgcn_perm(r[3], r[2], s23);
+        };
+        if (L == 2) {
+            out[0][dd] = gather(b, 1);
+            out[1][dd] = gather(a, 0);
+        } else {
+            out[0][dd] = gather(c, 2);
+            out[1][dd] = gather(b, 1);
+            out[2][dd] = gather(a, 0);
+        }
+    }
+    const int p = g >> 1, blk = g & 1;
+#pragma unroll
+    for (int l = 0; l < L; ++l) {
+        const int idx = blk * (8 * L) + l * 8 + 2 * sub;
+        *reinterpret_cast<uint2*>(xl + x_slot<QT>(p, idx)) = make_uint2(out[l][0], out[l][1]);
+    }
+    int sx = 0;
+    if (QT == 2) {  // sum X = 256 sum hi + sum lo over the thread's elements
+        const int ones = 0x01010101;
+        sx = 256 * (dot4(out[0][0], ones, 0) + dot4(out[0][1], ones, 0)) + dot4(out[1][0], ones, 0) +
+             dot4(out[1][1], ones, 0);
+        sx += __builtin_amdgcn_update_dpp(0, sx, 0xB1, 0xF, 0xF, false);
+        sx += __builtin_amdgcn_update_dpp(0, sx, 0x4E, 0xF, 0xF, false);
+    }
+    if (QT == 3) xs = quad_sum(xs);
+    if (sub == 0) xc[g] = make_float4(s, __builtin_bit_cast(float, -8 * sx), xs, 0.0f);
+}
+
+// Stages x (or, NORM, rmsnorm(x) * norm_w: src/ops.cpp:18-41, mean of squares
+// over the K elements, scale = 1 / sqrt(ms + eps), x * scale * w; every
+// workgroup normalises its own copy) into LDS as limbs plus block constants.
+// Loads are issued kBatch rounds (of blockDim / 4 blocks) at a time, so a long
+// x pays the load latency once per batch.  Ends with the workgroup barrier
+// that makes the limbs visible.
+constexpr int kBatch = 3;
+
+template <int QT, bool COHERENT>
+__device__ __forceinline__ void load_batch(__amdgpu_buffer_rsrc_t rs, int g, int per, int nb, int sub,
+                                           float (&v)[kBatch][8]) {
+#pragma unroll
+    for (int r = 0; r < kBatch; ++r)
+        if (g + r * per < nb) load8<QT, COHERENT>(rs, g + r * per, sub, v[r]);
+}
+
 template <int QT, bool COHERENT = false, bool NORM = false>
-__device__ __forceinline__ void stage_x(const float* __restrict__ x, int K, int nb,
-                                        float4* __restrict__ xs4, float2* __restrict__ cb,
-                                        const float* __restrict__ norm_w = nullptr, float norm_eps = 0.0f) {
-    if (COHERENT) {
-        constexpr int kAgentScope = 16;  // sc1 cache policy
-        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<float*>(x), static_cast<short>(0), K * 4, 0x00020000);
-        const int n4 = nb * (kQK / 4);
-        const int k4 = K / 4;
-        for (int i = threadIdx.x; i < n4; i += blockDim.x) {
-            float4 v;
-            if (i < k4) {
-                v = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rs, i * 16, 0, kAgentScope));
-            } else {
-                v.x = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, i * 16, 0, kAgentScope));
-                v.y = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, i * 16 + 4, 0, kAgentScope));
-                v.z = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, i * 16 + 8, 0, kAgentScope));
-                v.w = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, i * 16 + 12, 0, kAgentScope));
-            }
-            xs4[i] = v;
+__device__ __forceinline__ void stage_x(const float* __restrict__ x, int K, int nb, uint32_t* __restrict__ xl,
+                                        float4* __restrict__ xc, const float* __restrict__ norm_w = nullptr,
+                                        float norm_eps = 0.0f) {
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(x), static_cast<short>(0), K * 4, 0x00020000);
+    const int per = static_cast<int>(blockDim.x >> 2);
+    const int sub = threadIdx.x & 3;
+    const int g0 = static_cast<int>(threadIdx.x >> 2);
+    const int step = kBatch * per;
+    float v[kBatch][8];
+    float scale = 1.0f;
+    if (NORM) {
+        float ss = 0.0f;
+        for (int g = g0; g < nb; g += step) {
+            load_batch<QT, COHERENT>(rs, g, per, nb, sub, v);
+#pragma unroll
+            for (int r = 0; r < kBatch; ++r)
+                if (g + r * per < nb)
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) ss += v[r][i] * v[r][i];
         }
-        __syncthreads();
+        scale = 1.0f / sqrtf(workgroup_sum(ss) / static_cast<float>(K) + norm_eps);
     }
-    for (int g0 = 0; g0 < nb; g0 += blockDim.x) {
-        const int g = NORM ? min(static_cast<int>(threadIdx.x), nb - 1) : g0 + static_cast<int>(threadIdx.x);
-        if (!NORM && g >= nb) break;
-        float v[32];
-        const int k0 = g * kQK;
-        if (COHERENT) {
-            const float4* rb = xs4 + g * 8;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const float4 f = rb[i];
-                v[4 * i] = f.x;
-                v[4 * i + 1] = f.y;
-                v[4 * i + 2] = f.z;
-                v[4 * i + 3] = f.w;
-            }
-        } else if (k0 + kQK <= K && (reinterpret_cast<uintptr_t>(x + k0) & 15u) == 0) {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const f32x4_t fv = ((g_f4*)(x + k0))[i];
-                const float4 f = make_float4(fv.x, fv.y, fv.z, fv.w);
-                v[4 * i] = f.x;
-                v[4 * i + 1] = f.y;
-                v[4 * i + 2] = f.z;
-                v[4 * i + 3] = f.w;
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < 32; ++i) v[i] = (k0 + i < K) ? as_global(x)[k0 + i] : 0.0f;
-        }
+    for (int g = g0; g < nb; g += step) {
+        // With NORM and one batch the values loaded for the sum are reused.
+        if (!NORM || nb > step) load_batch<QT, COHERENT>(rs, g, per, nb, sub, v);
         if (NORM) {
-            float w[32];
-            if (k0 + kQK <= K && (reinterpret_cast<uintptr_t>(norm_w + k0) & 15u) == 0) {
+            const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<float*>(norm_w), static_cast<short>(0), K * 4, 0x00020000);
+            float w[kBatch][8];
+            load_batch<QT, false>(rw, g, per, nb, sub, w);
 #pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const f32x4_t fv = ((g_f4*)(norm_w + k0))[i];
-                    w[4 * i] = fv.x;
-                    w[4 * i + 1] = fv.y;
-                    w[4 * i + 2] = fv.z;
-                    w[4 * i + 3] = fv.w;
-                }
-            } else {
+            for (int r = 0; r < kBatch; ++r)
 #pragma unroll
-                for (int i = 0; i < 32; ++i) w[i] = (k0 + i < K) ? as_global(norm_w)[k0 + i] : 0.0f;
-            }
-            // Squares of this thread's block (a repeated last block counts 0).
-            float ss = 0.0f;
-            if (static_cast<int>(threadIdx.x) < nb) {
-#pragma unroll
-                for (int i = 0; i < 32; ++i) ss += v[i] * v[i];
-            }
-            __shared__ float part[16];
-#pragma unroll
-            for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
-            if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
-            __syncthreads();
-            float t = part[0];
-            for (int i = 1; i < static_cast<int>(blockDim.x >> 6); ++i) t += part[i];
-            const float scale = 1.0f / sqrtf(t / static_cast<float>(K) + norm_eps);
-#pragma unroll
-            for (int i = 0; i < 32; ++i) v[i] = v[i] * scale * w[i];
-            if (static_cast<int>(threadIdx.x) >= nb) break;
+                for (int i = 0; i < 8; ++i) v[r][i] = v[r][i] * scale * w[r][i];
         }
-        float X = 0.0f;
-        float S = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 32; i += 4) X += (v[i] + v[i + 1]) + (v[i + 2] + v[i + 3]);
-        if (QT != 1) {
-#pragma unroll
-            for (int i = 16; i < 32; ++i) v[i] *= 0.0625f;
-#pragma unroll
-            for (int i = 0; i < 32; i += 4) S += (v[i] + v[i + 1]) + (v[i + 2] + v[i + 3]);
-        }
-        const int p = g >> 1;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int slot = ((g & 1) << 3) + j;
-            xs4[p * 16 + (slot ^ (p & 15))] = make_float4(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
-        }
-        float2 c;
-        if (QT == 1) {
-            c.x = 1152.0f * X;
-            c.y = 0.0f;
-        } else if (QT == 2) {
-            c.x = 1024.0f * S + 8.0f * X;
-            c.y = 0.0f;
-        } else {
-            c.x = 1024.0f * S;
-            c.y = X;
-        }
-        cb[g] = c;
+        for (int r = 0; r < kBatch; ++r)
+            if (g + r * per < nb) emit_block<QT>(g + r * per, sub, v[r], xl, xc);
     }
+    __syncthreads();
 }
 
-__device__ __forceinline__ void load_xv(const float4* __restrict__ xs4, int p, float (&xv)[64]) {
+// A lane's x for pair p: its 16 L limb dwords and the two blocks' constants.
+template <int QT>
+__device__ __forceinline__ void load_xq(const uint32_t* __restrict__ xl, const float4* __restrict__ xc, int p,
+                                        uint32_t (&xq)[XLimbs<QT>::PAIR_DW], float4& c0, float4& c1) {
+    constexpr int Q = XLimbs<QT>::PAIR_DW / 4;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        const float4 v = xs4[p * 16 + (i ^ (p & 15))];
-        xv[4 * i] = v.x;
-        xv[4 * i + 1] = v.y;
-        xv[4 * i + 2] = v.z;
-        xv[4 * i + 3] = v.w;
+    for (int q = 0; q < Q; ++q) {
+        const uint4 v = *reinterpret_cast<const uint4*>(xl + x_slot<QT>(p, 4 * q));
+        xq[4 * q] = v.x;
+        xq[4 * q + 1] = v.y;
+        xq[4 * q + 2] = v.z;
+        xq[4 * q + 3] = v.w;
     }
+    c0 = xc[2 * p];
+    c1 = xc[2 * p + 1];
 }
 
-// Bit patterns the nibble expansion needs, held in VGPRs: gfx9 VOP3 encodings
-// take no literal, so only register operands let (d & mask) | magic issue as a
-// single v_and_or_b32.  The empty asm makes the values opaque to the compiler,
-// which would otherwise rematerialise them as literals of two VOP2 ops.
-struct NibConsts {
-    uint32_t lo;     // 0x000F000F: low nibbles of bytes 0 and 2
-    uint32_t hi;     // 0x00F000F0: high nibbles of bytes 0 and 2, in place
-    uint32_t magic;  // 0x64006400
-    __device__ __forceinline__ static NibConsts make() {
-        NibConsts c{0x000F000Fu, 0x00F000F0u, kF16Magic2};
-        asm volatile("" : "+v"(c.lo), "+v"(c.hi), "+v"(c.magic));
-        return c;
-    }
-};
+__device__ __forceinline__ int block_c(const float4& c) { return __builtin_bit_cast(int, c.y); }
 
-// One dword of Q4 nibbles: bytes hold qs[j0..j3] of one block (low nibble =
-// element j, high nibble = element j + 16, src/quant.cpp:259, 442-447).
-template <int J0, int J1, int J2, int J3, int BASE>
-__device__ __forceinline__ float nib_dot(uint32_t d, const float* xv, float a, const NibConsts& k) {
-    const uint32_t lo02 = (d & k.lo) | k.magic;
-    const uint32_t hi02 = (d & k.hi) | k.magic;
-    const uint32_t d8 = d >> 8;
-    const uint32_t lo13 = (d8 & k.lo) | k.magic;
-    const uint32_t hi13 = (d8 & k.hi) | k.magic;
-    a = __builtin_fmaf(h_lo(lo02), xv[BASE + J0], a);
-    a = __builtin_fmaf(h_hi(lo02), xv[BASE + J2], a);
-    a = __builtin_fmaf(h_lo(hi02), xv[BASE + J0 + 16], a);
-    a = __builtin_fmaf(h_hi(hi02), xv[BASE + J2 + 16], a);
-    a = __builtin_fmaf(h_lo(lo13), xv[BASE + J1], a);
-    a = __builtin_fmaf(h_hi(lo13), xv[BASE + J3], a);
-    a = __builtin_fmaf(h_lo(hi13), xv[BASE + J1 + 16], a);
-    a = __builtin_fmaf(h_hi(hi13), xv[BASE + J3 + 16], a);
-    return a;
-}
-
-// One dword of Q8_0 bytes qs[j0..j3].
-template <int J0, int J1, int J2, int J3, int BASE>
-__device__ __forceinline__ float byte_dot(uint32_t d, const float* xv, float a) {
-    const uint32_t dx = d ^ 0x80808080u;
-    const uint32_t p01 = __builtin_amdgcn_perm(kF16MagicB, dx, 0x04010400u);
-    const uint32_t p23 = __builtin_amdgcn_perm(kF16MagicB, dx, 0x04030402u);
-    a = __builtin_fmaf(h_lo(p01), xv[BASE + J0], a);
-    a = __builtin_fmaf(h_hi(p01), xv[BASE + J1], a);
-    a = __builtin_fmaf(h_lo(p23), xv[BASE + J2], a);
-    a = __builtin_fmaf(h_hi(p23), xv[BASE + J3], a);
-    return a;
-}
-
-// acc += contribution of one pair (two blocks) of one row; each block is
-// summed as two interleaved chains.
+// acc += contribution of one pair (two blocks) of one row.
 template <int QT> struct PairDot;
 
+// One Q4 block: qs dwords q[0..3], x dwords xb[0..15] (limb 0 then limb 1,
+// each low / high nibble alternating); returns the exact 256 H + L.
+__device__ __forceinline__ int q4_block(const uint32_t (&q)[4], const uint32_t* xb, int start) {
+    int h = 0, l = start;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t a = q[j] & 0x0F0F0F0Fu;
+        const uint32_t b = (q[j] >> 4) & 0x0F0F0F0Fu;
+        h = dot4(a, xb[2 * j], h);
+        l = dot4(a, xb[8 + 2 * j], l);
+        h = dot4(b, xb[2 * j + 1], h);
+        l = dot4(b, xb[8 + 2 * j + 1], l);
+    }
+    return h * 256 + l;
+}
+
 template <> struct PairDot<2> {  // Q4_0: w0 = {d0, qs0[0..1]}, w4 = {qs0[14..15], d1}
-    __device__ __forceinline__ static float run(const uint32_t* w, const float* xv, float2 c0,
-                                                float2 c1, float acc, const NibConsts& k) {
-        const uint32_t t = __builtin_amdgcn_perm(w[4], w[0], 0x05040302u);  // qs0[0,1,14,15]
-        float a0 = -c0.x, a1 = 0.0f, b0 = -c1.x, b1 = 0.0f;
-        a0 = nib_dot<0, 1, 14, 15, 0>(t, xv, a0, k);
-        a1 = nib_dot<2, 3, 4, 5, 0>(w[1], xv, a1, k);
-        b0 = nib_dot<0, 1, 2, 3, 32>(w[5], xv, b0, k);
-        b1 = nib_dot<4, 5, 6, 7, 32>(w[6], xv, b1, k);
-        a0 = nib_dot<6, 7, 8, 9, 0>(w[2], xv, a0, k);
-        a1 = nib_dot<10, 11, 12, 13, 0>(w[3], xv, a1, k);
-        b0 = nib_dot<8, 9, 10, 11, 32>(w[7], xv, b0, k);
-        b1 = nib_dot<12, 13, 14, 15, 32>(w[8], xv, b1, k);
-        acc = __builtin_fmaf(h_lo(w[0]), a0 + a1, acc);
-        acc = __builtin_fmaf(h_hi(w[4]), b0 + b1, acc);
+    __device__ __forceinline__ static float run(const uint32_t* w, const uint32_t (&xq)[32], const float4& c0,
+                                                const float4& c1, float acc) {
+        const uint32_t q0[4] = {__builtin_amdgcn_perm(w[4], w[0], 0x05040302u), w[1], w[2], w[3]};  // qs0[0,1,14,15]
+        const uint32_t q1[4] = {w[5], w[6], w[7], w[8]};
+        const int t0 = q4_block(q0, xq, block_c(c0));
+        const int t1 = q4_block(q1, xq + 16, block_c(c1));
+        acc = __builtin_fmaf(h_lo(w[0]), c0.x * static_cast<float>(t0), acc);
+        acc = __builtin_fmaf(h_hi(w[4]), c1.x * static_cast<float>(t1), acc);
         return acc;
     }
 };
 
 template <> struct PairDot<3> {  // Q4_1: w0 = {d0, m0}, w5 = {d1, m1}
-    __device__ __forceinline__ static float run(const uint32_t* w, const float* xv, float2 c0,
-                                                float2 c1, float acc, const NibConsts& k) {
-        float a0 = -c0.x, a1 = 0.0f, b0 = -c1.x, b1 = 0.0f;
-        a0 = nib_dot<0, 1, 2, 3, 0>(w[1], xv, a0, k);
-        a1 = nib_dot<4, 5, 6, 7, 0>(w[2], xv, a1, k);
-        b0 = nib_dot<0, 1, 2, 3, 32>(w[6], xv, b0, k);
-        b1 = nib_dot<4, 5, 6, 7, 32>(w[7], xv, b1, k);
-        a0 = nib_dot<8, 9, 10, 11, 0>(w[3], xv, a0, k);
-        a1 = nib_dot<12, 13, 14, 15, 0>(w[4], xv, a1, k);
-        b0 = nib_dot<8, 9, 10, 11, 32>(w[8], xv, b0, k);
-        b1 = nib_dot<12, 13, 14, 15, 32>(w[9], xv, b1, k);
-        acc = __builtin_fmaf(h_lo(w[0]), a0 + a1, acc);
-        acc = __builtin_fmaf(h_hi(w[0]), c0.y, acc);
-        acc = __builtin_fmaf(h_lo(w[5]), b0 + b1, acc);
-        acc = __builtin_fmaf(h_hi(w[5]), c1.y, acc);
+    __device__ __forceinline__ static float run(const uint32_t* w, const uint32_t (&xq)[32], const float4& c0,
+                                                const float4& c1, float acc) {
+        const uint32_t q0[4] = {w[1], w[2], w[3], w[4]};
+        const uint32_t q1[4] = {w[6], w[7], w[8], w[9]};
+        const int t0 = q4_block(q0, xq, 0);
+        const int t1 = q4_block(q1, xq + 16, 0);
+        acc = __builtin_fmaf(h_lo(w[0]), c0.x * static_cast<float>(t0), acc);
+        acc = __builtin_fmaf(h_hi(w[0]), c0.z, acc);
+        acc = __builtin_fmaf(h_lo(w[5]), c1.x * static_cast<float>(t1), acc);
+        acc = __builtin_fmaf(h_hi(w[5]), c1.z, acc);
         return acc;
     }
 };
 
 template <> struct PairDot<1> {  // Q8_0: w0 = {d0, qs0[0..1]}, w8 = {qs0[30..31], d1}
-    __device__ __forceinline__ static float run(const uint32_t* w, const float* xv, float2 c0,
-                                                float2 c1, float acc, const NibConsts&) {
-        const uint32_t t = __builtin_amdgcn_perm(w[8], w[0], 0x05040302u);  // qs0[0,1,30,31]
-        float a0 = -c0.x, a1 = 0.0f, b0 = -c1.x, b1 = 0.0f;
-        a0 = byte_dot<0, 1, 30, 31, 0>(t, xv, a0);
-        a1 = byte_dot<2, 3, 4, 5, 0>(w[1], xv, a1);
-        b0 = byte_dot<0, 1, 2, 3, 32>(w[9], xv, b0);
-        b1 = byte_dot<4, 5, 6, 7, 32>(w[10], xv, b1);
-        a0 = byte_dot<6, 7, 8, 9, 0>(w[2], xv, a0);
-        a1 = byte_dot<10, 11, 12, 13, 0>(w[3], xv, a1);
-        b0 = byte_dot<8, 9, 10, 11, 32>(w[11], xv, b0);
-        b1 = byte_dot<12, 13, 14, 15, 32>(w[12], xv, b1);
-        a0 = byte_dot<14, 15, 16, 17, 0>(w[4], xv, a0);
-        a1 = byte_dot<18, 19, 20, 21, 0>(w[5], xv, a1);
-        b0 = byte_dot<16, 17, 18, 19, 32>(w[13], xv, b0);
-        b1 = byte_dot<20, 21, 22, 23, 32>(w[14], xv, b1);
-        a0 = byte_dot<22, 23, 24, 25, 0>(w[6], xv, a0);
-        a1 = byte_dot<26, 27, 28, 29, 0>(w[7], xv, a1);
-        b0 = byte_dot<24, 25, 26, 27, 32>(w[15], xv, b0);
-        b1 = byte_dot<28, 29, 30, 31, 32>(w[16], xv, b1);
-        acc = __builtin_fmaf(h_lo(w[0]), a0 + a1, acc);
-        acc = __builtin_fmaf(h_hi(w[8]), b0 + b1, acc);
+    // One block: qs dwords q[0..7] (signed bytes), x dwords xb[0..23]
+    // (limbs hi, mid, lo); returns sum q X in f32 (|sum| < 2^34, so the
+    // limbs' partial sums are combined in f32).
+    __device__ __forceinline__ static float block(const uint32_t (&q)[8], const uint32_t* xb) {
+        int h = 0, md = 0, l = 0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            h = dot4(q[j], xb[j], h);
+            md = dot4(q[j], xb[8 + j], md);
+            l = dot4(q[j], xb[16 + j], l);
+        }
+        return __builtin_fmaf(65536.0f, static_cast<float>(h), static_cast<float>(md * 256 + l));
+    }
+    __device__ __forceinline__ static float run(const uint32_t* w, const uint32_t (&xq)[48], const float4& c0,
+                                                const float4& c1, float acc) {
+        const uint32_t q0[8] = {__builtin_amdgcn_perm(w[8], w[0], 0x05040302u), w[1], w[2], w[3], w[4], w[5], w[6], w[7]};
+        const uint32_t q1[8] = {w[9], w[10], w[11], w[12], w[13], w[14], w[15], w[16]};
+        const float t0 = block(q0, xq);
+        const float t1 = block(q1, xq + 24);
+        acc = __builtin_fmaf(h_lo(w[0]), c0.x * t0, acc);
+        acc = __builtin_fmaf(h_hi(w[8]), c1.x * t1, acc);
         return acc;
     }
 };
 
 // Sum over each aligned group of LPR lanes with DPP adds (VALU only).  The
 // total is complete in the group's last lane (in every lane for LPR <= 16).
-#define MLQ_DPP_F32(x, ctrl, rmask) \
-    __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, (x)), (ctrl), (rmask), 0xF, false))
 template <int LPR>
 __device__ __forceinline__ float group_sum(float v) {
     v += MLQ_DPP_F32(v, 0xB1, 0xF);    // quad_perm [1,0,3,2]

@@ -1064,7 +1064,7 @@ int mlq_hip_sequence_create(const mlq_linear_call* calls, int n, const int* stag
     for (int s = 0; s < seq->nstages; ++s) {
         const mlq_weight_s* w0 = calls[stage_first[s]].w;
         const int lpr = mlq::sequence_lpr(w0->K);
-        const int lds = mlq::sequence_stage_lds_bytes(w0->K);
+        const int lds = mlq::sequence_stage_lds_bytes(w0->qtype, w0->K);
         bool extend = !seq->segs.empty() && mode != MLQ_SEQ_PER_STAGE;
         if (extend) {
             const auto& last = seq->segs.back();

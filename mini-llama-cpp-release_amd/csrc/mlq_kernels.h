@@ -137,7 +137,7 @@ struct SeqSync {
 
 bool sequence_supported(int qtype, int K);
 int sequence_lpr(int K);                 // lane-group width for rows of K elements: 16 or 64
-int sequence_stage_lds_bytes(int K);     // x area of a stage (the result area comes on top)
+int sequence_stage_lds_bytes(int qtype, int K);  // x area of a stage
 hipError_t sequence_grid(int qtype, int lpr, int lds_bytes, int device, int* grid);
 hipError_t launch_sequence(int qtype, int lpr, const SeqStageDesc* stages, int nstages, SeqSync* sync,
                            int grid, int lds_bytes, unsigned spin_limit, hipStream_t stream);

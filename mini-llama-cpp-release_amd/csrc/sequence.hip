@@ -171,7 +171,6 @@ __global__ __launch_bounds__(kWaves * 64, SeqOcc<QT>::waves_per_simd) void gemv_
     const int pl = lane % LPR;
     const int gw = blockIdx.x * kWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int GW = gridDim.x * kWaves;
-    const NibConsts nk = NibConsts::make();
     bool gave_up = false;
 
     // The ring holds units 0 .. D-1 of stage `ws` (the next stage with items
@@ -203,14 +202,13 @@ __global__ __launch_bounds__(kWaves * 64, SeqOcc<QT>::waves_per_simd) void gemv_
             }
         }
         const int np = S.np;
-        float4* xs4 = lds4;
-        float2* cb = reinterpret_cast<float2*>(lds4 + np * 16);
+        uint32_t* xl = reinterpret_cast<uint32_t*>(lds4);
+        float4* xc = reinterpret_cast<float4*>(xl + np * XLimbs<QT>::PAIR_DW);
         if (S.coherent) {
-            stage_x<QT, true>(S.x, S.K, S.nb, xs4, cb);
+            stage_x<QT, true>(S.x, S.K, S.nb, xl, xc);
         } else {
-            stage_x<QT, false>(S.x, S.K, S.nb, xs4, cb);
+            stage_x<QT, false>(S.x, S.K, S.nb, xl, xc);
         }
-        __syncthreads();
 
         if (ws == s) {
             // Units of this wave: items gw, gw + GW, ... (< items), nch chunks each.
@@ -231,13 +229,12 @@ __global__ __launch_bounds__(kWaves * 64, SeqOcc<QT>::waves_per_simd) void gemv_
             if (S.nch == 1) {
                 // Rows of one chunk: every item of the stage uses the same x pair.
                 const int pp = min(pl, np - 1);
-                float xv[64];
-                load_xv(xs4, pp, xv);
-                const float2 c0 = cb[2 * pp];
-                const float2 c1 = cb[2 * pp + 1];
+                uint32_t xq[XLimbs<QT>::PAIR_DW];
+                float4 c0, c1;
+                load_xq<QT>(xl, xc, pp, xq, c0, c1);
                 const bool active = pl < np;
                 auto step = [&](uint32_t (&w)[DW]) {
-                    const float acc = active ? PairDot<QT>::run(w, xv, c0, c1, 0.0f, nk) : 0.0f;
+                    const float acc = active ? PairDot<QT>::run(w, xq, c0, c1, 0.0f) : 0.0f;
                     seq_load<QT, LPR>(S, pit, 0, slot, pl, w);  // past the end: clamped, unused
                     pit += GW;
                     seq_store_row(S, min(it * SUB + slot, S.rows - 1), seq_bcast<LPR>(group_sum<LPR>(acc)));
@@ -256,11 +253,10 @@ __global__ __launch_bounds__(kWaves * 64, SeqOcc<QT>::waves_per_simd) void gemv_
                 auto step = [&](uint32_t (&w)[DW]) {
                     const int p = c * LPR + pl;
                     const int pp = min(p, np - 1);
-                    float xv[64];
-                    load_xv(xs4, pp, xv);
-                    const float2 c0 = cb[2 * pp];
-                    const float2 c1 = cb[2 * pp + 1];
-                    const float a = PairDot<QT>::run(w, xv, c0, c1, acc, nk);
+                    uint32_t xq[XLimbs<QT>::PAIR_DW];
+                    float4 c0, c1;
+                    load_xq<QT>(xl, xc, pp, xq, c0, c1);
+                    const float a = PairDot<QT>::run(w, xq, c0, c1, acc);
                     acc = p < np ? a : acc;
                     seq_load<QT, LPR>(S, pit, pc, slot, pl, w);  // past the end: clamped, unused
                     if (++pc == S.nch) {
@@ -333,7 +329,7 @@ const void* seq_kernel(int qtype, int lpr) {
 
 bool sequence_supported(int qtype, int K) {
     const int nb = (K + kQK - 1) / kQK;
-    return (qtype >= 1 && qtype <= 3) && nb % 2 == 0 && pair_lds_bytes(nb) <= kMaxPairLdsBytes;
+    return (qtype >= 1 && qtype <= 3) && nb % 2 == 0 && pair_lds_bytes(qtype, nb) <= kMaxPairLdsBytes;
 }
 
 int sequence_lpr(int K) {
@@ -349,7 +345,7 @@ int sequence_lpr(int K) {
     return 16;
 }
 
-int sequence_stage_lds_bytes(int K) { return pair_lds_bytes((K + kQK - 1) / kQK); }
+int sequence_stage_lds_bytes(int qtype, int K) { return pair_lds_bytes(qtype, (K + kQK - 1) / kQK); }
 
 hipError_t sequence_grid(int qtype, int lpr, int lds_bytes, int device, int* grid) {
     const void* k = seq_kernel(qtype, lpr);
