@@ -19,9 +19,9 @@
 //  * Every lane requests its first W pair(s) before staging x, so the W
 //    latency overlaps the staging and the barrier.
 //  * "single" kernel (row of at most LPR pairs): each lane keeps its pair's
-//    x limbs in VGPRs and the workgroups are persistent (at most ~2 per CU),
-//    walking row groups with the next group's W requested before the current
-//    one is computed.  "multi" kernel (longer rows): one row group per wave,
+//    x limbs in VGPRs and the workgroups are persistent (one per CU), each
+//    wave walking its row groups with a ring of the next 2-3 groups' W
+//    requests in flight.  "multi" kernel (longer rows): one row group per wave,
 //    x read from LDS per pair, next pair's W requested before the current one
 //    is computed.
 //  * Row sums are reduced across the slot's lanes with DPP adds (quad_perm,
@@ -84,6 +84,34 @@ __device__ __forceinline__ float* group_y(const GemvGroup& g, int row, int M, in
     }
     return y + static_cast<size_t>(b) * (re - rb) + (row - rb);
 }
+
+// The call of a group that holds row `row`, kept in scalar registers by a
+// wave that visits rows in increasing order: the lookup runs only when a row
+// passes the current call's end.  y is the call's y of batch row b.
+struct CallCursor {
+    const uint32_t* w;
+    float* y;
+    int rb, re;  // the call's launch rows [rb, re)
+    __device__ __forceinline__ void seek(const GemvGroup& g, int M, int b, int row) {
+        const void* W = g.W[0];
+        float* Y = g.y[0];
+        int r0 = 0;
+        int r1 = g.ncalls > 1 ? g.row_begin[1] : M;
+#pragma unroll
+        for (int j = 1; j < kGroupMaxCalls; ++j) {
+            if (j < g.ncalls && row >= g.row_begin[j]) {
+                W = g.W[j];
+                Y = g.y[j];
+                r0 = g.row_begin[j];
+                r1 = j + 1 < g.ncalls ? g.row_begin[j + 1] : M;
+            }
+        }
+        w = static_cast<const uint32_t*>(W);
+        y = Y + static_cast<size_t>(b) * (r1 - r0);
+        rb = r0;
+        re = r1;
+    }
+};
 
 template <int R, int DW>
 __device__ __forceinline__ void load_rows(const GemvGroup& g, size_t row_dw, int row0, int M, int p,
@@ -153,17 +181,23 @@ template <int MODE> struct Mode {
     static constexpr bool acc = MODE == kModeAcc;
 };
 
-// Waves per SIMD the single kernel's registers are bounded for: four (two
-// workgroups per CU) except Q8_0 with two rows per slot, whose 2 x 17 pair
-// dwords in flight do not fit 128 VGPRs without spilling.
-template <int QT, int R> struct SingleOcc { static constexpr int waves_per_simd = (QT == 1 && R == 2) ? 2 : 4; };
+// Row groups in flight per wave in the single kernel (its register ring).
+// One workgroup of 8 waves per CU (2 waves per SIMD, up to 256 VGPRs) with a
+// deep ring measured faster on MI355X than two workgroups per CU with one
+// group in flight: x is staged half as often and more weight bytes are in
+// flight per CU.
+template <int QT> struct SingleDepth { static constexpr int D = QT == 1 ? 2 : 3; };
 
-// Rows of at most LPR pairs: x in VGPRs, persistent over row groups.
-template <int QT, int LPR, int R, int WAVES, int MODE>
-__global__ __launch_bounds__(WAVES * 64, (SingleOcc<QT, R>::waves_per_simd)) void gemv_single_kernel(
-    const GemvGroup g, const float* __restrict__ x, int M, int K, int nb, int groups) {
+// Rows of at most LPR pairs: x in VGPRs, persistent over row groups.  Wave w
+// takes groups w, w + W, ... (W waves in the grid), group i being rows
+// i * SUB + slot; its ring slot k holds groups k, k + D, k + 2D, ... of the
+// wave: a slot is computed, then refilled in place with the group D ahead.
+template <int QT, int LPR, int WAVES, int MODE>
+__global__ __launch_bounds__(WAVES * 64, 2) void gemv_single_kernel(const GemvGroup g, const float* __restrict__ x,
+                                                                   int M, int K, int nb, int groups) {
     constexpr int DW = Fmt<QT>::DW;
     constexpr int SUB = 64 / LPR;
+    constexpr int D = SingleDepth<QT>::D;
     extern __shared__ float4 lds4[];
     const int np = nb >> 1;
     uint32_t* xl = reinterpret_cast<uint32_t*>(lds4);
@@ -177,64 +211,77 @@ __global__ __launch_bounds__(WAVES * 64, (SingleOcc<QT, R>::waves_per_simd)) voi
     const int p = active ? pl : 0;
     const size_t row_dw = static_cast<size_t>(np) * DW;
     const int gstride = gridDim.x * WAVES;
-    int gi = blockIdx.x * WAVES + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g0 = blockIdx.x * WAVES + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nu = g0 < groups ? (groups - g0 + gstride - 1) / gstride : 0;  // groups of this wave
 
     // Every weight request is unconditional (a group past the end re-reads the
     // last one; its result is dropped): a guarded request makes the compiler
     // wait for it right away, which serialises the prefetch.
     constexpr bool PICK = Mode<MODE>::pick;
     constexpr bool ACC = Mode<MODE>::acc;
-    uint32_t wc[R][DW];
-    float rc[R];  // accumulate mode: the residual of the rows, requested with their weights
-    load_rows<R, DW>(g, row_dw, min(gi, groups - 1) * (SUB * R) + slot * R, M, p, wc);
-    if (ACC) {
+    uint32_t wq[D][DW];
+    float rq[D];  // accumulate mode: the residual of the slot's row, requested with its weights
+    // Units are requested (rq_cur) and stored (st_cur) in increasing row order.
+    CallCursor rq_cur, st_cur;
+    rq_cur.seek(g, M, blockIdx.y, 0);
+    st_cur = rq_cur;
+    auto request = [&](int gi, uint32_t (&w)[DW], float& r) {
+        const int r0 = min(gi, groups - 1) * SUB;
+        if (r0 >= rq_cur.re) rq_cur.seek(g, M, blockIdx.y, r0);
+        const uint32_t* src;
+        const float* res;
+        if (r0 + SUB <= rq_cur.re) {  // the unit's rows lie in one call
+            src = rq_cur.w + static_cast<size_t>(r0 + slot - rq_cur.rb) * row_dw;
+            res = rq_cur.y + (r0 + slot - rq_cur.rb);
+        } else {
+            const int row = min(r0 + slot, M - 1);
+            src = group_row(g, row, row_dw);
+            res = group_y(g, row, M, blockIdx.y);
+        }
+        src += static_cast<size_t>(p) * DW;
 #pragma unroll
-        for (int r = 0; r < R; ++r)
-            rc[r] = *group_y(g, min(min(gi, groups - 1) * (SUB * R) + slot * R + r, M - 1), M, blockIdx.y);
-    }
-    stage_x<QT, false, Mode<MODE>::norm>(x, K, nb, xl, xc, g.norm_w, g.norm_eps);
+        for (int i = 0; i < DW; ++i) w[i] = src[i];
+        if (ACC) r = *res;
+    };
+    stage_x<QT, false, Mode<MODE>::norm>(x, K, nb, xl, xc, g.norm_w, g.norm_eps, [&] {
+#pragma unroll
+        for (int k = 0; k < D; ++k) request(g0 + k * gstride, wq[k], rq[k]);
+    });
     uint32_t xq[XLimbs<QT>::PAIR_DW];
     float4 c0, c1;
     load_xq<QT>(xl, xc, p, xq, c0, c1);
     const bool store_y = !PICK || g.y[0] != nullptr;
     unsigned long long best = 0;
 
-    for (; gi < groups; gi += gstride) {
-        uint32_t wn[R][DW];
-        float rn[R];
-        const int gn = min(gi + gstride, groups - 1);
-        load_rows<R, DW>(g, row_dw, gn * (SUB * R) + slot * R, M, p, wn);
-        if (ACC) {
-#pragma unroll
-            for (int r = 0; r < R; ++r) rn[r] = *group_y(g, min(gn * (SUB * R) + slot * R + r, M - 1), M, blockIdx.y);
-        }
-        __builtin_amdgcn_sched_barrier(0);  // the request stays ahead of this group's compute
-        float acc[R];
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            acc[r] = active ? PairDot<QT>::run(wc[r], xq, c0, c1, 0.0f) : 0.0f;
-            acc[r] = group_sum<LPR>(acc[r]);
-        }
-        if (pl == LPR - 1) {
-            const int row0 = gi * (SUB * R) + slot * R;
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                if (row0 + r < M) {
-                    if (store_y) *group_y(g, row0 + r, M, blockIdx.y) = ACC ? rc[r] + acc[r] : acc[r];
-                    if (PICK) {
-                        const unsigned long long k = pick_key(acc[r], row0 + r);
-                        best = k > best ? k : best;
-                    }
-                }
+    int gi = g0;
+    auto step = [&](uint32_t (&w)[DW], float& r) {
+        const float v = PairDot<QT>::run(w, xq, c0, c1, 0.0f);  // inactive lanes hold pair 0: dropped
+        const float res = r;
+        request(gi + D * gstride, w, r);
+        const float acc = group_sum<LPR>(active ? v : 0.0f);
+        const int r0 = gi * SUB;
+        const int row = r0 + slot;
+        if (r0 >= st_cur.re && r0 < M) st_cur.seek(g, M, blockIdx.y, r0);
+        if (pl == LPR - 1 && row < M) {
+            if (store_y) {
+                float* yp = r0 + SUB <= st_cur.re ? st_cur.y + (row - st_cur.rb) : group_y(g, row, M, blockIdx.y);
+                *yp = ACC ? res + acc : acc;
+            }
+            if (PICK) {
+                const unsigned long long k = pick_key(acc, row);
+                best = k > best ? k : best;
             }
         }
+        gi += gstride;
+    };
+    int u = 0;
+    for (; u + D <= nu; u += D) {
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-#pragma unroll
-            for (int i = 0; i < DW; ++i) wc[r][i] = wn[r][i];
-            if (ACC) rc[r] = rn[r];
-        }
+        for (int k = 0; k < D; ++k) step(wq[k], rq[k]);
     }
+#pragma unroll
+    for (int k = 0; k < D; ++k)
+        if (u + k < nu) step(wq[k], rq[k]);
     if (PICK) pick_finish<WAVES>(g.pick, g.token, best);
 }
 
@@ -263,13 +310,14 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_multi_kernel(
     constexpr bool ACC = Mode<MODE>::acc;
     const int nch = (np + LPR - 1) / LPR;
     uint32_t wc[R][DW];
-    load_rows<R, DW>(g, row_dw, row0, M, min(pl, np - 1), wc);
     float res[R];  // accumulate mode: the rows' residual, requested up front
-    if (ACC) {
+    stage_x<QT, false, Mode<MODE>::norm>(x, K, nb, xl, xc, g.norm_w, g.norm_eps, [&] {
+        load_rows<R, DW>(g, row_dw, row0, M, min(pl, np - 1), wc);
+        if (ACC) {
 #pragma unroll
-        for (int r = 0; r < R; ++r) res[r] = *group_y(g, min(row0 + r, M - 1), M, blockIdx.y);
-    }
-    stage_x<QT, false, Mode<MODE>::norm>(x, K, nb, xl, xc, g.norm_w, g.norm_eps);
+            for (int r = 0; r < R; ++r) res[r] = *group_y(g, min(row0 + r, M - 1), M, blockIdx.y);
+        }
+    });
     float acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = 0.0f;
@@ -386,29 +434,28 @@ enum class Kind { Single, Multi, Generic };
 struct PairCfg {
     Kind kind;
     int lpr;
-    int r;
 };
 
 PairCfg choose_pair(const LinearShape& s) {
-    if (s.nb % 2 != 0 || pair_lds_bytes(s.qtype, s.nb) > kMaxPairLdsBytes) return PairCfg{Kind::Generic, 64, 1};
+    if (s.nb % 2 != 0 || pair_lds_bytes(s.qtype, s.nb) > kMaxPairLdsBytes) return PairCfg{Kind::Generic, 64};
     const int np = s.nb / 2;
-    if (np <= 16) return PairCfg{Kind::Single, 16, 1};
-    if (np <= 64) return PairCfg{Kind::Single, 64, s.M <= 8192 ? 2 : 1};
+    if (np <= 16) return PairCfg{Kind::Single, 16};
+    if (np <= 64) return PairCfg{Kind::Single, 64};
     // Longer rows: the widest lane group whose last sweep leaves <= 12.5% idle.
     for (int lpr : {64, 32, 16}) {
         const int iters = (np + lpr - 1) / lpr;
-        if (static_cast<double>(np) / (static_cast<double>(lpr) * iters) >= 0.875) return PairCfg{Kind::Multi, lpr, 1};
+        if (static_cast<double>(np) / (static_cast<double>(lpr) * iters) >= 0.875) return PairCfg{Kind::Multi, lpr};
     }
-    return PairCfg{Kind::Multi, 16, 1};
+    return PairCfg{Kind::Multi, 16};
 }
 
-template <int QT, int LPR, int R, int MODE>
+template <int QT, int LPR, int MODE>
 hipError_t launch_single_t(const LinearShape& s, const GemvGroup& g, const float* x, hipStream_t stream) {
-    constexpr int rows_per_group = (64 / LPR) * R;
+    constexpr int rows_per_group = 64 / LPR;
     const int groups = (s.M + rows_per_group - 1) / rows_per_group;
     int grid = (groups + kWaves - 1) / kWaves;
     if (grid > kPersistentWgs) grid = kPersistentWgs;
-    hipLaunchKernelGGL((gemv_single_kernel<QT, LPR, R, kWaves, MODE>), dim3(grid, s.rows), dim3(kWaves * 64),
+    hipLaunchKernelGGL((gemv_single_kernel<QT, LPR, kWaves, MODE>), dim3(grid, s.rows), dim3(kWaves * 64),
                        pair_lds_bytes(QT, s.nb), stream, g, x, s.M, s.K, s.nb, groups);
     return hipGetLastError();
 }
@@ -426,9 +473,8 @@ template <int QT, int MODE>
 hipError_t launch_q(const LinearShape& s, const PairCfg& c, const GemvGroup& g, const float* x,
                     hipStream_t stream) {
     if (c.kind == Kind::Single) {
-        if (c.lpr == 16) return launch_single_t<QT, 16, 1, MODE>(s, g, x, stream);
-        if (c.r == 2) return launch_single_t<QT, 64, 2, MODE>(s, g, x, stream);
-        return launch_single_t<QT, 64, 1, MODE>(s, g, x, stream);
+        if (c.lpr == 16) return launch_single_t<QT, 16, MODE>(s, g, x, stream);
+        return launch_single_t<QT, 64, MODE>(s, g, x, stream);
     }
     if (c.kind == Kind::Multi) {
         if (c.lpr == 64) return launch_multi_t<QT, 64, MODE>(s, g, x, stream);
@@ -507,7 +553,7 @@ const char* gemv_kernel_name(const LinearShape& s) {
     const char* fmt = s.qtype == 1 ? "q8_0" : s.qtype == 2 ? "q4_0" : "q4_1";
     const PairCfg c = choose_pair(s);
     if (c.kind == Kind::Single) {
-        snprintf(buf, sizeof buf, "gemv_single_%s_lpr%d_r%d", fmt, c.lpr, c.r);
+        snprintf(buf, sizeof buf, "gemv_single_%s_lpr%d", fmt, c.lpr);
     } else if (c.kind == Kind::Multi) {
         snprintf(buf, sizeof buf, "gemv_multi_%s_lpr%d", fmt, c.lpr);
     } else {

@@ -64,7 +64,7 @@ __device__ __forceinline__ g_f32* as_global(const float* p) { return (g_f32*)p; 
 
 constexpr int kMaxPairLdsBytes = 64 * 1024;
 constexpr int kWaves = 8;             // waves per workgroup
-constexpr int kPersistentWgs = 512;   // ~2 workgroups per CU on a 256-CU MI355X
+constexpr int kPersistentWgs = 256;   // one workgroup per CU on a 256-CU MI355X
 
 // LDS of the pair kernels: the x limbs (64 L bytes per pair) and 16 bytes of
 // constants per block.
@@ -240,38 +240,65 @@ __device__ __forceinline__ void load_batch(__amdgpu_buffer_rsrc_t rs, int g, int
         if (g + r * per < nb) load8<QT, COHERENT>(rs, g + r * per, sub, v[r]);
 }
 
-template <int QT, bool COHERENT = false, bool NORM = false>
+struct NoRequests {
+    __device__ __forceinline__ void operator()() const {}
+};
+
+// The first batch's x (and norm_w) loads are issued before `after_loads()`
+// runs, so a kernel can request its weights there: the x loads, older in the
+// in-order load counter, are then waited for without waiting for the weights.
+template <int QT, bool COHERENT = false, bool NORM = false, typename F = NoRequests>
 __device__ __forceinline__ void stage_x(const float* __restrict__ x, int K, int nb, uint32_t* __restrict__ xl,
                                         float4* __restrict__ xc, const float* __restrict__ norm_w = nullptr,
-                                        float norm_eps = 0.0f) {
+                                        float norm_eps = 0.0f, F&& after_loads = F{}) {
     const __amdgpu_buffer_rsrc_t rs =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(x), static_cast<short>(0), K * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(NORM ? norm_w : x), static_cast<short>(0), K * 4, 0x00020000);
     const int per = static_cast<int>(blockDim.x >> 2);
     const int sub = threadIdx.x & 3;
     const int g0 = static_cast<int>(threadIdx.x >> 2);
     const int step = kBatch * per;
     float v[kBatch][8];
-    float scale = 1.0f;
-    if (NORM) {
-        float ss = 0.0f;
+    float w[kBatch][8];
+    if (!NORM && __is_same(F, NoRequests)) {  // nothing to interleave: one loop over the batches
         for (int g = g0; g < nb; g += step) {
             load_batch<QT, COHERENT>(rs, g, per, nb, sub, v);
 #pragma unroll
             for (int r = 0; r < kBatch; ++r)
+                if (g + r * per < nb) emit_block<QT>(g + r * per, sub, v[r], xl, xc);
+        }
+        __syncthreads();
+        return;
+    }
+    load_batch<QT, COHERENT>(rs, g0, per, nb, sub, v);
+    if (NORM) load_batch<QT, false>(rw, g0, per, nb, sub, w);
+    after_loads();
+    float scale = 1.0f;
+    if (NORM) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int r = 0; r < kBatch; ++r)
+            if (g0 + r * per < nb)
+#pragma unroll
+                for (int i = 0; i < 8; ++i) ss += v[r][i] * v[r][i];
+        for (int g = g0 + step; g < nb; g += step) {
+            float t[kBatch][8];
+            load_batch<QT, COHERENT>(rs, g, per, nb, sub, t);
+#pragma unroll
+            for (int r = 0; r < kBatch; ++r)
                 if (g + r * per < nb)
 #pragma unroll
-                    for (int i = 0; i < 8; ++i) ss += v[r][i] * v[r][i];
+                    for (int i = 0; i < 8; ++i) ss += t[r][i] * t[r][i];
         }
         scale = 1.0f / sqrtf(workgroup_sum(ss) / static_cast<float>(K) + norm_eps);
     }
     for (int g = g0; g < nb; g += step) {
-        // With NORM and one batch the values loaded for the sum are reused.
-        if (!NORM || nb > step) load_batch<QT, COHERENT>(rs, g, per, nb, sub, v);
+        if (g != g0) {
+            load_batch<QT, COHERENT>(rs, g, per, nb, sub, v);
+            if (NORM) load_batch<QT, false>(rw, g, per, nb, sub, w);
+        }
         if (NORM) {
-            const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
-                const_cast<float*>(norm_w), static_cast<short>(0), K * 4, 0x00020000);
-            float w[kBatch][8];
-            load_batch<QT, false>(rw, g, per, nb, sub, w);
 #pragma unroll
             for (int r = 0; r < kBatch; ++r)
 #pragma unroll

@@ -62,10 +62,10 @@ def test_host_side_validation_without_gpu():
 
 def test_kernel_selection_names():
     # decode shapes of the benchmark take the pair kernel; odd block counts the generic one
-    assert mlq_hip.kernel_name(mlq_hip.Q4_0, 1, 4096, 4096) == "gemv_single_q4_0_lpr64_r2"
-    assert mlq_hip.kernel_name(mlq_hip.Q4_0, 1, 32000, 4096) == "gemv_single_q4_0_lpr64_r1"
+    assert mlq_hip.kernel_name(mlq_hip.Q4_0, 1, 4096, 4096) == "gemv_single_q4_0_lpr64"
+    assert mlq_hip.kernel_name(mlq_hip.Q4_0, 1, 32000, 4096) == "gemv_single_q4_0_lpr64"
     assert mlq_hip.kernel_name(mlq_hip.Q8_0, 1, 4096, 11008) == "gemv_multi_q8_0_lpr64"
     assert mlq_hip.kernel_name(mlq_hip.Q4_0, 1, 896, 4864) == "gemv_multi_q4_0_lpr16"
-    assert mlq_hip.kernel_name(mlq_hip.Q4_1, 1, 151936, 896) == "gemv_single_q4_1_lpr16_r1"
+    assert mlq_hip.kernel_name(mlq_hip.Q4_1, 1, 151936, 896) == "gemv_single_q4_1_lpr16"
     assert mlq_hip.kernel_name(mlq_hip.Q4_0, 1, 5, 13) == "gemv_generic_q4_0"
     assert mlq_hip.kernel_name(mlq_hip.Q4_0, 64, 4096, 4096).startswith("gemm_mfma_q4_0")
