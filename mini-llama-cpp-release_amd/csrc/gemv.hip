@@ -113,18 +113,6 @@ struct CallCursor {
     }
 };
 
-template <int R, int DW>
-__device__ __forceinline__ void load_rows(const GemvGroup& g, size_t row_dw, int row0, int M, int p,
-                                          uint32_t (&w)[R][DW]) {
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const int row = min(row0 + r, M - 1);  // rows past M compute on row M-1 and are dropped
-        const uint32_t* src = group_row(g, row, row_dw) + static_cast<size_t>(p) * DW;
-#pragma unroll
-        for (int i = 0; i < DW; ++i) w[r][i] = src[i];
-    }
-}
-
 // Folds every lane's key into the launch's result; called once by every
 // thread of every workgroup.  The workgroup's best key goes to its group slot
 // with one atomic max, then the workgroup arrives; the last arrival of the
@@ -285,10 +273,16 @@ __global__ __launch_bounds__(WAVES * 64, 2) void gemv_single_kernel(const GemvGr
     if (PICK) pick_finish<WAVES>(g.pick, g.token, best);
 }
 
-// Rows of more than LPR pairs: one row group per wave, x from LDS per pair.
-template <int QT, int LPR, int R, int WAVES, int MODE>
-__global__ __launch_bounds__(WAVES * 64) void gemv_multi_kernel(
-    const GemvGroup g, const float* __restrict__ x, int M, int K, int nb) {
+// Rows of more than LPR pairs: x from LDS per pair.  Wave w takes row items
+// w, w + W, ... (W waves in the grid; item i being rows i * SUB + slot), each
+// walked in chunks c = 0 .. nch-1 (pair c * LPR + pl of every lane; lanes past
+// the row keep their sum).  A ring of D units (item, chunk) of weight requests
+// is in flight per wave, refilled in place.  Workgroup size, grid cap and D
+// come from MI355X measurements (launch_multi_t).
+
+template <int QT, int LPR, int WAVES, int D, int MODE>
+__global__ __launch_bounds__(WAVES * 64) void gemv_multi_kernel(const GemvGroup g, const float* __restrict__ x,
+                                                               int M, int K, int nb, int items) {
     constexpr int DW = Fmt<QT>::DW;
     constexpr int SUB = 64 / LPR;
     extern __shared__ float4 lds4[];
@@ -300,61 +294,90 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_multi_kernel(
     const int lane = threadIdx.x & 63;
     const int slot = lane / LPR;
     const int pl = lane % LPR;
-    const int row0 = (blockIdx.x * WAVES + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) * (SUB * R) + slot * R;
     const size_t row_dw = static_cast<size_t>(np) * DW;
+    const int GW = gridDim.x * WAVES;
+    const int gw = blockIdx.x * WAVES + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nch = (np + LPR - 1) / LPR;
+    const int nit = gw < items ? (items - gw + GW - 1) / GW : 0;
+    const int nu = nit * nch;
 
-    // Chunks c = 0 .. nch-1 (pair c * LPR + pl of every lane) in a uniform loop;
-    // lanes past the row keep their sum.  Requests are unconditional (past the
-    // row: re-read the last pair) so the prefetch is never waited for early.
+    // Requests are unconditional (past the row: the last pair; past the
+    // items: the last item) so the prefetch is never waited for early.
     constexpr bool PICK = Mode<MODE>::pick;
     constexpr bool ACC = Mode<MODE>::acc;
-    const int nch = (np + LPR - 1) / LPR;
-    uint32_t wc[R][DW];
-    float res[R];  // accumulate mode: the rows' residual, requested up front
-    stage_x<QT, false, Mode<MODE>::norm>(x, K, nb, xl, xc, g.norm_w, g.norm_eps, [&] {
-        load_rows<R, DW>(g, row_dw, row0, M, min(pl, np - 1), wc);
-        if (ACC) {
-#pragma unroll
-            for (int r = 0; r < R; ++r) res[r] = *group_y(g, min(row0 + r, M - 1), M, blockIdx.y);
+    uint32_t wq[D][DW];
+    float rq[D];  // accumulate mode: the residual of the unit's row
+    CallCursor rq_cur, st_cur;
+    rq_cur.seek(g, M, blockIdx.y, 0);
+    st_cur = rq_cur;
+    int pit = gw, pc = 0;  // the next unit to request
+    auto request = [&](uint32_t (&w)[DW], float& r) {
+        const int r0 = min(pit, items - 1) * SUB;
+        if (r0 >= rq_cur.re) rq_cur.seek(g, M, blockIdx.y, r0);
+        const uint32_t* src;
+        const float* res;
+        if (r0 + SUB <= rq_cur.re) {
+            src = rq_cur.w + static_cast<size_t>(r0 + slot - rq_cur.rb) * row_dw;
+            res = rq_cur.y + (r0 + slot - rq_cur.rb);
+        } else {
+            const int row = min(r0 + slot, M - 1);
+            src = group_row(g, row, row_dw);
+            res = group_y(g, row, M, blockIdx.y);
         }
-    });
-    float acc[R];
+        src += static_cast<size_t>(min(pc * LPR + pl, np - 1)) * DW;
 #pragma unroll
-    for (int r = 0; r < R; ++r) acc[r] = 0.0f;
-    for (int c = 0; c < nch; ++c) {
+        for (int i = 0; i < DW; ++i) w[i] = src[i];
+        if (ACC) r = *res;
+        if (++pc == nch) {
+            pc = 0;
+            pit += GW;
+        }
+    };
+    stage_x<QT, false, Mode<MODE>::norm>(x, K, nb, xl, xc, g.norm_w, g.norm_eps, [&] {
+#pragma unroll
+        for (int k = 0; k < D; ++k) request(wq[k], rq[k]);
+    });
+    const bool store_y = !PICK || g.y[0] != nullptr;
+    unsigned long long best = 0;
+    int it = gw, c = 0;
+    float acc = 0.0f;
+    auto step = [&](uint32_t (&w)[DW], float& r) {
         const int p = c * LPR + pl;
-        const int pc = min(p, np - 1);
-        uint32_t wn[R][DW];
-        load_rows<R, DW>(g, row_dw, row0, M, min(p + LPR, np - 1), wn);
-        __builtin_amdgcn_sched_barrier(0);  // the request stays ahead of this chunk's compute
         uint32_t xq[XLimbs<QT>::PAIR_DW];
         float4 c0, c1;
-        load_xq<QT>(xl, xc, pc, xq, c0, c1);
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const float a = PairDot<QT>::run(wc[r], xq, c0, c1, acc[r]);
-            acc[r] = p < np ? a : acc[r];
-        }
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-#pragma unroll
-            for (int i = 0; i < DW; ++i) wc[r][i] = wn[r][i];
-    }
-#pragma unroll
-    for (int r = 0; r < R; ++r) acc[r] = group_sum<LPR>(acc[r]);
-    unsigned long long best = 0;
-    if (pl == LPR - 1) {
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            if (row0 + r < M) {
-                if (!PICK || g.y[0] != nullptr) *group_y(g, row0 + r, M, blockIdx.y) = ACC ? res[r] + acc[r] : acc[r];
+        load_xq<QT>(xl, xc, min(p, np - 1), xq, c0, c1);
+        const float a = PairDot<QT>::run(w, xq, c0, c1, acc);
+        acc = p < np ? a : acc;
+        const float res = r;
+        request(w, r);
+        if (++c == nch) {
+            const float t = group_sum<LPR>(acc);
+            const int r0 = it * SUB;
+            const int row = r0 + slot;
+            if (r0 >= st_cur.re && r0 < M) st_cur.seek(g, M, blockIdx.y, r0);
+            if (pl == LPR - 1 && row < M) {
+                if (store_y) {
+                    float* yp = r0 + SUB <= st_cur.re ? st_cur.y + (row - st_cur.rb) : group_y(g, row, M, blockIdx.y);
+                    *yp = ACC ? res + t : t;
+                }
                 if (PICK) {
-                    const unsigned long long k = pick_key(acc[r], row0 + r);
+                    const unsigned long long k = pick_key(t, row);
                     best = k > best ? k : best;
                 }
             }
+            acc = 0.0f;
+            c = 0;
+            it += GW;
         }
+    };
+    int u = 0;
+    for (; u + D <= nu; u += D) {
+#pragma unroll
+        for (int k = 0; k < D; ++k) step(wq[k], rq[k]);
     }
+#pragma unroll
+    for (int k = 0; k < D; ++k)
+        if (u + k < nu) step(wq[k], rq[k]);
     if (PICK) pick_finish<WAVES>(g.pick, g.token, best);
 }
 
@@ -462,11 +485,21 @@ hipError_t launch_single_t(const LinearShape& s, const GemvGroup& g, const float
 
 template <int QT, int LPR, int MODE>
 hipError_t launch_multi_t(const LinearShape& s, const GemvGroup& g, const float* x, hipStream_t stream) {
-    constexpr int rows_per_wg = kWaves * (64 / LPR);
-    dim3 grid((s.M + rows_per_wg - 1) / rows_per_wg, s.rows);
-    hipLaunchKernelGGL((gemv_multi_kernel<QT, LPR, 1, kWaves, MODE>), grid, dim3(kWaves * 64), pair_lds_bytes(QT, s.nb),
-                       stream, g, x, s.M, s.K, s.nb);
-    return hipGetLastError();
+    constexpr int sub = 64 / LPR;
+    const int items = (s.M + sub - 1) / sub;
+    auto go = [&](auto kernel, int waves, int cap) {
+        int grid = (items + waves - 1) / waves;
+        if (grid > cap) grid = cap;
+        hipLaunchKernelGGL(kernel, dim3(grid, s.rows), dim3(waves * 64), pair_lds_bytes(QT, s.nb), stream, g, x, s.M,
+                           s.K, s.nb, items);
+        return hipGetLastError();
+    };
+    // Few rows: small workgroups spread over more CUs, two units in flight.
+    // Many rows: Q4 one persistent 16-wave workgroup per CU (x staged once
+    // per CU), Q8_0 8-wave workgroups with one item per wave.
+    if (items < 2048) return go(gemv_multi_kernel<QT, LPR, 4, 2, MODE>, 4, 1 << 20);
+    if (QT == 1) return go(gemv_multi_kernel<QT, LPR, 8, 1, MODE>, 8, 1 << 20);
+    return go(gemv_multi_kernel<QT, LPR, 16, 1, MODE>, 16, kPersistentWgs);
 }
 
 template <int QT, int MODE>
