@@ -231,7 +231,8 @@ __global__ __launch_bounds__(WAVES * 64, 2) void gemv_single_kernel(const GemvGr
         for (int i = 0; i < DW; ++i) w[i] = src[i];
         if (ACC) r = *res;
     };
-    stage_x<QT, false, Mode<MODE>::norm>(x, K, nb, xl, xc, g.norm_w, g.norm_eps, [&] {
+    // nb <= 2 * 64 pairs <= blockDim / 4: one round of x loads
+    stage_x<QT, false, Mode<MODE>::norm, 1>(x, K, nb, xl, xc, g.norm_w, g.norm_eps, [&] {
 #pragma unroll
         for (int k = 0; k < D; ++k) request(g0 + k * gstride, wq[k], rq[k]);
     });
@@ -333,7 +334,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_multi_kernel(const GemvGroup 
             pit += GW;
         }
     };
-    stage_x<QT, false, Mode<MODE>::norm>(x, K, nb, xl, xc, g.norm_w, g.norm_eps, [&] {
+    stage_x_fit<QT, false, Mode<MODE>::norm>(x, K, nb, xl, xc, g.norm_w, g.norm_eps, [&] {
 #pragma unroll
         for (int k = 0; k < D; ++k) request(wq[k], rq[k]);
     });

@@ -232,12 +232,14 @@ __device__ __forceinline__ void emit_block(int g, int sub, const float (&v)[8], 
 // that makes the limbs visible.
 constexpr int kBatch = 3;
 
-template <int QT, bool COHERENT>
+// Rounds past the last block re-read the last block (unused): a load under a
+// branch makes the compiler wait for it at the branch's end, which would
+// serialise the x loads with the weight requests that follow them.
+template <int QT, bool COHERENT, int B>
 __device__ __forceinline__ void load_batch(__amdgpu_buffer_rsrc_t rs, int g, int per, int nb, int sub,
-                                           float (&v)[kBatch][8]) {
+                                           float (&v)[B][8]) {
 #pragma unroll
-    for (int r = 0; r < kBatch; ++r)
-        if (g + r * per < nb) load8<QT, COHERENT>(rs, g + r * per, sub, v[r]);
+    for (int r = 0; r < B; ++r) load8<QT, COHERENT>(rs, min(g + r * per, nb - 1), sub, v[r]);
 }
 
 struct NoRequests {
@@ -247,7 +249,8 @@ struct NoRequests {
 // The first batch's x (and norm_w) loads are issued before `after_loads()`
 // runs, so a kernel can request its weights there: the x loads, older in the
 // in-order load counter, are then waited for without waiting for the weights.
-template <int QT, bool COHERENT = false, bool NORM = false, typename F = NoRequests>
+// B: rounds per batch (1 when the caller knows nb <= blockDim / 4).
+template <int QT, bool COHERENT = false, bool NORM = false, int B = kBatch, typename F = NoRequests>
 __device__ __forceinline__ void stage_x(const float* __restrict__ x, int K, int nb, uint32_t* __restrict__ xl,
                                         float4* __restrict__ xc, const float* __restrict__ norm_w = nullptr,
                                         float norm_eps = 0.0f, F&& after_loads = F{}) {
@@ -258,35 +261,35 @@ __device__ __forceinline__ void stage_x(const float* __restrict__ x, int K, int 
     const int per = static_cast<int>(blockDim.x >> 2);
     const int sub = threadIdx.x & 3;
     const int g0 = static_cast<int>(threadIdx.x >> 2);
-    const int step = kBatch * per;
-    float v[kBatch][8];
-    float w[kBatch][8];
+    const int step = B * per;
+    float v[B][8];
+    float w[B][8];
     if (!NORM && __is_same(F, NoRequests)) {  // nothing to interleave: one loop over the batches
         for (int g = g0; g < nb; g += step) {
-            load_batch<QT, COHERENT>(rs, g, per, nb, sub, v);
+            load_batch<QT, COHERENT, B>(rs, g, per, nb, sub, v);
 #pragma unroll
-            for (int r = 0; r < kBatch; ++r)
+            for (int r = 0; r < B; ++r)
                 if (g + r * per < nb) emit_block<QT>(g + r * per, sub, v[r], xl, xc);
         }
         __syncthreads();
         return;
     }
-    load_batch<QT, COHERENT>(rs, g0, per, nb, sub, v);
-    if (NORM) load_batch<QT, false>(rw, g0, per, nb, sub, w);
+    load_batch<QT, COHERENT, B>(rs, g0, per, nb, sub, v);
+    if (NORM) load_batch<QT, false, B>(rw, g0, per, nb, sub, w);
     after_loads();
     float scale = 1.0f;
     if (NORM) {
         float ss = 0.0f;
 #pragma unroll
-        for (int r = 0; r < kBatch; ++r)
+        for (int r = 0; r < B; ++r)
             if (g0 + r * per < nb)
 #pragma unroll
                 for (int i = 0; i < 8; ++i) ss += v[r][i] * v[r][i];
         for (int g = g0 + step; g < nb; g += step) {
-            float t[kBatch][8];
-            load_batch<QT, COHERENT>(rs, g, per, nb, sub, t);
+            float t[B][8];
+            load_batch<QT, COHERENT, B>(rs, g, per, nb, sub, t);
 #pragma unroll
-            for (int r = 0; r < kBatch; ++r)
+            for (int r = 0; r < B; ++r)
                 if (g + r * per < nb)
 #pragma unroll
                     for (int i = 0; i < 8; ++i) ss += t[r][i] * t[r][i];
@@ -295,20 +298,36 @@ __device__ __forceinline__ void stage_x(const float* __restrict__ x, int K, int 
     }
     for (int g = g0; g < nb; g += step) {
         if (g != g0) {
-            load_batch<QT, COHERENT>(rs, g, per, nb, sub, v);
-            if (NORM) load_batch<QT, false>(rw, g, per, nb, sub, w);
+            load_batch<QT, COHERENT, B>(rs, g, per, nb, sub, v);
+            if (NORM) load_batch<QT, false, B>(rw, g, per, nb, sub, w);
         }
         if (NORM) {
 #pragma unroll
-            for (int r = 0; r < kBatch; ++r)
+            for (int r = 0; r < B; ++r)
 #pragma unroll
                 for (int i = 0; i < 8; ++i) v[r][i] = v[r][i] * scale * w[r][i];
         }
 #pragma unroll
-        for (int r = 0; r < kBatch; ++r)
+        for (int r = 0; r < B; ++r)
             if (g + r * per < nb) emit_block<QT>(g + r * per, sub, v[r], xl, xc);
     }
     __syncthreads();
+}
+
+// stage_x with as many load rounds per batch as the row needs (up to
+// kBatch): a round past the last block only re-reads it.
+template <int QT, bool COHERENT = false, bool NORM = false, typename F = NoRequests>
+__device__ __forceinline__ void stage_x_fit(const float* __restrict__ x, int K, int nb, uint32_t* __restrict__ xl,
+                                            float4* __restrict__ xc, const float* __restrict__ norm_w = nullptr,
+                                            float norm_eps = 0.0f, F&& after_loads = F{}) {
+    const int per = static_cast<int>(blockDim.x >> 2);
+    if (nb <= per) {
+        stage_x<QT, COHERENT, NORM, 1>(x, K, nb, xl, xc, norm_w, norm_eps, after_loads);
+    } else if (nb <= 2 * per) {
+        stage_x<QT, COHERENT, NORM, 2>(x, K, nb, xl, xc, norm_w, norm_eps, after_loads);
+    } else {
+        stage_x<QT, COHERENT, NORM, kBatch>(x, K, nb, xl, xc, norm_w, norm_eps, after_loads);
+    }
 }
 
 // A lane's x for pair p: its 16 L limb dwords and the two blocks' constants.

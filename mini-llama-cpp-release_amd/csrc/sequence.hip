@@ -205,9 +205,9 @@ __global__ __launch_bounds__(kWaves * 64, SeqOcc<QT>::waves_per_simd) void gemv_
         uint32_t* xl = reinterpret_cast<uint32_t*>(lds4);
         float4* xc = reinterpret_cast<float4*>(xl + np * XLimbs<QT>::PAIR_DW);
         if (S.coherent) {
-            stage_x<QT, true>(S.x, S.K, S.nb, xl, xc);
+            stage_x_fit<QT, true>(S.x, S.K, S.nb, xl, xc);
         } else {
-            stage_x<QT, false>(S.x, S.K, S.nb, xl, xc);
+            stage_x_fit<QT, false>(S.x, S.K, S.nb, xl, xc);
         }
 
         if (ws == s) {
