@@ -180,12 +180,11 @@ template <int QT> struct SingleDepth { static constexpr int D = QT == 1 ? 2 : 3;
 // takes groups w, w + W, ... (W waves in the grid), group i being rows
 // i * SUB + slot; its ring slot k holds groups k, k + D, k + 2D, ... of the
 // wave: a slot is computed, then refilled in place with the group D ahead.
-template <int QT, int LPR, int WAVES, int MODE>
+template <int QT, int LPR, int WAVES, int D, int MODE>
 __global__ __launch_bounds__(WAVES * 64, 2) void gemv_single_kernel(const GemvGroup g, const float* __restrict__ x,
                                                                    int M, int K, int nb, int groups) {
     constexpr int DW = Fmt<QT>::DW;
     constexpr int SUB = 64 / LPR;
-    constexpr int D = SingleDepth<QT>::D;
     extern __shared__ float4 lds4[];
     const int np = nb >> 1;
     uint32_t* xl = reinterpret_cast<uint32_t*>(lds4);
@@ -479,7 +478,7 @@ hipError_t launch_single_t(const LinearShape& s, const GemvGroup& g, const float
     const int groups = (s.M + rows_per_group - 1) / rows_per_group;
     int grid = (groups + kWaves - 1) / kWaves;
     if (grid > kPersistentWgs) grid = kPersistentWgs;
-    hipLaunchKernelGGL((gemv_single_kernel<QT, LPR, kWaves, MODE>), dim3(grid, s.rows), dim3(kWaves * 64),
+    hipLaunchKernelGGL((gemv_single_kernel<QT, LPR, kWaves, SingleDepth<QT>::D, MODE>), dim3(grid, s.rows), dim3(kWaves * 64),
                        pair_lds_bytes(QT, s.nb), stream, g, x, s.M, s.K, s.nb, groups);
     return hipGetLastError();
 }

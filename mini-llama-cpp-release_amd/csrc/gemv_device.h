@@ -174,8 +174,10 @@ __device__ __forceinline__ void emit_block(int g, int sub, const float (&v)[8], 
     // non-finite.
     const float k = m < 0x1p-100f ? 0x1p64f : 1.0f;
     const float mk = m * k;
-    const float inv = mk > 0.0f && mk <= 3.4e38f ? RANGE / mk : 0.0f;
-    const float s = (mk / RANGE) / k;
+    // 1 / s_b to within an ulp or two: s_b * inv = 1 + O(2^-22), far below
+    // x's own representation error (2^-16 of the block maximum).
+    const float inv = mk > 0.0f && mk <= 3.4e38f ? RANGE * __builtin_amdgcn_rcpf(mk) : 0.0f;
+    const float s = mk * (1.0f / RANGE) / k;
     uint32_t out[L][2];
     float xs = 0.0f;
 #pragma unroll
