@@ -1047,9 +1047,11 @@ void Decoder::linear_fused(hipStream_t s, const Linear* const* ws, float* const*
 }
 
 // One decode step.  Where a layer's linears are quantized, the RMSNorm is
-// done by the consuming GEMVs (norm mode, reading the residual stream x_) and
-// the residual add by the producing ones (o and down accumulate into x_):
-// per layer q/k/v -> attention -> o -> gate/up -> SwiGLU -> down.  Otherwise
+// done by the consuming GEMVs (norm mode, reading the residual stream x_),
+// the residual add by the producing ones (o and down accumulate into x_) and
+// SwiGLU by the gate/up launch (GLU mode, when gate and up share a format and
+// rows of at most 64 pairs): per layer q/k/v -> attention -> o -> gate/up +
+// SwiGLU -> down, five launches.  Otherwise
 // (F32 weights) the separate add + RMSNorm kernel runs, with `pending` the
 // residual delta it still has to add.
 void Decoder::enqueue_step(hipStream_t s, bool pick, bool advance) {
@@ -1093,16 +1095,31 @@ void Decoder::enqueue_step(hipStream_t s, bool pick, bool advance) {
         }
         const Linear* gu[2] = {&L.w_gate, &L.w_up};
         float* gu_y[2] = {gate_, up_};
-        if (pending == nullptr && quant(L.w_gate) && quant(L.w_up)) {
-            linear_fused(s, gu, gu_y, 2, x_, L.ffn_norm, false);
+        const LinearShape gu_shape{L.w_gate.qtype, L.w_gate.M, L.w_gate.K, (L.w_gate.K + 31) / 32, 1};
+        if (pending == nullptr && quant(L.w_gate) && L.w_up.qtype == L.w_gate.qtype && L.w_up.M == L.w_gate.M &&
+            L.w_up.K == L.w_gate.K && gemv_glu_supported(gu_shape)) {
+            // gate, up and SwiGLU in one launch (FFN RMSNorm staged)
+            GemvGroup g{};
+            g.W[0] = L.w_gate.data;
+            g.W[1] = L.w_up.data;
+            g.y[0] = act_;
+            g.row_begin[1] = L.w_gate.M;
+            g.ncalls = 2;
+            g.norm_w = L.ffn_norm;
+            g.norm_eps = c.rms_norm_eps;
+            check(launch_gemv_glu(gu_shape, g, x_, s), "launch_gemv_glu");
         } else {
-            launch_norm(s, pending, L.ffn_norm);
-            pending = nullptr;
-            linear_group(s, gu, gu_y, 2, h_);
+            if (pending == nullptr && quant(L.w_gate) && quant(L.w_up)) {
+                linear_fused(s, gu, gu_y, 2, x_, L.ffn_norm, false);
+            } else {
+                launch_norm(s, pending, L.ffn_norm);
+                pending = nullptr;
+                linear_group(s, gu, gu_y, 2, h_);
+            }
+            hipLaunchKernelGGL(swiglu_kernel, dim3((c.hidden_dim + 255) / 256), dim3(256), 0, s, gate_, up_, act_,
+                               c.hidden_dim);
+            check(hipGetLastError(), "swiglu_kernel");
         }
-        hipLaunchKernelGGL(swiglu_kernel, dim3((c.hidden_dim + 255) / 256), dim3(256), 0, s, gate_, up_, act_,
-                           c.hidden_dim);
-        check(hipGetLastError(), "swiglu_kernel");
         const Linear* wd[1] = {&L.w_down};
         if (quant(L.w_down)) {
             float* wd_y[1] = {x_};

@@ -80,6 +80,12 @@ hipError_t launch_gemv_pick(const LinearShape& s, const void* w, const float* x,
 //  accumulate: y += W x (the residual add; y must not overlap x).
 hipError_t launch_gemv_decode(const LinearShape& s, const GemvGroup& g, const float* x, bool norm, bool accumulate,
                               hipStream_t stream);
+// The decode step's SwiGLU: g.W[0] = gate, g.W[1] = up (s.M rows each,
+// g.row_begin[1] = s.M), rows == 1 or a batch; y[0][i] = silu(gate_i . h) *
+// (up_i . h) with h = rmsnorm(x) * g.norm_w (src/ops.cpp:72-107).  Rows of at
+// most 64 pairs only (gemv_glu_supported); hipErrorNotSupported otherwise.
+bool gemv_glu_supported(const LinearShape& s);
+hipError_t launch_gemv_glu(const LinearShape& s, const GemvGroup& g, const float* x, hipStream_t stream);
 // The greedy pick over W . (rmsnorm(x) * norm_w): the final norm and lm_head
 // of a decode step in one launch.
 hipError_t launch_gemv_pick_norm(const LinearShape& s, const void* w, const float* x, const float* norm_w,
