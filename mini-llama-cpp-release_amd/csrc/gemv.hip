@@ -247,7 +247,7 @@ __global__ __launch_bounds__(WAVES * 64, 2) void gemv_single_kernel(const GemvGr
         if (ACC) r = *res;
     };
     // nb <= 2 * 64 pairs <= blockDim / 4: one round of x loads
-    stage_x<QT, false, Mode<MODE>::norm, 1>(x, K, nb, xl, xc, g.norm_w, g.norm_eps, [&] {
+    stage_x<QT, false, Mode<MODE>::norm, 1, true>(x, K, nb, xl, xc, g.norm_w, g.norm_eps, [&] {
 #pragma unroll
         for (int k = 0; k < D; ++k) {
             if (GLU) {

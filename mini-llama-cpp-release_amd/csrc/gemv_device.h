@@ -177,7 +177,7 @@ __device__ __forceinline__ void emit_block(int g, int sub, const float (&v)[8], 
     // 1 / s_b to within an ulp or two: s_b * inv = 1 + O(2^-22), far below
     // x's own representation error (2^-16 of the block maximum).
     const float inv = mk > 0.0f && mk <= 3.4e38f ? RANGE * __builtin_amdgcn_rcpf(mk) : 0.0f;
-    const float s = mk * (1.0f / RANGE) / k;
+    const float s = mk * (1.0f / RANGE) * (m < 0x1p-100f ? 0x1p-64f : 1.0f);
     uint32_t out[L][2];
     float xs = 0.0f;
 #pragma unroll
@@ -252,7 +252,11 @@ struct NoRequests {
 // runs, so a kernel can request its weights there: the x loads, older in the
 // in-order load counter, are then waited for without waiting for the weights.
 // B: rounds per batch (1 when the caller knows nb <= blockDim / 4).
-template <int QT, bool COHERENT = false, bool NORM = false, int B = kBatch, typename F = NoRequests>
+// ONE: the caller guarantees nb <= B * blockDim / 4 (one batch): the code has
+// no loop and no load under a branch, so nothing makes the compiler wait for
+// the weight requests issued in `after_loads` before quantizing.
+template <int QT, bool COHERENT = false, bool NORM = false, int B = kBatch, bool ONE = false,
+          typename F = NoRequests>
 __device__ __forceinline__ void stage_x(const float* __restrict__ x, int K, int nb, uint32_t* __restrict__ xl,
                                         float4* __restrict__ xc, const float* __restrict__ norm_w = nullptr,
                                         float norm_eps = 0.0f, F&& after_loads = F{}) {
@@ -266,6 +270,31 @@ __device__ __forceinline__ void stage_x(const float* __restrict__ x, int K, int 
     const int step = B * per;
     float v[B][8];
     float w[B][8];
+    if (ONE) {
+        load_batch<QT, COHERENT, B>(rs, g0, per, nb, sub, v);
+        if (NORM) load_batch<QT, false, B>(rw, g0, per, nb, sub, w);
+        after_loads();
+        if (NORM) {
+            float ss = 0.0f;
+#pragma unroll
+            for (int r = 0; r < B; ++r) {
+                float t = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) t += v[r][i] * v[r][i];
+                ss += g0 + r * per < nb ? t : 0.0f;  // rounds past the last block re-read it
+            }
+            const float scale = 1.0f / sqrtf(workgroup_sum(ss) / static_cast<float>(K) + norm_eps);
+#pragma unroll
+            for (int r = 0; r < B; ++r)
+#pragma unroll
+                for (int i = 0; i < 8; ++i) v[r][i] = v[r][i] * scale * w[r][i];
+        }
+#pragma unroll
+        for (int r = 0; r < B; ++r)
+            if (g0 + r * per < nb) emit_block<QT>(g0 + r * per, sub, v[r], xl, xc);
+        __syncthreads();
+        return;
+    }
     if (!NORM && __is_same(F, NoRequests)) {  // nothing to interleave: one loop over the batches
         for (int g = g0; g < nb; g += step) {
             load_batch<QT, COHERENT, B>(rs, g, per, nb, sub, v);
@@ -324,11 +353,13 @@ __device__ __forceinline__ void stage_x_fit(const float* __restrict__ x, int K, 
                                             float norm_eps = 0.0f, F&& after_loads = F{}) {
     const int per = static_cast<int>(blockDim.x >> 2);
     if (nb <= per) {
-        stage_x<QT, COHERENT, NORM, 1>(x, K, nb, xl, xc, norm_w, norm_eps, after_loads);
+        stage_x<QT, COHERENT, NORM, 1, true>(x, K, nb, xl, xc, norm_w, norm_eps, after_loads);
     } else if (nb <= 2 * per) {
-        stage_x<QT, COHERENT, NORM, 2>(x, K, nb, xl, xc, norm_w, norm_eps, after_loads);
+        stage_x<QT, COHERENT, NORM, 2, true>(x, K, nb, xl, xc, norm_w, norm_eps, after_loads);
+    } else if (nb <= kBatch * per) {
+        stage_x<QT, COHERENT, NORM, kBatch, true>(x, K, nb, xl, xc, norm_w, norm_eps, after_loads);
     } else {
-        stage_x<QT, COHERENT, NORM, kBatch>(x, K, nb, xl, xc, norm_w, norm_eps, after_loads);
+        stage_x<QT, COHERENT, NORM, kBatch, false>(x, K, nb, xl, xc, norm_w, norm_eps, after_loads);
     }
 }
 
