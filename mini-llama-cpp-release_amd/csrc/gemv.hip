@@ -539,12 +539,13 @@ hipError_t launch_multi_t(const LinearShape& s, const GemvGroup& g, const float*
                            s.K, s.nb, items);
         return hipGetLastError();
     };
-    // Few rows: small workgroups spread over more CUs, two units in flight.
+    // Few rows: small workgroups spread over more CUs, three units in flight.
     // Many rows: Q4 one persistent 16-wave workgroup per CU (x staged once
-    // per CU), Q8_0 8-wave workgroups with one item per wave.
-    if (items < 2048) return go(gemv_multi_kernel<QT, LPR, 4, 2, MODE>, 4, 1 << 20);
+    // per CU) with two units in flight, Q8_0 8-wave workgroups with one item
+    // per wave.
+    if (items < 2048) return go(gemv_multi_kernel<QT, LPR, 4, 3, MODE>, 4, 1 << 20);
     if (QT == 1) return go(gemv_multi_kernel<QT, LPR, 8, 1, MODE>, 8, 1 << 20);
-    return go(gemv_multi_kernel<QT, LPR, 16, 1, MODE>, 16, kPersistentWgs);
+    return go(gemv_multi_kernel<QT, LPR, 16, 2, MODE>, 16, kPersistentWgs);
 }
 
 template <int QT, int MODE>
