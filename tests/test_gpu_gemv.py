@@ -81,6 +81,63 @@ def test_batched_rows(hip, orc, fmt, shape, rows):
     run_case(hip, orc, fmt, *shape, rows=rows)
 
 
+# x is held per 32-element block as an integer times the block's scale: the
+# scale must follow x over the whole f32 range (blocks below 2^-100 take a
+# second scaling step), a block of zeros and a block whose elements span 12
+# orders of magnitude must still meet the bound.  Shapes cover the single,
+# multi and generic kernels.
+@pytest.mark.parametrize("case", ["tiny_1e-33", "small_1e-20", "large_1e20", "zero_blocks", "mixed_in_block"])
+@pytest.mark.parametrize("shape", [(64, 4096), (64, 11008), (5, 13)], ids=lambda s: f"{s[0]}x{s[1]}")
+def test_x_dynamic_range(hip, orc, case, shape):
+    m, k = shape
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal(k, dtype=np.float32)
+    # Outputs are compared at unit scale (y / scale against x / scale): the
+    # reference's absolute 1e-3 criterion only has a meaning there.
+    scale = {"tiny_1e-33": 1e-33, "small_1e-20": 1e-20, "large_1e20": 1e20}.get(case, 1.0)
+    if scale != 1.0:
+        x *= np.float32(scale)
+    elif case == "zero_blocks":
+        x[: min(k, 64)] = 0.0
+        x[k // 2: k // 2 + 32] = 0.0
+    else:  # one large element per block, the rest 1e-6 of it
+        x *= np.float32(1e-6)
+        x[::32] = np.float32(1e6)
+    for fmt, qt in FMTS.items():
+        w = weights(m, k)
+        blocks = orc.quantize(qt, w, threads=THREADS)
+        want = orc.linear(qt, x, blocks, m, threads=THREADS)
+        say(f"range {case} {fmt} {m}x{k} kernel={hip.kernel_name(qt, 1, m, k)}")
+        wt = hip.Weight.upload(qt, blocks, m, k)
+        got = wt.linear_host(x)
+        wt.free()
+        assert np.isfinite(got).all() and np.isfinite(want).all(), f"{case} {fmt}: non-finite output"
+        # With 1e6-sized terms whose sum cancels to O(1), any other summation
+        # order misses the reference's unscaled 1e-3 criterion; the BASELINE
+        # bound (floor 1e-3 * ||x|| * max|d|) is the one that applies there.
+        check_close(got.astype(np.float64) / scale, want.astype(np.float64) / scale,
+                    x.astype(np.float64) / scale, qt, blocks, f"{case} {fmt} {m}x{k}",
+                    reference_bound=case != "mixed_in_block")
+
+
+@pytest.mark.parametrize("shape", [(64, 4096), (64, 11008), (5, 13)], ids=lambda s: f"{s[0]}x{s[1]}")
+def test_x_non_finite(hip, orc, shape):
+    """An Inf or NaN in x makes every output non-finite, as in the reference's
+    f32 sum (which gives Inf or NaN), without faulting."""
+    m, k = shape
+    for bad in (np.inf, -np.inf, np.nan):
+        x = np.random.default_rng(6).standard_normal(k, dtype=np.float32)
+        x[k // 3] = bad
+        for fmt, qt in FMTS.items():
+            blocks = orc.quantize(qt, weights(m, k), threads=THREADS)
+            want = orc.linear(qt, x, blocks, m, threads=THREADS)
+            wt = hip.Weight.upload(qt, blocks, m, k)
+            got = wt.linear_host(x)
+            wt.free()
+            assert not np.isfinite(want).any(), "reference output expected non-finite"
+            assert not np.isfinite(got).any(), f"{fmt} {m}x{k} x[{k // 3}]={bad}: finite outputs"
+
+
 def test_golden_vectors(hip, golden):
     """The reference's own outputs (tests/golden) reproduced by the GPU path."""
     for n in golden["names"]:
