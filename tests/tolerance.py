@@ -6,8 +6,9 @@
 * Reference criterion (tests/test_cuda_quant.cpp:23-36): abs err <= 1e-3, or
   abs err / max(1, |y_cpu|) <= 1e-3.
 Both must hold, except where a caller passes reference_bound=False: inputs
-whose products reach 1e6 and cancel to O(1) (the reference's own kernels miss
-its unscaled 1e-3 there too), where the BASELINE bound alone applies.
+whose products reach 1e6 and cancel to O(1), where fp32 rounding of any
+summation order other than the CPU's exceeds an unscaled 1e-3 and the
+BASELINE bound alone applies.
 """
 
 import numpy as np
