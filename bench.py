@@ -573,7 +573,28 @@ def main():
     ap.add_argument("--decode-steps", type=int, default=0,
                     help="with --decode-only: instead run this many single forward() steps (one launch "
                          "sequence per token, no recorded graph) on the same model, for kernel profiles")
+    ap.add_argument("--gemm-only", action="store_true",
+                    help="run only the prefill GEMM table (config 4) and print it as one JSON line")
+    ap.add_argument("--gemm-filter", default="",
+                    help="with --gemm-only: keep the configs named fmt:M:N (comma-separated, e.g. q4_0:4096:64)")
     args = ap.parse_args()
+    if args.gemm_only:
+        hip.load()
+        hip.init(0)
+        stream = hip.stream(0)
+        keep = {f for f in args.gemm_filter.split(",") if f}
+        rows = []
+        for cfg in GEMM_CONFIGS:
+            qt, m, _, n = cfg
+            if keep and f"{FMT_NAME[qt]}:{m}:{n}" not in keep:
+                continue
+            r = gemm_shape_bench(*cfg, stream)
+            log(f"  gemm {r['fmt']} {r['M']:>6}x{r['K']:<5} N={r['N']:<4} {r['us_per_call']:9.2f} us "
+                f"{r['tflops']:8.1f} TFLOP/s ({100 * r['frac_of_fp16_dense_peak']:.1f}% of fp16 peak) "
+                f"{r['gbs']:8.1f} GB/s {r['kernel']}")
+            rows.append(r)
+        print(json.dumps({"gemm": rows}), flush=True)
+        return
     if args.decode_only:
         hip.load()
         hip.init(0)

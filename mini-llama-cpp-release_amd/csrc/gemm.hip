@@ -1107,14 +1107,22 @@ hipError_t launch_q(const LinearShape& s, const GemmCfg& c, const WsLayout& l, c
     }
 }
 
-// Chunked-kernel configuration: 128 rows per workgroup, 16 tokens per
-// workgroup for batches up to 16 and 32 above; x split in the kernel for
-// batches up to 16, and up to 64 when there are few row tiles, else by
-// xsplit_kernel first (the in-kernel split is repeated by every row tile:
-// measured on MI355X, 4096 rows x 64 tokens favour it, 11008 rows do not);
-// K split until the grid is about two workgroups per CU.
+// Chunked-kernel configuration (rules from an MI355X sweep of rows per wave,
+// token tile, x split, prefetch depth and K splits at 4096x4096 and
+// 11008x4096, Q4_0 and Q8_0, N = 16 / 64 / 512):
+//  * up to 16 tokens: 64 rows (one row tile per wave) x 16 tokens per
+//    workgroup, K split until the grid is about 640 workgroups with at least
+//    4 chunks per split (fewer, longer splits beat a larger grid: the split
+//    reduction is a serial tail; short rows keep 2 chunks per split);
+//  * up to 128 tokens: 128 rows x 32 tokens, x split in the kernel;
+//  * more tokens: x split once by xsplit_kernel (the in-kernel split would be
+//    repeated by every row tile), 128 rows x 32 tokens, or x 64 tokens for
+//    Q8_0 (its 34-byte blocks gain most from fewer weight passes; Q4 measured
+//    equal or slower with the larger tile's single workgroup per CU);
+//  * from 32 tokens on, 8 chunks per split unless the tiles alone give every
+//    CU a workgroup (then no K split).
 struct ChunkCfg {
-    int tt, row_tiles, tok_tiles, splits, cps, npad;
+    int rw, tt, row_tiles, tok_tiles, splits, cps, npad;
     bool xs;
 };
 
@@ -1124,16 +1132,22 @@ bool chunk_supported(const LinearShape& s) {
 
 ChunkCfg choose_chunk(const LinearShape& s) {
     ChunkCfg c;
-    c.tt = s.rows <= 16 ? 1 : 2;
-    c.xs = s.rows > 64 || (s.rows > 16 && s.M > 8192);
-    c.row_tiles = (s.M + 127) / 128;
+    c.rw = s.rows <= 16 ? 1 : 2;
+    c.tt = s.rows <= 16 ? 1 : (s.rows > 128 && s.qtype == 1) ? 4 : 2;
+    c.xs = s.rows > 128;
+    c.row_tiles = (s.M + 64 * c.rw - 1) / (64 * c.rw);
     c.tok_tiles = (s.rows + 16 * c.tt - 1) / (16 * c.tt);
     c.npad = c.tok_tiles * 16 * c.tt;
     const long long tiles = static_cast<long long>(c.row_tiles) * c.tok_tiles;
     const int nchunks = s.nb / kChunkBlocks;
-    const long long target = 512;
-    int splits = static_cast<int>((target + tiles - 1) / tiles);
-    splits = std::max(1, std::min(splits, nchunks / 2));
+    int splits;
+    if (c.tt == 1) {
+        splits = static_cast<int>((640 + tiles - 1) / tiles);
+        splits = std::min(splits, nchunks >= 16 ? nchunks / 4 : nchunks / 2);
+    } else {
+        splits = tiles >= 256 ? 1 : nchunks / 8;
+    }
+    splits = std::max(1, splits);
     if (tiles > kGemmMaxTiles) splits = 1;
     c.cps = (nchunks + splits - 1) / splits;
     c.splits = (nchunks + c.cps - 1) / c.cps;
@@ -1154,18 +1168,18 @@ ChunkWs chunk_layout(const LinearShape& s, const ChunkCfg& c) {
     l.part = l.scale + (c.xs ? up(static_cast<size_t>(c.npad) * sizeof(float)) : 0);
     l.part_bytes = c.splits == 1 ? 0
                                  : static_cast<size_t>(c.row_tiles) * c.tok_tiles * c.splits *
-                                       (2 * c.tt * kGemmThreads * 16);
+                                       (c.rw * c.tt * kGemmThreads * 16);
     l.total = l.part + l.part_bytes;
     return l;
 }
 
 size_t chunk_workspace_bytes(const LinearShape& s) { return chunk_layout(s, choose_chunk(s)).total; }
 
-template <int QT, int TT, bool XS, int P = (TT == 1 ? 4 : 2)>
+template <int QT, int RW, int TT, bool XS, int P = (TT == 1 ? 4 : 2)>
 hipError_t launch_chunk_t(const LinearShape& s, const ChunkCfg& c, const void* w, const float* x, float* y,
                           char* ws, hipStream_t stream) {
-    constexpr int lds = ChunkLds<QT, 2, TT, XS>::bytes;
-    auto kern = gemm_chunk_kernel<QT, 2, TT, P, XS>;
+    constexpr int lds = ChunkLds<QT, RW, TT, XS>::bytes;
+    auto kern = gemm_chunk_kernel<QT, RW, TT, P, XS>;
     static bool attr = [&] {
         return hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                                    lds) == hipSuccess;
@@ -1197,9 +1211,10 @@ hipError_t launch_chunk_t(const LinearShape& s, const ChunkCfg& c, const void* w
 template <int QT>
 hipError_t launch_chunk_q(const LinearShape& s, const ChunkCfg& c, const void* w, const float* x, float* y,
                           char* ws, hipStream_t stream) {
-    if (c.tt == 1) return launch_chunk_t<QT, 1, false>(s, c, w, x, y, ws, stream);
-    if (!c.xs) return launch_chunk_t<QT, 2, false>(s, c, w, x, y, ws, stream);
-    return launch_chunk_t<QT, 2, true>(s, c, w, x, y, ws, stream);
+    if (c.tt == 1) return launch_chunk_t<QT, 1, 1, false>(s, c, w, x, y, ws, stream);
+    if (c.tt == 2 && !c.xs) return launch_chunk_t<QT, 2, 2, false>(s, c, w, x, y, ws, stream);
+    if (c.tt == 2) return launch_chunk_t<QT, 2, 2, true>(s, c, w, x, y, ws, stream);
+    return launch_chunk_t<QT, 2, 4, true>(s, c, w, x, y, ws, stream);
 }
 
 bool use_chunk(const LinearShape& s, const float* x) {
@@ -1252,8 +1267,8 @@ const char* gemm_kernel_name(const LinearShape& s) {
     const char* fmt = s.qtype == 1 ? "q8_0" : s.qtype == 2 ? "q4_0" : "q4_1";
     if (chunk_supported(s)) {
         const ChunkCfg c = choose_chunk(s);
-        snprintf(buf, sizeof buf, "gemm_mfma_%s_chunk%s_bm128_bn%d_splitk%d", fmt, c.xs ? "_xs" : "", 16 * c.tt,
-                 c.splits);
+        snprintf(buf, sizeof buf, "gemm_mfma_%s_chunk%s_bm%d_bn%d_splitk%d", fmt, c.xs ? "_xs" : "", 64 * c.rw,
+                 16 * c.tt, c.splits);
         return buf;
     }
     const GemmCfg c = choose(s);

@@ -45,7 +45,8 @@ def test_gemm_baseline_config4(hip, orc, shape, n):
 
 
 @pytest.mark.parametrize("m,k,n", [(4096, 4096, 16), (64, 64, 2), (33, 4096, 17), (300, 896, 40),
-                                   (4864, 896, 7), (17, 64, 100), (1000, 11008, 3)])
+                                   (4864, 896, 7), (17, 64, 100), (1000, 11008, 3), (520, 4096, 130),
+                                   (300, 896, 200), (200, 4096, 96)])
 def test_gemm_q4_1_and_ragged(hip, orc, m, k, n):
     for fmt, qt in FMTS.items():
         run(hip, orc, qt, m, k, n)
