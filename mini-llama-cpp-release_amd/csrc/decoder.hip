@@ -233,18 +233,43 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
     }
 }
 
+// Sum over aligned groups of LPR lanes (a power of two up to 64), in every
+// lane of the group: DPP within rows of 16, one swizzle across the two rows
+// of a 32-lane half, a shuffle across halves.
+template <int LPR>
+__device__ __forceinline__ float lane_group_sum(float v) {
+#define MLQ_ATTN_DPP(x, ctrl) \
+    __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, (x)), (ctrl), 0xF, 0xF, false))
+    if (LPR >= 2) v += MLQ_ATTN_DPP(v, 0xB1);   // quad_perm [1,0,3,2]
+    if (LPR >= 4) v += MLQ_ATTN_DPP(v, 0x4E);   // quad_perm [2,3,0,1]
+    if (LPR >= 8) v += MLQ_ATTN_DPP(v, 0x141);  // row_half_mirror: 8-lane sums
+    if (LPR >= 16) v += MLQ_ATTN_DPP(v, 0x140); // row_mirror: 16-lane sums
+#undef MLQ_ATTN_DPP
+    if (LPR >= 32) v += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
+    if (LPR >= 64) v += __shfl_xor(v, 32, 64);
+    return v;
+}
+
 // Decode attention for one query head per workgroup with the step's RoPE,
 // biases and KV-cache write folded in (head_dim = 4 * LPR, a power of two up
 // to 256).  Each workgroup rotates its q head and its kv head's k (as
 // rope_kv_kernel does), uses this position's k and v from LDS and writes them
-// to the cache when it is the first query head of its kv group; earlier
-// positions come from the cache.  A cache row is read as LPR float4s by LPR
-// lanes, ROWS = 256 / LPR rows at a time, so every load is a coalesced row
-// segment.  The softmax is folded into the same pass (running maximum, sum
-// and weighted v per row group, rescaled when the maximum grows), and the
-// row groups are merged once at the end: sum_t e^(s_t - m) v_t / sum_t
-// e^(s_t - m), the reference's softmax-then-sum to rounding.  The first
-// cache rows are requested before the RoPE math, which hides their latency.
+// to the cache; earlier positions come from the cache.  A cache row is read
+// as LPR float4s by LPR lanes, ROWS = 512 / LPR rows at a time, so every load
+// is a coalesced row segment.  The softmax is folded into the same pass
+// (running maximum, sum and weighted v per row group, rescaled when the
+// maximum grows), and the row groups are merged once at the end:
+// sum_t e^(s_t - m) v_t / sum_t e^(s_t - m), the reference's
+// softmax-then-sum to rounding.
+// Latency structure (measured with in-kernel timestamps on MI355X): q, k, v
+// are requested together with the position, the first pass's cache rows
+// right after it (before the RoPE math), and the KV-cache row is stored
+// before the first pass without being waited for -- every load and store
+// here is unconditional (clamped indices; the query heads of one kv group
+// store identical values), since a load or store inside a branch makes the
+// compiler wait for all outstanding memory operations at the join.  The
+// AHEAD rows of a pass are reduced together (DPP, no LDS round trips per
+// step) and folded into the running softmax with selects.
 template <int LPR>
 __global__ __launch_bounds__(kFlashThreads) void attention_rope_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
@@ -253,6 +278,7 @@ __global__ __launch_bounds__(kFlashThreads) void attention_rope_kernel(
     float* __restrict__ vc, float* __restrict__ out) {
     constexpr int HD = 4 * LPR;
     constexpr int ROWS = kFlashThreads / LPR;
+    constexpr int AHEAD = kFlashAhead;
     __shared__ float4 qs4[LPR], ks4[LPR], vs4[LPR];
     __shared__ float gm[ROWS], gl[ROWS];
     __shared__ float4 gacc[ROWS][LPR];
@@ -263,6 +289,28 @@ __global__ __launch_bounds__(kFlashThreads) void attention_rope_kernel(
     const int h = blockIdx.x;
     const int group = n_heads / n_kv;
     const int kvh = h / group;
+    const int half = HD / 2;
+    // Threads 0..half-1 rotate pair tid of q, threads half..HD-1 pair
+    // tid - half of k; every thread adds v's bias for element tid.  Threads
+    // past HD load the last pair / element again; an absent bias reads the
+    // value itself and adds zero.
+    const bool is_q = tid < half;
+    const int r = min(is_q ? tid : tid - half, half - 1);
+    const int i0 = neox ? r : 2 * r;
+    const int i1 = neox ? i0 + half : i0 + 1;
+    const int te = min(tid, HD - 1);
+    const float* src = is_q ? q + h * HD : k + kvh * HD;
+    const bool has_b = is_q ? bq != nullptr : bk != nullptr;
+    const float* bsrc = has_b ? (is_q ? bq + h * HD : bk + kvh * HD) : src;
+    const float* bvsrc = bv != nullptr ? bv + kvh * HD : v + kvh * HD;
+    float a0 = src[i0];
+    float a1 = src[i1];
+    float ve = v[kvh * HD + te];
+    const float b0 = bsrc[i0], b1 = bsrc[i1], bve = bvsrc[te];
+    a0 += has_b ? b0 : 0.0f;
+    a1 += has_b ? b1 : 0.0f;
+    ve += bv != nullptr ? bve : 0.0f;
+
     const int p0 = st->pos;
     const bool ok = p0 >= 0 && p0 < max_seq;
     if (!ok && h == 0 && tid == 0) st->error |= kDecodeErrPos;
@@ -274,88 +322,88 @@ __global__ __launch_bounds__(kFlashThreads) void attention_rope_kernel(
     const float* vbase = vc + layer_base + kvh * HD;
     const int lr = tid / LPR;
     const int li = tid % LPR;
-    // This row group's first kFlashAhead cache rows, requested ahead of the
-    // RoPE math (rows past the last cached one re-read it and are not used).
-    float4 kr[kFlashAhead], vr[kFlashAhead];
+    // The first pass's cache rows, requested ahead of the RoPE math (rows past
+    // the last cached one re-read it and are not used).
+    float4 kr[AHEAD], vr[AHEAD];
 #pragma unroll
-    for (int j = 0; j < kFlashAhead; ++j) {
+    for (int j = 0; j < AHEAD; ++j) {
         const int tj = min(lr + j * ROWS, last);
         kr[j] = *reinterpret_cast<const float4*>(kbase + tj * t_stride + 4 * li);
         vr[j] = *reinterpret_cast<const float4*>(vbase + tj * t_stride + 4 * li);
     }
-    const int half = HD / 2;
     if (tid < HD) {
-        // Threads 0..half-1 rotate pair tid of q, threads half..HD-1 pair
-        // tid - half of k; every thread adds v's bias for element tid.
-        const bool is_q = tid < half;
-        const int r = is_q ? tid : tid - half;
-        const int i0 = neox ? r : 2 * r;
-        const int i1 = neox ? i0 + half : i0 + 1;
         const float freq = 1.0f / powf(theta, static_cast<float>(2 * r) / static_cast<float>(HD));
         const float ang = static_cast<float>(pos) * freq;
         const float c = cosf(ang);
-        const float s = sinf(ang);
-        const float* src = is_q ? q + h * HD : k + kvh * HD;
-        const float* b = is_q ? (bq ? bq + h * HD : nullptr) : (bk ? bk + kvh * HD : nullptr);
-        float a0 = src[i0];
-        float a1 = src[i1];
-        if (b != nullptr) {
-            a0 = a0 + b[i0];
-            a1 = a1 + b[i1];
-        }
+        const float sn = sinf(ang);
         float* dst = is_q ? qs : ks;
-        dst[i0] = a0 * c - a1 * s;
-        dst[i1] = a0 * s + a1 * c;
-        vs[tid] = bv != nullptr ? v[kvh * HD + tid] + bv[kvh * HD + tid] : v[kvh * HD + tid];
+        dst[i0] = a0 * c - a1 * sn;
+        dst[i1] = a0 * sn + a1 * c;
+        vs[tid] = ve;
     }
     __syncthreads();
-    if (h % group == 0 && tid < HD) {
-        kc[layer_base + pos * t_stride + kvh * HD + tid] = ks[tid];
-        vc[layer_base + pos * t_stride + kvh * HD + tid] = vs[tid];
-    }
+    kc[layer_base + pos * t_stride + kvh * HD + te] = ks[te];
+    vc[layer_base + pos * t_stride + kvh * HD + te] = vs[te];
+
     const float4 qv = qs4[li];
+    const float4 kp = ks4[li];
+    const float4 vp = vs4[li];
     const float scale = 1.0f / sqrtf(static_cast<float>(HD));
     float m = -INFINITY;
     float l = 0.0f;
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    for (int t0 = lr; t0 <= pos; t0 += kFlashAhead * ROWS) {
-        float4 kc4[kFlashAhead], vc4[kFlashAhead];
+    auto pass = [&](int t0, const float4 (&kc4)[AHEAD], const float4 (&vc4)[AHEAD]) {
+        float dot[AHEAD];
 #pragma unroll
-        for (int j = 0; j < kFlashAhead; ++j) {
-            kc4[j] = kr[j];
-            vc4[j] = vr[j];
+        for (int j = 0; j < AHEAD; ++j) {
+            const float4 kv = t0 + j * ROWS == pos ? kp : kc4[j];
+            dot[j] = lane_group_sum<LPR>(qv.x * kv.x + qv.y * kv.y + qv.z * kv.z + qv.w * kv.w);
         }
-        // The next kFlashAhead rows, requested before these are used -- only
-        // when another pass follows: requests left outstanding at the loop's
-        // end would be waited for at the merge's barrier.
-        if (t0 + kFlashAhead * ROWS <= pos) {
+        // Rows past pos (clamped re-reads, or at pos 0 a cache row not yet
+        // written) are selected away before any arithmetic touches them.
 #pragma unroll
-            for (int j = 0; j < kFlashAhead; ++j) {
-                const int tj = min(t0 + (kFlashAhead + j) * ROWS, last);
-                kr[j] = *reinterpret_cast<const float4*>(kbase + tj * t_stride + 4 * li);
-                vr[j] = *reinterpret_cast<const float4*>(vbase + tj * t_stride + 4 * li);
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < kFlashAhead; ++j) {
+        for (int j = 0; j < AHEAD; ++j) {
             const int t = t0 + j * ROWS;
-            const float4 kv = t == pos ? ks4[li] : kc4[j];
-            const float4 vv = t == pos ? vs4[li] : vc4[j];
-            float dot = qv.x * kv.x + qv.y * kv.y + qv.z * kv.z + qv.w * kv.w;
+            const bool in = t <= pos;
+            const float4 z4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            const float4 vv = t == pos ? vp : in ? vc4[j] : z4;
+            const float sc = in ? dot[j] * scale : 0.0f;
+            const float mn = in ? fmaxf(m, sc) : m;
+            const float c_old = in ? expf(m - mn) : 1.0f;
+            const float p = in ? expf(sc - mn) : 0.0f;
+            l = l * c_old + p;
+            acc.x = acc.x * c_old + p * vv.x;
+            acc.y = acc.y * c_old + p * vv.y;
+            acc.z = acc.z * c_old + p * vv.z;
+            acc.w = acc.w * c_old + p * vv.w;
+            m = mn;
+        }
+    };
+    pass(lr, kr, vr);
+    if (lr + AHEAD * ROWS <= pos) {
+        // Longer contexts: the following passes, each requesting the next.
 #pragma unroll
-            for (int o = LPR / 2; o > 0; o >>= 1) dot += __shfl_xor(dot, o, 64);
-            if (t <= pos) {
-                const float sc = dot * scale;
-                const float mn = fmaxf(m, sc);
-                const float c_old = expf(m - mn);
-                const float p = expf(sc - mn);
-                l = l * c_old + p;
-                acc.x = acc.x * c_old + p * vv.x;
-                acc.y = acc.y * c_old + p * vv.y;
-                acc.z = acc.z * c_old + p * vv.z;
-                acc.w = acc.w * c_old + p * vv.w;
-                m = mn;
+        for (int j = 0; j < AHEAD; ++j) {
+            const int tj = min(lr + (AHEAD + j) * ROWS, last);
+            kr[j] = *reinterpret_cast<const float4*>(kbase + tj * t_stride + 4 * li);
+            vr[j] = *reinterpret_cast<const float4*>(vbase + tj * t_stride + 4 * li);
+        }
+        for (int t0 = lr + AHEAD * ROWS; t0 <= pos; t0 += AHEAD * ROWS) {
+            float4 kc4[AHEAD], vc4[AHEAD];
+#pragma unroll
+            for (int j = 0; j < AHEAD; ++j) {
+                kc4[j] = kr[j];
+                vc4[j] = vr[j];
             }
+            if (t0 + AHEAD * ROWS <= pos) {
+#pragma unroll
+                for (int j = 0; j < AHEAD; ++j) {
+                    const int tj = min(t0 + (AHEAD + j) * ROWS, last);
+                    kr[j] = *reinterpret_cast<const float4*>(kbase + tj * t_stride + 4 * li);
+                    vr[j] = *reinterpret_cast<const float4*>(vbase + tj * t_stride + 4 * li);
+                }
+            }
+            pass(t0, kc4, vc4);
         }
     }
     if (li == 0) {
@@ -366,17 +414,19 @@ __global__ __launch_bounds__(kFlashThreads) void attention_rope_kernel(
     __syncthreads();
     if (tid < HD) {
         float mx = -INFINITY;
+#pragma unroll
         for (int g = 0; g < ROWS; ++g) mx = fmaxf(mx, gm[g]);
         const int c4 = tid / 4;
         const int e = tid % 4;
         float num = 0.0f;
         float den = 0.0f;
+#pragma unroll
         for (int g = 0; g < ROWS; ++g) {
-            if (gm[g] == -INFINITY) continue;  // a group without rows (pos + 1 < ROWS)
-            const float w = expf(gm[g] - mx);
+            const bool rows = gm[g] != -INFINITY;  // false: a group without rows (pos + 1 < ROWS)
+            const float w = rows ? expf(gm[g] - mx) : 0.0f;
             const float4 a = gacc[g][c4];
-            num += w * (e == 0 ? a.x : e == 1 ? a.y : e == 2 ? a.z : a.w);
-            den += w * gl[g];
+            num += rows ? w * (e == 0 ? a.x : e == 1 ? a.y : e == 2 ? a.z : a.w) : 0.0f;
+            den += rows ? w * gl[g] : 0.0f;
         }
         out[h * HD + tid] = num / den;
     }

@@ -84,6 +84,24 @@ def test_logits_match_reference(hip, orc, ref, tmp_path, name):
     dec.close()
 
 
+@pytest.mark.parametrize("name,n_tok", [("head_dim_128", 160), ("mha_q4_0", 560)])
+def test_long_context_logits_match_reference(hip, orc, ref, tmp_path, name, n_tok):
+    """Contexts of several attention passes: one pass covers 64 cache rows at
+    head_dim 128 and 256 rows at head_dim 32 (512 threads, 4 rows each), so
+    these runs take the multi-pass path with its one-pass-ahead requests."""
+    path = mf.write_model(orc, str(tmp_path / f"{name}_long.gguf"), **dict(VARIANTS[name], ctx=n_tok + 8))
+    say(f"decoder {name} over {n_tok} positions")
+    dec = hip.Decoder(path)
+    rd = ref.decoder(path)
+    rng = np.random.default_rng(11)
+    tokens = rng.integers(0, dec.config["vocab_size"], n_tok).tolist()
+    worst = 0.0
+    for pos, t in enumerate(tokens):
+        worst = max(worst, close(dec.forward(t, pos), rd.forward(t, pos), f"{name} pos {pos}"))
+    say(f"  worst relative logit difference {worst:.2e}")
+    dec.close()
+
+
 @pytest.mark.parametrize("name", list(VARIANTS))
 def test_greedy_generation_matches_reference(hip, orc, ref, tmp_path, name):
     path = model(orc, tmp_path, name)
