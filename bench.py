@@ -553,7 +553,22 @@ def gemm_shape_bench(qt, m, k, n, stream, reps_target=100):
     return res
 
 
+_JSON_FD = None
+
+
+def emit(obj):
+    """Writes the one JSON line to the process's original stdout.  main()
+    points fd 1 at stderr first: C code loaded here (the reference's GGUF
+    loader behind the CPU baseline among it) prints progress on stdout."""
+    line = (json.dumps(obj) + "\n").encode()
+    os.write(_JSON_FD if _JSON_FD is not None else 1, line)
+
+
 def main():
+    global _JSON_FD
+    sys.stdout.flush()
+    _JSON_FD = os.dup(1)
+    os.dup2(2, 1)
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
@@ -593,15 +608,15 @@ def main():
                 f"{r['tflops']:8.1f} TFLOP/s ({100 * r['frac_of_fp16_dense_peak']:.1f}% of fp16 peak) "
                 f"{r['gbs']:8.1f} GB/s {r['kernel']}")
             rows.append(r)
-        print(json.dumps({"gemm": rows}), flush=True)
+        emit({"gemm": rows})
         return
     if args.decode_only:
         hip.load()
         hip.init(0)
         if args.decode_steps > 0:
-            print(json.dumps(decode_steps_bench(args.decode_steps)), flush=True)
+            emit(decode_steps_bench(args.decode_steps))
         else:
-            print(json.dumps(decode_bench()), flush=True)
+            emit(decode_bench())
         return
 
     if args.gpus != 1:
@@ -764,7 +779,7 @@ def main():
         "decode": decode,
         "gemm": gemm,
     }
-    print(json.dumps(out), flush=True)
+    emit(out)
 
 
 if __name__ == "__main__":
