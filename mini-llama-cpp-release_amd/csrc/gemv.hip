@@ -185,7 +185,10 @@ template <int QT> struct SingleDepth { static constexpr int D = QT == 1 ? 2 : 3;
 // takes groups w, w + W, ... (W waves in the grid), group i being rows
 // i * SUB + slot; its ring slot k holds groups k, k + D, k + 2D, ... of the
 // wave: a slot is computed, then refilled in place with the group D ahead.
-template <int QT, int LPR, int WAVES, int D, int MODE>
+// The first PRE ring slots are requested with x, before x is quantized; the
+// rest right after (issuing requests stalls once the memory system is
+// saturated, and x's quantization waits behind them).
+template <int QT, int LPR, int WAVES, int D, int MODE, int PRE = D>
 __global__ __launch_bounds__(WAVES * 64, 2) void gemv_single_kernel(const GemvGroup g, const float* __restrict__ x,
                                                                    int M, int K, int nb, int groups) {
     constexpr int DW = Fmt<QT>::DW;
@@ -247,16 +250,20 @@ __global__ __launch_bounds__(WAVES * 64, 2) void gemv_single_kernel(const GemvGr
         if (ACC) r = *res;
     };
     // nb <= 2 * 64 pairs <= blockDim / 4: one round of x loads
+    static_assert(PRE >= 1 && PRE <= D, "ring slots requested before staging");
+    auto request_slot = [&](int k) {
+        if (GLU) {
+            request_glu(g0 + k * gstride, k);
+        } else {
+            request(g0 + k * gstride, wq[k], rq[k]);
+        }
+    };
     stage_x<QT, false, Mode<MODE>::norm, 1, true>(x, K, nb, xl, xc, g.norm_w, g.norm_eps, [&] {
 #pragma unroll
-        for (int k = 0; k < D; ++k) {
-            if (GLU) {
-                request_glu(g0 + k * gstride, k);
-            } else {
-                request(g0 + k * gstride, wq[k], rq[k]);
-            }
-        }
+        for (int k = 0; k < PRE; ++k) request_slot(k);
     });
+#pragma unroll
+    for (int k = PRE; k < D; ++k) request_slot(k);
     uint32_t xq[XLimbs<QT>::PAIR_DW];
     float4 c0, c1;
     load_xq<QT>(xl, xc, p, xq, c0, c1);
@@ -322,10 +329,11 @@ __global__ __launch_bounds__(WAVES * 64, 2) void gemv_single_kernel(const GemvGr
 // w, w + W, ... (W waves in the grid; item i being rows i * SUB + slot), each
 // walked in chunks c = 0 .. nch-1 (pair c * LPR + pl of every lane; lanes past
 // the row keep their sum).  A ring of D units (item, chunk) of weight requests
-// is in flight per wave, refilled in place.  Workgroup size, grid cap and D
-// come from MI355X measurements (launch_multi_t).
+// is in flight per wave, refilled in place; the first PRE of them are
+// requested with x, the rest once x is staged.  Workgroup size, grid cap, D
+// and PRE come from MI355X measurements (launch_multi_t).
 
-template <int QT, int LPR, int WAVES, int D, int MODE>
+template <int QT, int LPR, int WAVES, int D, int MODE, int PRE = D>
 __global__ __launch_bounds__(WAVES * 64) void gemv_multi_kernel(const GemvGroup g, const float* __restrict__ x,
                                                                int M, int K, int nb, int items) {
     constexpr int DW = Fmt<QT>::DW;
@@ -378,10 +386,13 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_multi_kernel(const GemvGroup 
             pit += GW;
         }
     };
+    static_assert(PRE >= 1 && PRE <= D, "ring units requested before staging");
     stage_x_fit<QT, false, Mode<MODE>::norm>(x, K, nb, xl, xc, g.norm_w, g.norm_eps, [&] {
 #pragma unroll
-        for (int k = 0; k < D; ++k) request(wq[k], rq[k]);
+        for (int k = 0; k < PRE; ++k) request(wq[k], rq[k]);
     });
+#pragma unroll
+    for (int k = PRE; k < D; ++k) request(wq[k], rq[k]);
     const bool store_y = !PICK || g.y[0] != nullptr;
     unsigned long long best = 0;
     int it = gw, c = 0;
@@ -520,11 +531,20 @@ PairCfg choose_pair(const LinearShape& s) {
 template <int QT, int LPR, int MODE>
 hipError_t launch_single_t(const LinearShape& s, const GemvGroup& g, const float* x, hipStream_t stream) {
     constexpr int rows_per_group = 64 / LPR;
+    constexpr int D = SingleDepth<QT>::D;
     const int groups = (s.M + rows_per_group - 1) / rows_per_group;
     int grid = (groups + kWaves - 1) / kWaves;
     if (grid > kPersistentWgs) grid = kPersistentWgs;
-    hipLaunchKernelGGL((gemv_single_kernel<QT, LPR, kWaves, SingleDepth<QT>::D, MODE>), dim3(grid, s.rows), dim3(kWaves * 64),
-                       pair_lds_bytes(QT, s.nb), stream, g, x, s.M, s.K, s.nb, groups);
+    // Ring slots requested before x is quantized (MI355X, Q4_0 x 4096, cold
+    // weights): one when a wave has at most two groups (4096 rows: 5.55 ->
+    // 5.30 us), all but one for longer runs (12288 rows: 8.39 -> 8.26 us).
+    // Q8_0's two-slot ring keeps both ahead of x (one measured 2 % slower).
+    const int per_wave = (groups + grid * kWaves - 1) / (grid * kWaves);
+    auto kern = D < 3 ? gemv_single_kernel<QT, LPR, kWaves, D, MODE, D>
+                      : per_wave <= 2 ? gemv_single_kernel<QT, LPR, kWaves, D, MODE, 1>
+                                      : gemv_single_kernel<QT, LPR, kWaves, D, MODE, (D > 1 ? D - 1 : 1)>;
+    hipLaunchKernelGGL(kern, dim3(grid, s.rows), dim3(kWaves * 64), pair_lds_bytes(QT, s.nb), stream, g, x, s.M, s.K,
+                       s.nb, groups);
     return hipGetLastError();
 }
 
@@ -545,7 +565,9 @@ hipError_t launch_multi_t(const LinearShape& s, const GemvGroup& g, const float*
     // per wave.
     if (items < 2048) return go(gemv_multi_kernel<QT, LPR, 4, 3, MODE>, 4, 1 << 20);
     if (QT == 1) return go(gemv_multi_kernel<QT, LPR, 8, 1, MODE>, 8, 1 << 20);
-    return go(gemv_multi_kernel<QT, LPR, 16, 2, MODE>, 16, kPersistentWgs);
+    // One of the two units requested with x, the other once x is staged
+    // (4096 x 11008 Q4_0, cold weights: 9.50 -> 9.34 us).
+    return go(gemv_multi_kernel<QT, LPR, 16, 2, MODE, 1>, 16, kPersistentWgs);
 }
 
 template <int QT, int MODE>
