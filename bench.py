@@ -397,11 +397,22 @@ def decode_bench(n_new=128, layers=32, cpu=False):
     dec.prefill(long_prompt)
     dt_pre = time.perf_counter() - t0
     dec.close()
+    # Roofline of both legs: a decode step streams every quantized linear once
+    # (Q4_0: 18 bytes per 32 weights); a prefill pass does 2 flops per linear
+    # weight and token (attention, norms and RoPE left out).
+    lin_params = layers * (4 * 4096 * 4096 + 3 * 11008 * 4096) + 32000 * 4096
+    step_bytes = lin_params * 18 // 32
+    dec_gbs = step_bytes / (dt / n_new) / 1e9
+    pre_tflops = 2.0 * lin_params * len(long_prompt) / dt_pre / 1e12
     return {"model": "llama7b-shaped q4_0 (synthetic weights)", "layers": layers, "prompt_tokens": len(prompt),
             "new_tokens": n_new, "s": round(dt, 4), "tokens_per_s": round(n_new / dt, 1),
             "ms_per_token": round(dt * 1e3 / n_new, 3), "distinct_tokens": len(set(toks)),
             "prefill_tokens": len(long_prompt), "prefill_s": round(dt_pre, 4),
             "prefill_tokens_per_s": round(len(long_prompt) / dt_pre, 1),
+            "weight_bytes_per_token": step_bytes, "weight_gbs": round(dec_gbs, 1),
+            "weight_frac_of_hbm_peak": round(dec_gbs / HBM_PEAK_GBS, 4),
+            "prefill_linear_tflops": round(pre_tflops, 1),
+            "prefill_frac_of_fp16_dense_peak": round(pre_tflops / FP16_PEAK_TFLOPS, 4),
             "file_gb": round(nbytes / 1e9, 3), "s_write_file": round(t_write, 2), "s_load": round(t_load, 2),
             "cpu_baseline": cpu_leg,
             "note": "wall time of one mlq_hip_decoder_generate call (prompt steps, recorded step replayed per "
@@ -709,8 +720,10 @@ def main():
     decode = None
     if not args.no_shapes:
         decode = decode_bench(cpu=not args.no_cpu)
-        log(f"  decode {decode['model']}: {decode['tokens_per_s']} tokens/s ({decode['ms_per_token']} ms/token), "
-            f"batched prefill {decode['prefill_tokens_per_s']} tokens/s, load {decode['s_load']} s")
+        log(f"  decode {decode['model']}: {decode['tokens_per_s']} tokens/s ({decode['ms_per_token']} ms/token, "
+            f"weights at {decode['weight_gbs']} GB/s = {100 * decode['weight_frac_of_hbm_peak']:.1f}% of HBM peak), "
+            f"batched prefill {decode['prefill_tokens_per_s']} tokens/s ({decode['prefill_linear_tflops']} TFLOP/s "
+            f"in the linears), load {decode['s_load']} s")
 
     ingest = None
     if not args.no_shapes:
