@@ -378,7 +378,7 @@ def decode_bench(n_new=128, layers=32, cpu=False):
         nbytes = write_llama7b_q4_0(path, layers)
         t_write = time.perf_counter() - t0
         t0 = time.perf_counter()
-        dec = hip.Decoder(path, max_seq_len=1024)
+        dec = hip.Decoder(path, max_seq_len=2048)
         t_load = time.perf_counter() - t0
         if cpu:
             cpu_leg = decode_cpu_baseline(path, dec)
@@ -396,6 +396,15 @@ def decode_bench(n_new=128, layers=32, cpu=False):
     t0 = time.perf_counter()
     dec.prefill(long_prompt)
     dt_pre = time.perf_counter() - t0
+    # Decode at ~1k context: two generations after the same 960-token prompt,
+    # 8 and 72 new tokens; their difference is 64 steps at positions 967..1030.
+    ctx_prompt = (np.arange(960) * 13 % 32000).tolist()
+    times = []
+    for n in (8, 72):
+        t0 = time.perf_counter()
+        dec.generate(ctx_prompt, n)
+        times.append(time.perf_counter() - t0)
+    dt_ctx = (times[1] - times[0]) / 64
     dec.close()
     # Roofline of both legs: a decode step streams every quantized linear once
     # (Q4_0: 18 bytes per 32 weights); a prefill pass does 2 flops per linear
@@ -412,11 +421,13 @@ def decode_bench(n_new=128, layers=32, cpu=False):
             "weight_bytes_per_token": step_bytes, "weight_gbs": round(dec_gbs, 1),
             "weight_frac_of_hbm_peak": round(dec_gbs / HBM_PEAK_GBS, 4),
             "prefill_linear_tflops": round(pre_tflops, 1),
+            "tokens_per_s_at_1k_context": round(1.0 / dt_ctx, 1), "ms_per_token_at_1k_context": round(dt_ctx * 1e3, 3),
             "prefill_frac_of_fp16_dense_peak": round(pre_tflops / FP16_PEAK_TFLOPS, 4),
             "file_gb": round(nbytes / 1e9, 3), "s_write_file": round(t_write, 2), "s_load": round(t_load, 2),
             "cpu_baseline": cpu_leg,
             "note": "wall time of one mlq_hip_decoder_generate call (prompt steps, recorded step replayed per "
-                    "token, one upload, one download); attention over positions 0..131"}
+                    "token, one upload, one download); attention over positions 0..131; the 1k-context rate is the "
+                    "difference of two generations after the same 960-token prompt (64 steps at positions 967..1030)"}
 
 
 def decode_cpu_baseline(path, dec, tokens=(11, 22, 33)):

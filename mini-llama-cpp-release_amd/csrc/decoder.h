@@ -126,6 +126,9 @@ private:
     int32_t* io_ = nullptr;      // prompt tokens then generated tokens
     size_t io_cap_ = 0;
     void* pick_ = nullptr;       // PickState
+    float* attn_part_ = nullptr;     // [n_heads][attn_splits_][head_dim + 2]: split attention states
+    unsigned* attn_cnt_ = nullptr;   // [n_heads] arrival counts of the split attention
+    int attn_splits_ = 1;
     // Batched prefill: activations of kPrefillRows rows and the GEMM workspace.
     float *X_ = nullptr, *H_ = nullptr, *Q_ = nullptr, *K_ = nullptr, *V_ = nullptr, *ATT_ = nullptr;
     float *PROJ_ = nullptr, *GATE_ = nullptr, *UP_ = nullptr, *ACT_ = nullptr, *FF_ = nullptr;

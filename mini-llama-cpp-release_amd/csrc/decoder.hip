@@ -30,6 +30,10 @@ constexpr int kAttnThreads = 256;
 constexpr int kFlashThreads = 512;
 constexpr int kFlashAhead = 4;
 constexpr int kMaxHeadDim = 256;
+// Decode attention splits a head's positions over up to kAttnMaxSplits
+// workgroups once there are more than kAttnSplitRows of them.
+constexpr int kAttnSplitRows = 128;
+constexpr int kAttnMaxSplits = 8;
 
 // Sum (or max) over a workgroup of `nthreads`; every thread gets the result.
 template <int NT, bool MAX>
@@ -270,12 +274,20 @@ __device__ __forceinline__ float lane_group_sum(float v) {
 // compiler wait for all outstanding memory operations at the join.  The
 // AHEAD rows of a pass are reduced together (DPP, no LDS round trips per
 // step) and folded into the running softmax with selects.
+// Long contexts: workgroup (h, s) of the grid's nsplit per head takes the s-th
+// of S = min(nsplit, ceil((pos + 1) / kAttnSplitRows)) equal runs of
+// positions (workgroups past S return at once; S = 1 is the single-workgroup
+// path).  Each writes its (maximum, sum, weighted V) with agent-scope stores
+// to part[h][s], waits for them, and counts in on cnt[h]; the last to arrive
+// resets the count (graph replays need no memset) and merges the S states in
+// split order — the protocol of the GEMM's split-K reduction.
 template <int LPR>
 __global__ __launch_bounds__(kFlashThreads) void attention_rope_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     const float* __restrict__ bq, const float* __restrict__ bk, const float* __restrict__ bv, int n_heads, int n_kv,
     float theta, int neox, int max_seq, int layer, DecodeState* st, float* __restrict__ kc,
-    float* __restrict__ vc, float* __restrict__ out) {
+    float* __restrict__ vc, float* __restrict__ out, float* __restrict__ part, unsigned* __restrict__ cnt,
+    int nsplit) {
     constexpr int HD = 4 * LPR;
     constexpr int ROWS = kFlashThreads / LPR;
     constexpr int AHEAD = kFlashAhead;
@@ -313,9 +325,16 @@ __global__ __launch_bounds__(kFlashThreads) void attention_rope_kernel(
 
     const int p0 = st->pos;
     const bool ok = p0 >= 0 && p0 < max_seq;
-    if (!ok && h == 0 && tid == 0) st->error |= kDecodeErrPos;
+    const int split = blockIdx.y;
+    if (!ok && h == 0 && split == 0 && tid == 0) st->error |= kDecodeErrPos;
     const int pos = ok ? p0 : 0;
-    const int last = pos > 0 ? pos - 1 : 0;  // rows read from the cache stay below pos
+    const int S = min(nsplit, (pos + kAttnSplitRows) / kAttnSplitRows);  // ceil((pos + 1) / kAttnSplitRows)
+    if (split >= S) return;
+    const int chunk = (pos + S) / S;  // ceil((pos + 1) / S)
+    const int t_begin = split * chunk;
+    const int t_end = min(pos + 1, t_begin + chunk);  // this workgroup's positions: [t_begin, t_end)
+    // Rows read from the cache stay below pos and inside the run.
+    const int last = max(min(t_end, pos) - 1, 0);
     const size_t layer_base = static_cast<size_t>(layer) * max_seq * n_kv * HD;
     const size_t t_stride = static_cast<size_t>(n_kv) * HD;
     const float* kbase = kc + layer_base + kvh * HD;
@@ -327,7 +346,7 @@ __global__ __launch_bounds__(kFlashThreads) void attention_rope_kernel(
     float4 kr[AHEAD], vr[AHEAD];
 #pragma unroll
     for (int j = 0; j < AHEAD; ++j) {
-        const int tj = min(lr + j * ROWS, last);
+        const int tj = min(t_begin + lr + j * ROWS, last);
         kr[j] = *reinterpret_cast<const float4*>(kbase + tj * t_stride + 4 * li);
         vr[j] = *reinterpret_cast<const float4*>(vbase + tj * t_stride + 4 * li);
     }
@@ -359,12 +378,12 @@ __global__ __launch_bounds__(kFlashThreads) void attention_rope_kernel(
             const float4 kv = t0 + j * ROWS == pos ? kp : kc4[j];
             dot[j] = lane_group_sum<LPR>(qv.x * kv.x + qv.y * kv.y + qv.z * kv.z + qv.w * kv.w);
         }
-        // Rows past pos (clamped re-reads, or at pos 0 a cache row not yet
-        // written) are selected away before any arithmetic touches them.
+        // Rows past the run (clamped re-reads, or at pos 0 a cache row not
+        // yet written) are selected away before any arithmetic touches them.
 #pragma unroll
         for (int j = 0; j < AHEAD; ++j) {
             const int t = t0 + j * ROWS;
-            const bool in = t <= pos;
+            const bool in = t < t_end;
             const float4 z4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
             const float4 vv = t == pos ? vp : in ? vc4[j] : z4;
             const float sc = in ? dot[j] * scale : 0.0f;
@@ -379,23 +398,23 @@ __global__ __launch_bounds__(kFlashThreads) void attention_rope_kernel(
             m = mn;
         }
     };
-    pass(lr, kr, vr);
-    if (lr + AHEAD * ROWS <= pos) {
-        // Longer contexts: the following passes, each requesting the next.
+    pass(t_begin + lr, kr, vr);
+    if (t_begin + lr + AHEAD * ROWS < t_end) {
+        // Longer runs: the following passes, each requesting the next.
 #pragma unroll
         for (int j = 0; j < AHEAD; ++j) {
-            const int tj = min(lr + (AHEAD + j) * ROWS, last);
+            const int tj = min(t_begin + lr + (AHEAD + j) * ROWS, last);
             kr[j] = *reinterpret_cast<const float4*>(kbase + tj * t_stride + 4 * li);
             vr[j] = *reinterpret_cast<const float4*>(vbase + tj * t_stride + 4 * li);
         }
-        for (int t0 = lr + AHEAD * ROWS; t0 <= pos; t0 += AHEAD * ROWS) {
+        for (int t0 = t_begin + lr + AHEAD * ROWS; t0 < t_end; t0 += AHEAD * ROWS) {
             float4 kc4[AHEAD], vc4[AHEAD];
 #pragma unroll
             for (int j = 0; j < AHEAD; ++j) {
                 kc4[j] = kr[j];
                 vc4[j] = vr[j];
             }
-            if (t0 + AHEAD * ROWS <= pos) {
+            if (t0 + AHEAD * ROWS < t_end) {
 #pragma unroll
                 for (int j = 0; j < AHEAD; ++j) {
                     const int tj = min(t0 + (AHEAD + j) * ROWS, last);
@@ -428,8 +447,41 @@ __global__ __launch_bounds__(kFlashThreads) void attention_rope_kernel(
             num += rows ? w * (e == 0 ? a.x : e == 1 ? a.y : e == 2 ? a.z : a.w) : 0.0f;
             den += rows ? w * gl[g] : 0.0f;
         }
-        out[h * HD + tid] = num / den;
+        if (S == 1) {
+            out[h * HD + tid] = num / den;
+        } else {
+            float* ps = part + (static_cast<size_t>(h) * nsplit + split) * (HD + 2);
+            if (tid == 0) {
+                __hip_atomic_store(ps, mx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(ps + 1, den, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            __hip_atomic_store(ps + 2 + tid, num, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
     }
+    if (S == 1) return;
+    // Count in once this workgroup's state has reached the point of coherence.
+    __shared__ unsigned last_in;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (tid == 0) {
+        const unsigned done = __hip_atomic_fetch_add(cnt + h, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last_in = done == static_cast<unsigned>(S) - 1 ? 1u : 0u;
+        if (last_in) __hip_atomic_store(cnt + h, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (last_in == 0u || tid >= HD) return;
+    const float* ph = part + static_cast<size_t>(h) * nsplit * (HD + 2);
+    float mx = -INFINITY;
+    for (int j = 0; j < S; ++j) mx = fmaxf(mx, __hip_atomic_load(ph + j * (HD + 2), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    float num = 0.0f;
+    float den = 0.0f;
+    for (int j = 0; j < S; ++j) {
+        const float* pj = ph + j * (HD + 2);
+        const float w = expf(__hip_atomic_load(pj, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - mx);
+        den += w * __hip_atomic_load(pj + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        num += w * __hip_atomic_load(pj + 2 + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    out[h * HD + tid] = num / den;
 }
 
 // ---- Batched prefill (rows r = 0..n-1 at positions start + r) ----
@@ -1026,6 +1078,12 @@ std::unique_ptr<Decoder> Decoder::from_gguf(const std::string& path, int device,
     d->check(hipMemset(d->state_, 0, sizeof(DecodeState)), "hipMemset");
     d->pick_ = alloc(sizeof(PickState));
     d->check(hipMemset(d->pick_, 0, sizeof(PickState)), "hipMemset");
+    // Split decode attention: partial states and arrival counts (zero; the
+    // last workgroup of each head resets its count).
+    d->attn_splits_ = std::max(1, std::min(kAttnMaxSplits, (c.max_seq_len + kAttnSplitRows - 1) / kAttnSplitRows));
+    d->attn_part_ = f32buf(static_cast<size_t>(c.n_heads) * d->attn_splits_ * (c.head_dim + 2));
+    d->attn_cnt_ = static_cast<unsigned*>(alloc(static_cast<size_t>(c.n_heads) * sizeof(unsigned)));
+    d->check(hipMemset(d->attn_cnt_, 0, static_cast<size_t>(c.n_heads) * sizeof(unsigned)), "hipMemset");
     d->check(hipDeviceSynchronize(), "hipDeviceSynchronize");
     return d;
 }
@@ -1090,9 +1148,9 @@ bool Decoder::launch_attention_rope(hipStream_t s, int l) {
     const DecoderConfig& c = cfg_;
     const Layer& L = layers_[l];
 #define MLQ_ATTN(LPR)                                                                                            \
-    hipLaunchKernelGGL((attention_rope_kernel<LPR>), dim3(c.n_heads), dim3(kFlashThreads), 0, s, q_, k_, v_, L.bq, \
-                       L.bk, L.bv, c.n_heads, c.n_kv_heads, c.rope_theta, c.rope_neox, c.max_seq_len, l, state_,    \
-                       kcache_, vcache_, att_)
+    hipLaunchKernelGGL((attention_rope_kernel<LPR>), dim3(c.n_heads, attn_splits_), dim3(kFlashThreads), 0, s, q_, \
+                       k_, v_, L.bq, L.bk, L.bv, c.n_heads, c.n_kv_heads, c.rope_theta, c.rope_neox, c.max_seq_len, l, \
+                       state_, kcache_, vcache_, att_, attn_part_, attn_cnt_, attn_splits_)
     switch (c.head_dim) {
         case 16: MLQ_ATTN(4); break;
         case 32: MLQ_ATTN(8); break;
