@@ -84,11 +84,13 @@ def test_logits_match_reference(hip, orc, ref, tmp_path, name):
     dec.close()
 
 
-@pytest.mark.parametrize("name,n_tok", [("head_dim_128", 160), ("mha_q4_0", 560)])
+@pytest.mark.parametrize("name,n_tok", [("head_dim_128", 160), ("mha_q4_0", 560), ("head_dim_128", 1000)])
 def test_long_context_logits_match_reference(hip, orc, ref, tmp_path, name, n_tok):
     """Contexts of several attention passes: one pass covers 64 cache rows at
     head_dim 128 and 256 rows at head_dim 32 (512 threads, 4 rows each), so
-    these runs take the multi-pass path with its one-pass-ahead requests."""
+    these runs take the multi-pass path with its one-pass-ahead requests; past
+    128 positions the positions are split over up to 8 workgroups per head
+    (2, 5 and 8 splits for caches of 168, 568 and 1008 positions)."""
     path = mf.write_model(orc, str(tmp_path / f"{name}_long.gguf"), **dict(VARIANTS[name], ctx=n_tok + 8))
     say(f"decoder {name} over {n_tok} positions")
     dec = hip.Decoder(path)
@@ -140,6 +142,26 @@ def test_device_loop_equals_stepwise_forward(hip, orc, tmp_path):
     assert dec.generate(prompt, n_new) == loop
     longer = dec.generate(list(range(1, 30)), 30)
     assert len(longer) == 30
+    dec.close()
+
+
+def test_device_loop_long_context(hip, orc, tmp_path):
+    """Past 128 positions decode attention splits each head over several
+    workgroups that count in on a per-head counter the last one resets: the
+    recorded step replayed over a long context (twice) gives the tokens of
+    stepwise forwards after the same batched prefill."""
+    path = mf.write_model(orc, str(tmp_path / "long.gguf"), **dict(VARIANTS["head_dim_128"], ctx=600))
+    dec = hip.Decoder(path)
+    rng = np.random.default_rng(5)
+    prompt = rng.integers(0, dec.config["vocab_size"], 300).tolist()
+    n_new = 40
+    loop = dec.generate(prompt, n_new)
+    assert dec.generate(prompt, n_new) == loop
+    dec.prefill(prompt[:-1])
+    toks = list(prompt)
+    for pos in range(len(prompt) - 1, len(prompt) + n_new - 1):
+        toks.append(int(np.argmax(dec.forward(toks[pos], pos))))
+    assert loop == toks[len(prompt):]
     dec.close()
 
 
