@@ -1117,10 +1117,13 @@ hipError_t launch_q(const LinearShape& s, const GemmCfg& c, const WsLayout& l, c
 //  * up to 128 tokens: 128 rows x 32 tokens, x split in the kernel;
 //  * more tokens: x split once by xsplit_kernel (the in-kernel split would be
 //    repeated by every row tile), 128 rows x 32 tokens, or x 64 tokens for
-//    Q8_0 (its 34-byte blocks gain most from fewer weight passes; Q4 measured
-//    equal or slower with the larger tile's single workgroup per CU);
+//    Q8_0 from 512 tokens (its 34-byte blocks gain most from fewer weight
+//    passes there; at 256 tokens, and for Q4 throughout, the larger tile's
+//    single workgroup per CU measured slower: 11008 x 4096 Q8_0 N = 256
+//    124.2 against 110.4 us);
 //  * from 32 tokens on, 8 chunks per split unless the tiles alone give every
-//    CU a workgroup (then no K split).
+//    CU a workgroup (then no K split; with x split once, two splits until
+//    there are two workgroups per CU).
 struct ChunkCfg {
     int rw, tt, row_tiles, tok_tiles, splits, cps, npad;
     bool xs;
@@ -1133,7 +1136,7 @@ bool chunk_supported(const LinearShape& s) {
 ChunkCfg choose_chunk(const LinearShape& s) {
     ChunkCfg c;
     c.rw = s.rows <= 16 ? 1 : 2;
-    c.tt = s.rows <= 16 ? 1 : (s.rows > 128 && s.qtype == 1) ? 4 : 2;
+    c.tt = s.rows <= 16 ? 1 : (s.rows >= 512 && s.qtype == 1) ? 4 : 2;
     c.xs = s.rows > 128;
     c.row_tiles = (s.M + 64 * c.rw - 1) / (64 * c.rw);
     c.tok_tiles = (s.rows + 16 * c.tt - 1) / (16 * c.tt);
@@ -1144,8 +1147,12 @@ ChunkCfg choose_chunk(const LinearShape& s) {
     if (c.tt == 1) {
         splits = static_cast<int>((640 + tiles - 1) / tiles);
         splits = std::min(splits, nchunks >= 16 ? nchunks / 4 : nchunks / 2);
-    } else {
+    } else if (!c.xs) {
         splits = tiles >= 256 ? 1 : nchunks / 8;
+    } else {
+        // N = 256: two splits for 256 tiles (4096 x 4096 Q4_0: 45.2 -> 40.1 us)
+        const bool fill = c.tt == 4 ? tiles >= 256 : tiles >= 512;
+        splits = fill ? 1 : tiles >= 256 ? 2 : nchunks / 8;
     }
     splits = std::max(1, splits);
     if (tiles > kGemmMaxTiles) splits = 1;
