@@ -389,10 +389,10 @@ def decode_bench(n_new=128, layers=32, cpu=False):
     t0 = time.perf_counter()
     toks = dec.generate(prompt, n_new)
     dt = time.perf_counter() - t0
-    # Batched prefill of a 512-token prompt (two passes of 256 rows: MFMA
+    # Batched prefill of a 512-token prompt (one pass of 512 rows: MFMA
     # GEMMs for the linears, causal attention per row).
     long_prompt = (np.arange(512) * 7 % 32000).tolist()
-    dec.prefill(long_prompt[:256])  # warm-up (GEMM workspace, kernels)
+    dec.prefill(long_prompt)  # warm-up (GEMM workspace, kernels)
     t0 = time.perf_counter()
     dec.prefill(long_prompt)
     dt_pre = time.perf_counter() - t0

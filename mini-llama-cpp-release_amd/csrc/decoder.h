@@ -74,7 +74,9 @@ public:
     // linears); logits of the last token to host memory (when not null).
     void prefill(const int* tokens, int n, int start, float* logits_host);
 
-    static constexpr int kPrefillRows = 256;  // rows per batched pass
+    // Rows per batched pass: the GEMM at 512 token rows does 17 % more work per
+    // µs than at 256 (4096 x 4096 Q4_0: 66.8 against 2 x 40.1 us).
+    static constexpr int kPrefillRows = 512;
 
 private:
     Decoder() = default;

@@ -222,7 +222,7 @@ def test_batched_prefill_matches_reference(hip, orc, ref, tmp_path, name):
 
 
 def test_batched_prefill_longer_than_one_pass(hip, orc, ref, tmp_path):
-    """A prompt of more rows than one batched pass holds (chunks of 256)."""
+    """A prompt of more rows than one batched pass holds (chunks of 512)."""
     path = mf.write_model(orc, str(tmp_path / "long.gguf"), ctx=640, vocab=300, layers=2, seed=9)
     dec = hip.Decoder(path)
     rd = ref.decoder(path)
