@@ -44,6 +44,14 @@ def test_gemm_baseline_config4(hip, orc, shape, n):
         assert name.startswith("gemm_mfma"), name
 
 
+@pytest.mark.parametrize("shape", [(4096, 4096), (4096, 11008)], ids=lambda s: f"{s[0]}x{s[1]}")
+def test_gemm_256_tokens_two_splits(hip, orc, shape):
+    """256 token rows (x split once, 256 tiles: two K splits and their reduction)."""
+    for fmt, qt in FMTS.items():
+        name, _ = run(hip, orc, qt, *shape, 256)
+        assert "splitk2" in name, name
+
+
 @pytest.mark.parametrize("m,k,n", [(4096, 4096, 16), (64, 64, 2), (33, 4096, 17), (300, 896, 40),
                                    (4864, 896, 7), (17, 64, 100), (1000, 11008, 3), (520, 4096, 130),
                                    (300, 896, 200), (200, 4096, 96)])
