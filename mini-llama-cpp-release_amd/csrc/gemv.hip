@@ -144,11 +144,15 @@ __device__ __forceinline__ void pick_finish(PickState* ps, int32_t* token, unsig
     __hip_atomic_store(&ps->sub[j][0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (__hip_atomic_fetch_add(&ps->top[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != groups - 1) return;
     __hip_atomic_store(&ps->top[0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // Every slot, unrolled: slots past `groups` are never written and hold 0,
+    // and issuing all exchanges before using any costs one round trip.
+    unsigned long long v[kPickGroups];
+#pragma unroll
+    for (int i = 0; i < kPickGroups; ++i)
+        v[i] = __hip_atomic_exchange(&ps->key[i][0], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     unsigned long long k = 0;
-    for (unsigned i = 0; i < groups; ++i) {
-        const unsigned long long v = __hip_atomic_exchange(&ps->key[i][0], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        k = v > k ? v : k;
-    }
+#pragma unroll
+    for (int i = 0; i < kPickGroups; ++i) k = v[i] > k ? v[i] : k;
     *token = pick_token(k);
 }
 
