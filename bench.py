@@ -159,9 +159,25 @@ class Sweep:
         return ids
 
 
-def cpu_sweep_check(sw: Sweep, threads: int):
-    """Run the reference CPU linear over the whole sweep on the same blocks,
-    time it, and compare every output with the GPU's."""
+def cpu_model():
+    """The host CPU's model name (from /proc/cpuinfo), for the baseline line."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_sweep_check(sw: Sweep, threads: int, runs: int = 3):
+    """Run the reference CPU linear over the whole sweep on the same blocks and
+    compare every output with the GPU's.  Timing follows the reference's own
+    benchmark pattern (src/main.cpp:1226-1238): one untimed warm-up sweep, then
+    `runs` timed sweeps, median reported; each sweep calls the threaded
+    linear() once per weight (parallel_for over all host cores,
+    src/thread_pool.cpp:23-73)."""
     import oracle
 
     sys.path.insert(0, os.path.join(REPO, "tests"))
@@ -170,32 +186,37 @@ def cpu_sweep_check(sw: Sweep, threads: int):
     ref = oracle.reference()
     kind = "reference" if ref is not None else "port"
     orc = oracle.get()
-    worst = 0.0
-    cpu_s = 0.0
+    prepared = []
     cpu_bytes = 0
-    for i, (name, w, x, y) in enumerate(sw.calls_desc):
+    for name, w, x, y in sw.calls_desc:
         nblk = w.m * w.nb
         blocks = w._keep.download(np.uint8, nblk * BB[w.qtype]).reshape(nblk, BB[w.qtype])
-        xv = x.download(np.float32)
-        yg = y.download(np.float32)
-        yc = np.empty(w.m, np.float32)
-        if ref is not None:
-            rw = ref.weight(w.qtype, blocks, w.m, w.k)
-            t0 = time.perf_counter()
-            rw.linear(xv, yc, threads)
-            cpu_s += time.perf_counter() - t0
-            del rw
-        else:
-            t0 = time.perf_counter()
-            yc = orc.linear(w.qtype, xv, blocks, w.m, threads=threads)
-            cpu_s += time.perf_counter() - t0
+        rw = ref.weight(w.qtype, blocks, w.m, w.k) if ref is not None else None
+        prepared.append((name, w, blocks, rw, x.download(np.float32), y.download(np.float32),
+                         np.empty(w.m, np.float32)))
         cpu_bytes += gemv_bytes(w.qtype, w.m, w.k)
+
+    def sweep_once():
+        t0 = time.perf_counter()
+        for _, w, blocks, rw, xv, _, yc in prepared:
+            if rw is not None:
+                rw.linear(xv, yc, threads)
+            else:
+                yc[:] = orc.linear(w.qtype, xv, blocks, w.m, threads=threads)
+        return time.perf_counter() - t0
+
+    warm = sweep_once()
+    times = [sweep_once() for _ in range(runs)]
+    worst = 0.0
+    for name, w, blocks, _, xv, yg, yc in prepared:
         worst = max(worst, check_close(yg, yc, xv, w.qtype, blocks, name))
         if name == "lm_head":
             arg_gpu, arg_cpu = int(np.argmax(yg)), orc.argmax(yc)
             top2 = np.sort(yc)[-2:]
+    del prepared
     return {
-        "kind": kind, "cpu_s": cpu_s, "cpu_bytes": cpu_bytes, "worst_err_over_bound": worst,
+        "kind": kind, "cpu_s": float(np.median(times)), "cpu_s_runs": [round(t, 4) for t in times],
+        "cpu_s_warmup": round(warm, 4), "cpu_bytes": cpu_bytes, "worst_err_over_bound": worst,
         "argmax_gpu": arg_gpu, "argmax_cpu": arg_cpu, "argmax_top2_gap": float(top2[1] - top2[0]),
     }
 
@@ -430,7 +451,7 @@ def decode_bench(n_new=128, layers=32, cpu=False):
                     "difference of two generations after the same 960-token prompt (64 steps at positions 967..1030)"}
 
 
-def decode_cpu_baseline(path, dec, tokens=(11, 22, 33)):
+def decode_cpu_baseline(path, dec, tokens=(11, 22, 33, 44)):
     """The reference's own load_gguf_model + forward_token (oracle/_ref, the
     threaded CPU path) on the same model file, a bounded sample of tokens;
     its logits also check the device decoder's at full size."""
@@ -451,12 +472,13 @@ def decode_cpu_baseline(path, dec, tokens=(11, 22, 33)):
         got = dec.forward(t, pos)
         worst = max(worst, float(np.abs(got.astype(np.float64) - want).max()) / max(1.0, float(np.abs(want).max())))
     del rd
-    per_token = sum(times[1:]) / max(1, len(times) - 1)
+    per_token = float(np.median(times[1:]))  # the first token is the warm-up
     if worst > 1e-3:
         raise SystemExit(f"decoder logits differ from the reference's by {worst:.2e} of max |logit|")
-    return {"kind": "reference", "cores": threads, "tokens_per_s": round(1.0 / per_token, 3),
+    return {"kind": "reference", "cores": threads, "cpu_model": cpu_model(), "tokens_per_s": round(1.0 / per_token, 3),
             "ms_per_token": round(per_token * 1e3, 1), "s_load": round(t_load, 2),
-            "sample": f"forward_token at positions 0..{len(tokens) - 1} (first excluded from the rate)",
+            "sample": f"forward_token at positions 0..{len(tokens) - 1}: position 0 is the warm-up, the rate is "
+                      f"the median of the other {len(tokens) - 1} ({', '.join(f'{t * 1e3:.0f}' for t in times[1:])} ms)",
             "gpu_vs_reference_max_rel_logit_diff": worst}
 
 
@@ -759,9 +781,12 @@ def main():
         threads = os.cpu_count() or 1
         chk = cpu_sweep_check(sw, threads)
         cpu = {"value": round(chk["cpu_bytes"] / chk["cpu_s"] / 1e9, 3), "unit": "GB/s",
-               "cores": threads, "kind": chk["kind"],
-               "sample": f"whole sweep once ({sw.n()} calls, {chk['cpu_bytes'] / 1e9:.3f} GB), "
-                         f"{chk['cpu_s'] * 1e3:.0f} ms"}
+               "cores": threads, "cpu_model": cpu_model(), "kind": chk["kind"],
+               "sample": f"whole sweep ({sw.n()} calls, {chk['cpu_bytes'] / 1e9:.3f} GB): one warm-up sweep "
+                         f"({chk['cpu_s_warmup'] * 1e3:.0f} ms), then the median of {len(chk['cpu_s_runs'])} "
+                         f"timed sweeps ({', '.join(f'{t * 1e3:.0f}' for t in chk['cpu_s_runs'])} ms); "
+                         f"the reference's threaded linear() with {threads} threads",
+               "ms_per_sweep": round(chk["cpu_s"] * 1e3, 1)}
         parity = {"outputs_within_tolerance": True,
                   "worst_err_over_bound": round(chk["worst_err_over_bound"], 4),
                   "argmax_gpu": chk["argmax_gpu"], "argmax_cpu": chk["argmax_cpu"],

@@ -168,6 +168,12 @@ int mlq_hip_memcpy_dtoh(void* dst, const void* src, size_t bytes);
 int mlq_hip_memcpy_dtod(void* dst, const void* src, size_t bytes, void* stream);
 int mlq_hip_memset(void* ptr, int value, size_t bytes);
 int mlq_hip_stream(int device, void** stream);       /* the library's stream for device */
+/* A new non-blocking stream on `device` (default priority) and its release.
+ * The library keeps per-stream state (batched-call workspace, pick state)
+ * until the process ends; destroy a stream only when no graph recorded on it
+ * is replayed any more. */
+int mlq_hip_stream_create(int device, void** stream);
+int mlq_hip_stream_destroy(void* stream);
 int mlq_hip_synchronize(void* stream);
 int mlq_hip_event_create(void** ev);
 int mlq_hip_event_destroy(void* ev);
@@ -175,7 +181,11 @@ int mlq_hip_event_record(void* ev, void* stream);
 int mlq_hip_event_elapsed_ms(void* start, void* stop, float* ms);
 
 /* Capture mlq_hip_quant_linear_many(calls, n) into a graph and instantiate it;
- * replay with mlq_hip_graph_launch.  Buffers are baked in at capture time. */
+ * replay with mlq_hip_graph_launch.  Buffers are baked in at capture time,
+ * including the stream's batched-call workspace: when a later, larger batched
+ * call grows that workspace, the old buffer is kept (never freed) for the
+ * graphs that recorded it.  Replays of such a graph share its workspace with
+ * nothing else as long as they run on the stream it was recorded on. */
 typedef struct mlq_graph_s* mlq_graph_t;
 int mlq_hip_graph_capture_many(const mlq_linear_call* calls, int n, void* stream, mlq_graph_t* out);
 int mlq_hip_graph_launch(mlq_graph_t g, void* stream);

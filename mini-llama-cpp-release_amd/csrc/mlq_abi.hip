@@ -122,6 +122,10 @@ struct DeviceState {
     size_t stage_bytes = 0;
     std::mutex ws_mu;          // guards the GEMM workspaces and the pick states
     std::vector<Workspace> ws;
+    // Workspaces replaced by a larger one.  A graph recorded before the growth
+    // still holds the old buffer's address (split-K counters, partials, split
+    // x), so a retired buffer is kept until the process ends.
+    std::vector<void*> retired_ws;
     std::vector<PickSlot> picks;
     std::mutex pin_mu;         // guards the pinned stage of file uploads
     void* pin[2] = {nullptr, nullptr};
@@ -263,7 +267,8 @@ bool capturing(hipStream_t s) {
 }
 
 // Returns a workspace of at least `bytes` for `stream` on `device`.  Growing
-// waits for the stream first so a buffer is never freed under a running kernel.
+// allocates a new buffer and retires the old one without freeing it: graphs
+// recorded on the stream keep using the buffer they were recorded with.
 int stream_workspace(int device, hipStream_t stream, size_t bytes, void** out) {
     DeviceState& st = g_dev[device];
     std::lock_guard<std::mutex> lock(st.ws_mu);
@@ -274,14 +279,13 @@ int stream_workspace(int device, hipStream_t stream, size_t bytes, void** out) {
                 return fail(MLQ_ERR_INVALID, "the stream's batched-call workspace must grow, which cannot happen "
                                              "under graph capture: make the largest batched call once first");
             }
-            MLQ_HIP_CHECK(hipStreamSynchronize(stream));
-            MLQ_HIP_CHECK(hipFree(w.ptr));
-            w.ptr = nullptr;
-            w.bytes = 0;
-            MLQ_HIP_CHECK(hipMalloc(&w.ptr, bytes));
+            void* p = nullptr;
+            MLQ_HIP_CHECK(hipMalloc(&p, bytes));
             // The split-K arrival counters start at zero; every launch leaves
             // them so.  Cleared on the workspace's own stream, ahead of its kernels.
-            MLQ_HIP_CHECK(hipMemsetAsync(w.ptr, 0, bytes, stream));
+            MLQ_HIP_CHECK(hipMemsetAsync(p, 0, bytes, stream));
+            st.retired_ws.push_back(w.ptr);
+            w.ptr = p;
             w.bytes = bytes;
         }
         *out = w.ptr;
@@ -763,6 +767,25 @@ int mlq_hip_stream(int device, void** stream) {
     int rc = ensure_device(device);
     if (rc != MLQ_OK) return rc;
     *stream = g_dev[device].stream;
+    return MLQ_OK;
+}
+
+int mlq_hip_stream_create(int device, void** stream) {
+    if (stream == nullptr) return fail(MLQ_ERR_INVALID, "mlq_hip_stream_create: null output");
+    *stream = nullptr;
+    int rc = ensure_device(device);
+    if (rc != MLQ_OK) return rc;
+    MLQ_HIP_CHECK(hipSetDevice(device));
+    hipStream_t s = nullptr;
+    MLQ_HIP_CHECK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));  // default priority
+    *stream = s;
+    return MLQ_OK;
+}
+
+int mlq_hip_stream_destroy(void* stream) {
+    if (stream == nullptr) return MLQ_OK;
+    MLQ_HIP_CHECK(hipStreamSynchronize(static_cast<hipStream_t>(stream)));
+    MLQ_HIP_CHECK(hipStreamDestroy(static_cast<hipStream_t>(stream)));
     return MLQ_OK;
 }
 

@@ -76,6 +76,8 @@ _SIGS = {
     "mlq_hip_memcpy_dtod": (ctypes.c_int, [_vp, _vp, ctypes.c_size_t, _vp]),
     "mlq_hip_memset": (ctypes.c_int, [_vp, ctypes.c_int, ctypes.c_size_t]),
     "mlq_hip_stream": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(_vp)]),
+    "mlq_hip_stream_create": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(_vp)]),
+    "mlq_hip_stream_destroy": (ctypes.c_int, [_vp]),
     "mlq_hip_synchronize": (ctypes.c_int, [_vp]),
     "mlq_hip_event_create": (ctypes.c_int, [ctypes.POINTER(_vp)]),
     "mlq_hip_event_destroy": (ctypes.c_int, [_vp]),
@@ -539,6 +541,17 @@ def stream(device: int = 0) -> int:
     s = _vp()
     _check(load().mlq_hip_stream(device, ctypes.byref(s)))
     return s.value
+
+
+def stream_create(device: int = 0) -> int:
+    """A new stream on ``device`` (release it with stream_destroy)."""
+    s = _vp()
+    _check(load().mlq_hip_stream_create(device, ctypes.byref(s)))
+    return s.value
+
+
+def stream_destroy(stream: int) -> None:
+    _check(load().mlq_hip_stream_destroy(stream))
 
 
 def synchronize(stream=None) -> None:

@@ -118,9 +118,18 @@ def test_greedy_generation_matches_reference(hip, orc, ref, tmp_path, name):
         toks = prompt + want[:i]
         for pos, t in enumerate(toks):
             logits = rd.forward(t, pos)
+        scale = max(1.0, float(np.abs(logits).max()))
         top = np.sort(logits)[-2:]
-        assert top[1] - top[0] <= TOL * max(1.0, float(np.abs(logits).max())), \
+        say(f"  {name}: divergence allowance used at token {i}: HIP {got[i]}, reference {want[i]}, "
+            f"reference top-2 gap {top[1] - top[0]:.3e}, HIP pick's logit {logits[got[i]]:.6g} "
+            f"vs max {logits.max():.6g}")
+        assert top[1] - top[0] <= TOL * scale, \
             f"{name}: token {i} is {got[i]}, reference {want[i]} (gap {top[1] - top[0]:.3e})"
+        # The HIP pick must itself be one of the (near-)maximal logits of the
+        # reference, not an arbitrary token.
+        assert logits[got[i]] >= logits.max() - TOL * scale, \
+            f"{name}: token {i}: HIP picked {got[i]} whose reference logit {logits[got[i]]:.6g} is not near " \
+            f"the maximum {logits.max():.6g}"
     dec.close()
 
 

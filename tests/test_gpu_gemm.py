@@ -73,3 +73,38 @@ def test_gemm_odd_block_count_uses_gemv_rows(hip, orc):
     for m, k, n in [(64, 4095, 5), (64, 100, 3), (48, 4128, 4)]:
         for fmt, qt in FMTS.items():
             run(hip, orc, qt, m, k, n)
+
+
+def test_graph_replay_after_workspace_growth(hip, orc):
+    """A graph recorded with a stream's batched-call workspace keeps working
+    after a larger eager call on the same stream grows that workspace (the old
+    buffer is retired, not freed): every replay equals the eager result bit
+    for bit."""
+    qt, m, k = oracle.Q4_0, 4096, 4096
+    rng = np.random.default_rng(77)
+    w = (rng.standard_normal((m, k), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+    blocks = orc.quantize(qt, w, threads=THREADS)
+    wt = hip.Weight.upload(qt, blocks, m, k)
+    sp = hip.stream_create(0)  # a stream with no workspace yet
+    x16 = hip.DeviceBuffer.from_array(rng.standard_normal((16, k), dtype=np.float32))
+    y16 = hip.DeviceBuffer(16 * m * 4)
+    x512 = hip.DeviceBuffer.from_array(rng.standard_normal((512, k), dtype=np.float32))
+    y512 = hip.DeviceBuffer(512 * m * 4)
+    print("gemm workspace growth: eager N=16, record, eager N=512, replays", flush=True)
+    wt.linear_device(x16, y16, rows=16, stream=sp)  # creates the stream's workspace (N=16 size)
+    hip.synchronize(sp)
+    want = y16.download(np.float32)
+    g = hip.Graph(hip.make_calls([(wt, x16, y16, 16)]), sp)
+    wt.linear_device(x512, y512, rows=512, stream=sp)  # grows the workspace
+    hip.synchronize(sp)
+    for i in range(3):
+        y16.fill(0)
+        g.launch(sp)
+        hip.synchronize(sp)
+        got = y16.download(np.float32)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"replay {i} differs"
+        wt.linear_device(x512, y512, rows=512, stream=sp)  # eager work between replays
+        hip.synchronize(sp)
+    g.destroy()
+    hip.stream_destroy(sp)
+    wt.free()
