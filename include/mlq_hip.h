@@ -107,6 +107,20 @@ int mlq_hip_weight_info(mlq_weight_t w, int* qtype, int* out_features, int* in_f
 int mlq_hip_quant_linear(mlq_weight_t w, const float* x, int rows, float* y, int flags,
                          void* stream);
 
+/* The device-pointer form of mlq_hip_quant_linear (MLQ_X_ON_DEVICE |
+ * MLQ_Y_ON_DEVICE | MLQ_ASYNC) that allocates nothing: batched calls
+ * (rows > 1) use a fixed 48 MiB scratch array the library holds on each GPU
+ * (from library set-up until the process ends) instead of the stream's
+ * workspace, so the call works under graph capture, in serving loops and in
+ * harnesses that forbid hipMalloc, from the first call on.  A shape whose GEMM
+ * needs more scratch is refused with MLQ_ERR_LIMIT (2048 token rows of a
+ * 4096x4096 weight fit, 4096 do not).  All calls on one GPU share the scratch: calls that
+ * overlap in time on one GPU (different streams, or a graph replayed while
+ * another runs) race and give wrong results.  Results equal
+ * mlq_hip_quant_linear bit for bit.  No counterpart in the reference; for
+ * callers that cannot allocate. */
+int mlq_hip_quant_linear_noalloc(mlq_weight_t w, const float* x, int rows, float* y, void* stream);
+
 /* Device-pointer form without a handle: cuda_q8_0/q4_0/q4_1_linear_device_input
  * (include/mini_llama/cuda_quant.h:30-86, src/cuda_quant.cu:289-496).  x and y
  * are device pointers on `device`; the call is asynchronous on `stream`. */

@@ -113,10 +113,19 @@ struct PickSlot {
     int32_t* token;
 };
 
+// Device memory of the no-allocation entry point (mlq_hip_quant_linear_noalloc):
+// the batched GEMM's workspace (split-K arrival counters, partial tiles, split
+// x) for callers that cannot allocate.  Each GPU the library runs on holds its
+// own copy until the process ends; host code uses the per-device address from
+// hipGetSymbolAddress (DeviceState::scratch), never the array's name.
+constexpr size_t kScratchBytes = size_t(48) << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
 struct DeviceState {
     std::once_flag once;
     hipError_t init_err = hipSuccess;
     hipStream_t stream = nullptr;
+    void* scratch = nullptr;   // this device's address of `scratch` (zeroed at set-up)
     std::mutex mu;             // guards the host-pointer staging buffers
     void* stage = nullptr;     // x and y staging for host-pointer calls
     size_t stage_bytes = 0;
@@ -167,6 +176,14 @@ int ensure_device(int device) {
             // Default priority, non-blocking with respect to the null stream.
             st.init_err = hipStreamCreateWithFlags(&st.stream, hipStreamNonBlocking);
         }
+        if (st.init_err == hipSuccess) {
+            // This device's copy of the no-allocation scratch: its address,
+            // then its split-K counters (and the rest) cleared once; every
+            // GEMM launch leaves the counters at zero again.
+            st.init_err = hipGetSymbolAddress(&st.scratch, HIP_SYMBOL(scratch));
+        }
+        if (st.init_err == hipSuccess) st.init_err = hipMemsetAsync(st.scratch, 0, kScratchBytes, st.stream);
+        if (st.init_err == hipSuccess) st.init_err = hipStreamSynchronize(st.stream);
     });
     if (st.init_err != hipSuccess) return hip_fail(st.init_err, "device init");
     e = hipSetDevice(device);
@@ -494,6 +511,36 @@ int mlq_hip_quant_linear_device(int device, int qtype, const void* device_blocks
     if ((rc = check_device_ptr(y, device, caller, "output", ybytes)) != MLQ_OK) return rc;
     mlq::LinearShape s{qtype, out_features, in_features, (in_features + 31) / 32, rows};
     return dispatch(device, s, device_blocks, x, y, resolve_stream(device, stream));
+}
+
+int mlq_hip_quant_linear_noalloc(mlq_weight_t w, const float* x, int rows, float* y, void* stream) {
+    if (w == nullptr) return fail(MLQ_ERR_INVALID, "hip_quant_linear: null weight handle");
+    const char* caller = caller_for(w->qtype);
+    int rc = validate_linear(w->qtype, w->M, w->K, w->n_blocks, rows);
+    if (rc != MLQ_OK) return rc;
+    rc = ensure_device(w->device);
+    if (rc != MLQ_OK) return rc;
+    const size_t xb = static_cast<size_t>(rows) * w->K * sizeof(float);
+    const size_t yb = static_cast<size_t>(rows) * w->M * sizeof(float);
+    if ((rc = check_device_ptr(x, w->device, caller, "input", xb)) != MLQ_OK) return rc;
+    if ((rc = check_device_ptr(y, w->device, caller, "output", yb)) != MLQ_OK) return rc;
+    mlq::LinearShape s{w->qtype, w->M, w->K, w->nb, rows};
+    const hipStream_t st = resolve_stream(w->device, stream);
+    hipError_t e;
+    if (rows > 1 && mlq::gemm_supported(s)) {
+        const size_t need = mlq::gemm_workspace_bytes(s);
+        if (need > kScratchBytes) {
+            return fail(MLQ_ERR_LIMIT, std::string(caller) + ": the no-allocation entry point has " +
+                                           std::to_string(kScratchBytes) + " bytes of scratch; " +
+                                           std::to_string(rows) + " rows of this weight need " +
+                                           std::to_string(need) + " (use mlq_hip_quant_linear)");
+        }
+        e = mlq::launch_gemm(s, w->ptr, x, y, g_dev[w->device].scratch, need, st);
+    } else {
+        e = mlq::launch_gemv(s, w->ptr, x, y, st);  // no scratch
+    }
+    if (e != hipSuccess) return hip_fail(e, caller);
+    return MLQ_OK;
 }
 
 int mlq_hip_quant_linear(mlq_weight_t w, const float* x, int rows, float* y, int flags,

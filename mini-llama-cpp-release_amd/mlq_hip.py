@@ -62,6 +62,7 @@ _SIGS = {
                                             ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_size_t),
                                             ctypes.POINTER(_vp), ctypes.POINTER(ctypes.c_int)]),
     "mlq_hip_quant_linear": (ctypes.c_int, [_vp, _vp, ctypes.c_int, _vp, ctypes.c_int, _vp]),
+    "mlq_hip_quant_linear_noalloc": (ctypes.c_int, [_vp, _vp, ctypes.c_int, _vp, _vp]),
     "mlq_hip_quant_linear_device": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, _vp, ctypes.c_size_t,
                                                     ctypes.c_int, ctypes.c_int, _vp, ctypes.c_int, _vp, _vp]),
     "mlq_hip_quant_linear_many": (ctypes.c_int, [ctypes.POINTER(LinearCall), ctypes.c_int, _vp]),
@@ -258,6 +259,11 @@ class Weight:
                       sync: bool = True) -> None:
         flags = X_ON_DEVICE | Y_ON_DEVICE | (0 if sync else ASYNC)
         _check(_LIB.mlq_hip_quant_linear(self.h, x.ptr, rows, y.ptr, flags, stream))
+
+    def linear_noalloc(self, x: DeviceBuffer, y: DeviceBuffer, rows: int = 1, stream=None) -> None:
+        """mlq_hip_quant_linear_noalloc: device x / y, asynchronous on `stream`,
+        the library's fixed scratch instead of an allocated workspace."""
+        _check(_LIB.mlq_hip_quant_linear_noalloc(self.h, x.ptr, rows, y.ptr, stream))
 
     def linear_argmax(self, x: DeviceBuffer, y: "DeviceBuffer | None", token: DeviceBuffer,
                       stream=None) -> None:
