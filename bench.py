@@ -221,6 +221,34 @@ def cpu_sweep_check(sw: Sweep, threads: int, runs: int = 3):
     }
 
 
+def floor_bench(sw: Sweep, stream, steps: int, warmup: int):
+    """The sweep's 129 stages as weight-stream-only launches (mlq_hip_stream_floor:
+    the GEMV kernels' grid, work units and request ring, no arithmetic),
+    recorded as one graph like the headline: the floor that one launch per
+    stage pays for launching and streaming the weights."""
+    ids = sw.stage_ids()
+    groups, i = [], 0
+    while i < len(ids):
+        j = i + 1
+        while j < len(ids) and ids[j] == ids[i]:
+            j += 1
+        groups.append(hip.make_calls([(w, x, y, 1) for (_, w, x, y) in sw.calls_desc[i:j]]))
+        i = j
+    sink = hip.DeviceBuffer(4 * 65536)
+    graph = hip.Graph.record(lambda: [hip.stream_floor(g, sink, stream) for g in groups], stream,
+                             keep=(groups, sink))
+    for _ in range(warmup):
+        graph.launch(stream)
+    ms = time_region(lambda: graph.launch(stream), steps, stream) / steps
+    graph.destroy()
+    sink.free()
+    return {"launches": len(groups), "us_per_step": round(ms * 1e3, 1),
+            "gbs": round(sw.bytes / (ms * 1e-3) / 1e9, 1),
+            "us_per_launch": round(ms * 1e3 / len(groups), 3),
+            "note": "mlq_hip_stream_floor per stage (weights streamed with the GEMV grid and ring, no "
+                    "arithmetic), one graph of the same 129 dependent launches as per_stage"}
+
+
 # ------------------------------------------------------------------ per-shape GEMV
 GEMV_CONFIGS = (
     [("c1_qwen_ffn_up", hip.Q8_0, 4864, 896)] +
@@ -600,6 +628,83 @@ def gemm_shape_bench(qt, m, k, n, stream, reps_target=100):
 _JSON_FD = None
 
 
+STAGE_NAMES = ("q/k/v fused 12288x4096", "o 4096x4096", "gate/up fused 22016x4096", "down 4096x11008")
+
+
+def profile_summary(path: str, steps: int, stages: int = 129) -> None:
+    """Per-stage table of a rocprofv3 CSV output directory (`-f csv`) of a
+    `--no-shapes --no-cpu --no-variants --launch per_stage` run: the last
+    `steps` x `stages` dispatches of the GEMV kernels and of the stream floor
+    kernel, i.e. the timed steps of each leg (each leg runs its warm-up steps
+    before its timed ones).  A kernel trace gives durations; a counter
+    collection gives each counter's mean per dispatch.  Returns the text."""
+    import csv
+    import glob
+    import statistics
+
+    lines = []
+    out = lines.append
+
+    def family(name):
+        if "gemv_single" in name or "gemv_multi" in name:
+            return "gemv"
+        return "floor" if "stream_floor" in name else None
+
+    def short(name):
+        return name.replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0]
+
+    def stage(i):
+        return "lm_head 32000x4096" if i % stages == stages - 1 else STAGE_NAMES[(i % stages) % 4]
+
+    last = steps * stages
+    trace = glob.glob(os.path.join(path, "**", "*kernel_trace.csv"), recursive=True)
+    counters = glob.glob(os.path.join(path, "**", "*counter_collection.csv"), recursive=True)
+    if trace:
+        rows = sorted(csv.DictReader(open(trace[0])), key=lambda r: int(r["Start_Timestamp"]))
+        for fam in ("gemv", "floor"):
+            sel = [r for r in rows if family(r["Kernel_Name"]) == fam][-last:]
+            if len(sel) < last:
+                continue
+            out(f"\n{fam}: last {len(sel)} dispatches ({steps} steps)\n")
+            out("| kernel | stage | dispatches | avg us | median us | min us | max us |")
+            out("|---|---|---|---|---|---|---|")
+            by = {}
+            for i, r in enumerate(sel):
+                key = (short(r["Kernel_Name"]), stage(i))
+                by.setdefault(key, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+            total = 0.0
+            for (k, st), v in by.items():
+                total += sum(v)
+                out(f"| {k} | {st} | {len(v)} | {statistics.mean(v):.3f} | {statistics.median(v):.3f} | "
+                      f"{min(v):.3f} | {max(v):.3f} |")
+            out(f"\nkernel time per step {total / steps:.1f} us, {total / len(sel):.3f} us per launch")
+    if counters:
+        per = {}
+        for r in csv.DictReader(open(counters[0])):
+            per.setdefault(int(r["Dispatch_Id"]), [r["Kernel_Name"], {}])[1][r["Counter_Name"]] = float(r["Counter_Value"])
+        ids = sorted(per)
+        for fam in ("gemv", "floor"):
+            sel = [i for i in ids if family(per[i][0]) == fam][-last:]
+            if len(sel) < last:
+                continue
+            names = sorted(per[sel[0]][1])
+            out(f"\n{fam}: last {len(sel)} dispatches ({steps} steps), mean per dispatch\n")
+            out("| kernel | stage | dispatches | " + " | ".join(names) + " |")
+            out("|---|---|---|" + "---|" * len(names))
+            by = {}
+            for j, i in enumerate(sel):
+                by.setdefault((short(per[i][0]), stage(j)), []).append(per[i][1])
+            for (k, st), v in by.items():
+                out(f"| {k} | {st} | {len(v)} | " +
+                      " | ".join(f"{statistics.mean(d[n] for d in v):.1f}" for n in names) + " |")
+        copies = [per[i][1] for i in ids if "copyBuffer" in per[i][0]]
+        if copies:
+            big = max(copies, key=lambda d: sum(d.values()))
+            out("\nlargest __amd_rocclr_copyBuffer dispatch (the calibration copy): " +
+                  ", ".join(f"{n} {v:.1f}" for n, v in sorted(big.items())))
+    return "\n".join(lines) + "\n"
+
+
 def emit(obj):
     """Writes the one JSON line to the process's original stdout.  main()
     points fd 1 at stderr first: C code loaded here (the reference's GGUF
@@ -636,7 +741,13 @@ def main():
                     help="run only the prefill GEMM table (config 4) and print it as one JSON line")
     ap.add_argument("--gemm-filter", default="",
                     help="with --gemm-only: keep the configs named fmt:M:N (comma-separated, e.g. q4_0:4096:64)")
+    ap.add_argument("--profile-summary", default="",
+                    help="print per-stage tables of this rocprofv3 CSV output directory (of a --launch "
+                         "per_stage --no-variants run with the same --steps) and exit; no GPU use")
     args = ap.parse_args()
+    if args.profile_summary:
+        os.write(_JSON_FD, profile_summary(args.profile_summary, args.steps).encode())
+        return
     if args.gemm_only:
         hip.load()
         hip.init(0)
@@ -728,6 +839,10 @@ def main():
     ms = time_region(step, args.steps, stream)
     ms_step = ms / args.steps
     gbs = sw.bytes / (ms_step * 1e-3) / 1e9
+    floor = floor_bench(sw, stream, args.steps, args.warmup)
+    if floor:
+        log(f"sweep floor (weights only, one launch per stage): {floor['us_per_step']:8.1f} us/step, "
+            f"{floor['gbs']:8.1f} GB/s")
     seq_info = seqs["sequence"].info()
     launches = {"graph": sw.n(), "plain": sw.n(), "per_stage": seqs["per_stage"].info()["launches"],
                 "sequence": seq_info["launches"], "independent": seqs["independent"].info()["launches"]}[args.launch]
@@ -813,7 +928,8 @@ def main():
                    "calls_per_step": sw.n(), "stages_per_step": seq_info["stages"],
                    "bytes_per_step": sw.bytes, "launch": args.launch,
                    "sweep_us": round(ms_step * 1e3, 1),
-                   "sweep_us_by_launch": {k: round(v * 1e3, 1) for k, v in variants.items()}},
+                   "sweep_us_by_launch": {k: round(v * 1e3, 1) for k, v in variants.items()},
+                   "per_stage_floor": floor},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(args.launch),
                      "algorithmic_bytes_per_launch": round(sw.bytes / launches),

@@ -147,6 +147,14 @@ int mlq_hip_quant_linear_many(const mlq_linear_call* calls, int n, void* stream)
  * src/forward.cpp:172-227).  Asynchronous on `stream`. */
 int mlq_hip_quant_linear_fused(const mlq_linear_call* calls, int n, void* stream);
 
+/* Measurement, not a linear: streams exactly the weights a fused launch of
+ * `calls` (as mlq_hip_quant_linear_fused; x and y are ignored) would read,
+ * with the GEMV kernels' grid, work units and request ring, and no
+ * arithmetic; `sink` is a device buffer of 65536 words it overwrites.  Its
+ * time is the floor of a GEMV launch of that shape (launch plus weight
+ * stream).  Asynchronous on `stream`. */
+int mlq_hip_stream_floor(const mlq_linear_call* calls, int n, void* sink, void* stream);
+
 /* Greedy pick fused into the decode GEMV of an output projection (lm_head):
  * y = W x as mlq_hip_quant_linear (bit for bit; y may be NULL when the logits
  * are not needed) and *token = the first index of the largest y, or -1 when

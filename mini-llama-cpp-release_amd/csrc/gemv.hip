@@ -602,6 +602,60 @@ hipError_t launch_mode(const LinearShape& s, const GemvGroup& g, const float* x,
     }
 }
 
+// ---------------------------------------------------------------------------
+// Measurement kernel (not a GEMV): the weight stream of a grouped decode GEMV
+// launch with no arithmetic.  The grid (one persistent workgroup of 8 waves
+// per CU), the work units (row item x chunk of LPR pairs, each lane one pair
+// of 9 / 17 / 10 dwords), the dealing of items to waves and the ring of D
+// units requested ahead are those of the GEMV kernels; each lane folds the
+// dwords it loads into one XOR, stored at the end so no load is dropped.  Its
+// time is the floor a GEMV launch of that shape pays for launching and for
+// streaming its weights.
+template <int QT, int LPR, int D>
+__global__ __launch_bounds__(kWaves * 64, 2) void stream_floor_kernel(const GemvGroup g, int M, int nb, int items,
+                                                                      uint32_t* __restrict__ sink) {
+    constexpr int DW = Fmt<QT>::DW;
+    constexpr int SUB = 64 / LPR;
+    const int np = nb >> 1;
+    const int nch = (np + LPR - 1) / LPR;
+    const int lane = threadIdx.x & 63;
+    const int slot = lane / LPR;
+    const int pl = lane % LPR;
+    const size_t row_dw = static_cast<size_t>(np) * DW;
+    const int GW = gridDim.x * kWaves;
+    const int gw = blockIdx.x * kWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nu = gw < items ? (items - gw + GW - 1) / GW * nch : 0;
+    int pit = gw, pc = 0;  // the next unit to request (past the end: the last one again)
+    auto request = [&](uint32_t (&w)[DW]) {
+        const int row = min(min(pit, items - 1) * SUB + slot, M - 1);
+        const uint32_t* src = group_row(g, row, row_dw) + static_cast<size_t>(min(pc * LPR + pl, np - 1)) * DW;
+#pragma unroll
+        for (int i = 0; i < DW; ++i) w[i] = src[i];
+        if (++pc == nch) {
+            pc = 0;
+            pit += GW;
+        }
+    };
+    uint32_t wq[D][DW];
+#pragma unroll
+    for (int k = 0; k < D; ++k) request(wq[k]);
+    uint32_t acc = 0;
+    auto step = [&](uint32_t (&w)[DW]) {
+#pragma unroll
+        for (int i = 0; i < DW; ++i) acc ^= w[i];
+        request(w);
+    };
+    int u = 0;
+    for (; u + D <= nu; u += D) {
+#pragma unroll
+        for (int k = 0; k < D; ++k) step(wq[k]);
+    }
+#pragma unroll
+    for (int k = 0; k < D; ++k)
+        if (u + k < nu) step(wq[k]);
+    sink[(static_cast<size_t>(gw) * 64 + lane) & (kFloorSinkWords - 1)] = acc;
+}
+
 }  // namespace
 
 hipError_t launch_gemv_group(const LinearShape& s, const GemvGroup& g, const float* x, hipStream_t stream) {
@@ -680,6 +734,42 @@ hipError_t launch_gemv(const LinearShape& s, const void* w, const float* x, floa
     g.y[0] = y;
     g.ncalls = 1;
     return launch_gemv_group(s, g, x, stream);
+}
+
+hipError_t launch_stream_floor(const LinearShape& s, const GemvGroup& g, uint32_t* sink, hipStream_t stream) {
+    if (g.ncalls < 1 || g.ncalls > kGroupMaxCalls || s.nb % 2 != 0 || sink == nullptr) return hipErrorInvalidValue;
+    const int np = s.nb / 2;
+    int lpr = 16;
+    if (np > 16) lpr = 64;
+    if (np > 64) {
+        lpr = 16;
+        for (int l : {64, 32, 16}) {
+            const int iters = (np + l - 1) / l;
+            if (static_cast<double>(np) / (static_cast<double>(l) * iters) >= 0.875) {
+                lpr = l;
+                break;
+            }
+        }
+    }
+    const int items = (s.M + (64 / lpr) - 1) / (64 / lpr);
+    int grid = (items + kWaves - 1) / kWaves;
+    if (grid > kPersistentWgs) grid = kPersistentWgs;
+    auto go = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, dim3(grid), dim3(kWaves * 64), 0, stream, g, s.M, s.nb, items, sink);
+        return hipGetLastError();
+    };
+    switch (s.qtype * 100 + lpr) {
+        case 116: return go(stream_floor_kernel<1, 16, 2>);
+        case 132: return go(stream_floor_kernel<1, 32, 2>);
+        case 164: return go(stream_floor_kernel<1, 64, 2>);
+        case 216: return go(stream_floor_kernel<2, 16, 3>);
+        case 232: return go(stream_floor_kernel<2, 32, 3>);
+        case 264: return go(stream_floor_kernel<2, 64, 3>);
+        case 316: return go(stream_floor_kernel<3, 16, 3>);
+        case 332: return go(stream_floor_kernel<3, 32, 3>);
+        case 364: return go(stream_floor_kernel<3, 64, 3>);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 const char* gemv_kernel_name(const LinearShape& s) {

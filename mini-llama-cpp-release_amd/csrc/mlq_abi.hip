@@ -673,6 +673,42 @@ int mlq_hip_quant_linear_fused(const mlq_linear_call* calls, int n, void* stream
     return MLQ_OK;
 }
 
+int mlq_hip_stream_floor(const mlq_linear_call* calls, int n, void* sink, void* stream) {
+    static const char* caller = "mlq_hip_stream_floor";
+    if (calls == nullptr || n <= 0) return fail(MLQ_ERR_INVALID, std::string(caller) + ": no calls");
+    if (n > mlq::kGroupMaxCalls) {
+        return fail(MLQ_ERR_LIMIT, std::string(caller) + ": " + std::to_string(n) + " calls (at most " +
+                                       std::to_string(mlq::kGroupMaxCalls) + ")");
+    }
+    if (calls[0].w == nullptr) return fail(MLQ_ERR_INVALID, std::string(caller) + ": null weight handle");
+    const mlq_weight_s* w0 = calls[0].w;
+    const int device = w0->device;
+    int rc = ensure_device(device);
+    if (rc != MLQ_OK) return rc;
+    if ((rc = check_device_ptr(sink, device, caller, "sink", size_t(mlq::kFloorSinkWords) * 4)) != MLQ_OK) return rc;
+    if (w0->nb % 2 != 0) return fail(MLQ_ERR_INVALID, std::string(caller) + ": needs an even block count");
+    mlq::GemvGroup g{};
+    long long rows = 0;
+    for (int i = 0; i < n; ++i) {
+        const mlq_linear_call& c = calls[i];
+        const std::string at = std::string(caller) + ": call " + std::to_string(i);
+        if (c.w == nullptr) return fail(MLQ_ERR_INVALID, at + ": null weight handle");
+        if (c.w->device != device) return fail(MLQ_ERR_DEVICE, at + ": weight on a different device");
+        if (c.w->K != w0->K || c.w->qtype != w0->qtype) {
+            return fail(MLQ_ERR_INVALID, at + ": differs from call 0 in in_features or quant type");
+        }
+        g.W[i] = c.w->ptr;
+        g.row_begin[i] = static_cast<int>(rows);
+        rows += c.w->M;
+    }
+    if (rows > (1ll << 30)) return fail(MLQ_ERR_LIMIT, std::string(caller) + ": too many rows");
+    g.ncalls = n;
+    mlq::LinearShape shape{w0->qtype, static_cast<int>(rows), w0->K, w0->nb, 1};
+    hipError_t e = mlq::launch_stream_floor(shape, g, static_cast<uint32_t*>(sink), resolve_stream(device, stream));
+    if (e != hipSuccess) return hip_fail(e, caller);
+    return MLQ_OK;
+}
+
 namespace {
 
 // Shared front of the two greedy-pick entries: validates, then launches the

@@ -91,6 +91,12 @@ hipError_t launch_gemv_glu(const LinearShape& s, const GemvGroup& g, const float
 hipError_t launch_gemv_pick_norm(const LinearShape& s, const void* w, const float* x, const float* norm_w,
                                  float norm_eps, float* y, PickState* ps, int32_t* token, hipStream_t stream);
 
+// Measurement: the weight stream of a grouped GEMV launch (same grid, units
+// and ring) without the arithmetic -- the per-launch floor.  `sink` holds
+// kFloorSinkWords words the kernel overwrites.
+constexpr int kFloorSinkWords = 1 << 16;
+hipError_t launch_stream_floor(const LinearShape& s, const GemvGroup& g, uint32_t* sink, hipStream_t stream);
+
 // Batched prefill GEMM for rows > 1 (MFMA).  Needs a device workspace of
 // gemm_workspace_bytes(s) bytes (split x, scales, split-K partials) that no
 // other launch uses concurrently.  Returns hipErrorNotSupported when the shape

@@ -63,6 +63,7 @@ _SIGS = {
                                             ctypes.POINTER(_vp), ctypes.POINTER(ctypes.c_int)]),
     "mlq_hip_quant_linear": (ctypes.c_int, [_vp, _vp, ctypes.c_int, _vp, ctypes.c_int, _vp]),
     "mlq_hip_quant_linear_noalloc": (ctypes.c_int, [_vp, _vp, ctypes.c_int, _vp, _vp]),
+    "mlq_hip_stream_floor": (ctypes.c_int, [ctypes.POINTER(LinearCall), ctypes.c_int, _vp, _vp]),
     "mlq_hip_quant_linear_device": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, _vp, ctypes.c_size_t,
                                                     ctypes.c_int, ctypes.c_int, _vp, ctypes.c_int, _vp, _vp]),
     "mlq_hip_quant_linear_many": (ctypes.c_int, [ctypes.POINTER(LinearCall), ctypes.c_int, _vp]),
@@ -323,6 +324,12 @@ def make_calls(calls) -> ctypes.Array:
 
 def linear_many(arr: ctypes.Array, stream=None) -> None:
     _check(load().mlq_hip_quant_linear_many(arr, len(arr), stream))
+
+
+def stream_floor(arr: ctypes.Array, sink: "DeviceBuffer", stream=None) -> None:
+    """mlq_hip_stream_floor: the weight stream of a fused launch of `arr`,
+    without the arithmetic (a measurement of the per-launch floor)."""
+    _check(load().mlq_hip_stream_floor(arr, len(arr), sink.ptr, stream))
 
 
 def linear_fused(arr: ctypes.Array, stream=None) -> None:

@@ -301,3 +301,22 @@ def test_fused_validation(hip):
         fused([(l1.w, x, x, 1)])
     with pytest.raises(hip.MlqError, match="rows must be 1"):
         fused([(l1.w, x, y[0], 2)])
+
+
+def test_stream_floor_runs_and_validates(hip):
+    """mlq_hip_stream_floor (the weight stream of a fused launch without the
+    arithmetic, a measurement) accepts the fused group shapes and refuses a
+    sink that is too small or mixed in_features."""
+    qkv = [Lin(hip, oracle.Q4_0, 4096, 4096, 60 + i) for i in range(3)]
+    down = Lin(hip, oracle.Q4_0, 4096, 11008, 63)
+    x = vec(hip, 4096, 64)
+    y = hip.DeviceBuffer(4 * 4096)
+    sink = hip.DeviceBuffer(4 * 65536)
+    for calls in ([(l.w, x, y, 1) for l in qkv], [(down.w, x, y, 1)]):
+        hip.stream_floor(hip.make_calls(calls), sink)
+    hip.synchronize()
+    small = hip.DeviceBuffer(1024)
+    with pytest.raises(hip.MlqError, match="sink"):
+        hip.stream_floor(hip.make_calls([(qkv[0].w, x, y, 1)]), small)
+    with pytest.raises(hip.MlqError, match="differs from call 0"):
+        hip.stream_floor(hip.make_calls([(qkv[0].w, x, y, 1), (down.w, x, y, 1)]), sink)
