@@ -262,7 +262,13 @@ __global__ __launch_bounds__(WAVES * 64, 2) void gemv_single_kernel(const GemvGr
             request(g0 + k * gstride, wq[k], rq[k]);
         }
     };
+    // x first: every wave of the workgroup has issued its x loads before any
+    // wave requests weights (a bare barrier, no memory wait), so the CU's
+    // memory queue serves x ahead of the weight misses.  With the weights
+    // first, x came back only after ~3 us at the start of a launch on MI355X
+    // (queued behind other waves' misses); x first: the 7B sweep 1028 -> 1000 us.
     stage_x<QT, false, Mode<MODE>::norm, 1, true>(x, K, nb, xl, xc, g.norm_w, g.norm_eps, [&] {
+        __builtin_amdgcn_s_barrier();
 #pragma unroll
         for (int k = 0; k < PRE; ++k) request_slot(k);
     });
@@ -391,7 +397,9 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_multi_kernel(const GemvGroup 
         }
     };
     static_assert(PRE >= 1 && PRE <= D, "ring units requested before staging");
+    // x first (see the single kernel): every thread reaches this callback once.
     stage_x_fit<QT, false, Mode<MODE>::norm>(x, K, nb, xl, xc, g.norm_w, g.norm_eps, [&] {
+        __builtin_amdgcn_s_barrier();
 #pragma unroll
         for (int k = 0; k < PRE; ++k) request(wq[k], rq[k]);
     });
