@@ -676,24 +676,26 @@ hipError_t launch_gemv_glu(const LinearShape& s, const GemvGroup& g, const float
         return hipErrorInvalidValue;
     const PairCfg c = choose_pair(s);
     if (c.kind != Kind::Single) return hipErrorNotSupported;
-    // A unit is two rows (gate and up): one unit in flight per wave and two
-    // workgroups per CU measured fastest (11008x4096 Q4_0: 11.8 us, against
-    // 12.0 us for the gate/up launch alone and 13.4-17.2 us for deeper rings).
-    auto go = [&](auto kernel, int lpr) {
+    // A unit is two rows (gate and up).  Q4: two units in flight per wave and
+    // one workgroup per CU measured fastest (LLaMA-7B-shaped Q4_0 greedy decode
+    // 727 -> 737 tokens/s; one unit and two workgroups per CU had been best
+    // before x was loaded ahead of the weights; three units: 717).  Q8_0 keeps
+    // one unit (its 17-dword pairs would not fit two units in 128 VGPRs).
+    auto go = [&](auto kernel, int lpr, int wgs_per_cu) {
         const int groups = (s.M + (64 / lpr) - 1) / (64 / lpr);
         int grid = (groups + kWaves - 1) / kWaves;
-        if (grid > 2 * kPersistentWgs) grid = 2 * kPersistentWgs;
+        if (grid > wgs_per_cu * kPersistentWgs) grid = wgs_per_cu * kPersistentWgs;
         hipLaunchKernelGGL(kernel, dim3(grid, s.rows), dim3(kWaves * 64), pair_lds_bytes(s.qtype, s.nb), stream, g, x,
                            s.M, s.K, s.nb, groups);
         return hipGetLastError();
     };
     switch (s.qtype * 100 + c.lpr) {
-        case 116: return go(gemv_single_kernel<1, 16, kWaves, 1, kModeNormGlu>, 16);
-        case 164: return go(gemv_single_kernel<1, 64, kWaves, 1, kModeNormGlu>, 64);
-        case 216: return go(gemv_single_kernel<2, 16, kWaves, 1, kModeNormGlu>, 16);
-        case 264: return go(gemv_single_kernel<2, 64, kWaves, 1, kModeNormGlu>, 64);
-        case 316: return go(gemv_single_kernel<3, 16, kWaves, 1, kModeNormGlu>, 16);
-        case 364: return go(gemv_single_kernel<3, 64, kWaves, 1, kModeNormGlu>, 64);
+        case 116: return go(gemv_single_kernel<1, 16, kWaves, 1, kModeNormGlu>, 16, 2);
+        case 164: return go(gemv_single_kernel<1, 64, kWaves, 1, kModeNormGlu>, 64, 2);
+        case 216: return go(gemv_single_kernel<2, 16, kWaves, 2, kModeNormGlu>, 16, 1);
+        case 264: return go(gemv_single_kernel<2, 64, kWaves, 2, kModeNormGlu>, 64, 1);
+        case 316: return go(gemv_single_kernel<3, 16, kWaves, 2, kModeNormGlu>, 16, 1);
+        case 364: return go(gemv_single_kernel<3, 64, kWaves, 2, kModeNormGlu>, 64, 1);
         default: return hipErrorInvalidValue;
     }
 }
