@@ -903,13 +903,18 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_chunk_kernel(const ChunkArg
     // flight.  Requests past the last chunk re-read the last chunk (L2 hits),
     // so that every load is unconditional and can be counted exactly.
     const int clast = nchunk - 1;
+    // x first: every wave requests the first x chunk before any wave requests
+    // weights (a bare barrier, no memory wait), so the CU's memory queue serves
+    // x ahead of the weight misses and x is split while the weights arrive
+    // (4096 x 4096 Q4_0: N = 16 13.0 -> 12.0 us, N = 64 20.4 -> 19.9 us).
+    load_x(0);
+    __builtin_amdgcn_s_barrier();
     load_w(0, wreg[0]);
 #pragma unroll
     for (int k = 1; k < P; ++k) load_w(min(k, clast), wreg[k]);
-    load_x(0);
-    store_w(wreg[0], 0);
     put_x(0);
     load_x(min(1, clast));
+    store_w(wreg[0], 0);
     __builtin_amdgcn_sched_barrier(0);
     load_w(min(P, clast), wreg[0]);
     __syncthreads();
