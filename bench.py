@@ -705,6 +705,71 @@ def profile_summary(path: str, steps: int, stages: int = 129) -> None:
     return "\n".join(lines) + "\n"
 
 
+def kernel_summary(path: str, match=("gemm_", "xsplit_kernel")) -> str:
+    """Per-kernel table of a rocprofv3 CSV output directory (`-f csv`) of a
+    `--gemm-only` run: every dispatch of each kernel whose name contains one
+    of `match`, grouped by full kernel name (template arguments included);
+    durations from a kernel trace, each counter's mean per dispatch from a
+    counter collection, and the largest copyBuffer dispatch (the
+    `--calibration-copy-mb` copy) for scaling byte counters.  Returns the text."""
+    import csv
+    import glob
+    import statistics
+
+    lines = []
+    out = lines.append
+
+    def short(name):
+        return name.replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0]
+
+    trace = glob.glob(os.path.join(path, "**", "*kernel_trace.csv"), recursive=True)
+    counters = glob.glob(os.path.join(path, "**", "*counter_collection.csv"), recursive=True)
+    if trace:
+        by = {}
+        for r in csv.DictReader(open(trace[0])):
+            if any(m in r["Kernel_Name"] for m in match):
+                by.setdefault(short(r["Kernel_Name"]), []).append(
+                    (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+        out("| kernel | dispatches | avg us | median us | min us | max us |")
+        out("|---|---|---|---|---|---|")
+        for k, v in by.items():
+            out(f"| {k} | {len(v)} | {statistics.mean(v):.3f} | {statistics.median(v):.3f} | "
+                f"{min(v):.3f} | {max(v):.3f} |")
+    if counters:
+        per = {}
+        for r in csv.DictReader(open(counters[0])):
+            per.setdefault(int(r["Dispatch_Id"]), [r["Kernel_Name"], {}])[1][r["Counter_Name"]] = float(r["Counter_Value"])
+        by = {}
+        for i in sorted(per):
+            if any(m in per[i][0] for m in match):
+                by.setdefault(short(per[i][0]), []).append(per[i][1])
+        if by:
+            names = sorted(next(iter(by.values()))[0])
+            out("\n| kernel | dispatches | " + " | ".join(names) + " |")
+            out("|---|---|" + "---|" * len(names))
+            for k, v in by.items():
+                out(f"| {k} | {len(v)} | " + " | ".join(f"{statistics.mean(d.get(n, 0.0) for d in v):.1f}"
+                                                        for n in names) + " |")
+        copies = [d for name, d in per.values() if "copyBuffer" in name]
+        if copies:
+            big = max(copies, key=lambda d: sum(d.values()))
+            out("\nlargest __amd_rocclr_copyBuffer dispatch (the calibration copy): " +
+                ", ".join(f"{n} {v:.1f}" for n, v in sorted(big.items())))
+    return "\n".join(lines) + "\n"
+
+
+def calibration_copy(mb: int, stream) -> None:
+    """One device-to-device copy of `mb` MiB: a dispatch of known traffic
+    against which a profiler's byte counters are scaled."""
+    nbytes = mb << 20
+    src, dst = hip.DeviceBuffer(nbytes), hip.DeviceBuffer(nbytes)
+    hip.load().mlq_hip_memcpy_dtod(dst.ptr, src.ptr, nbytes, stream)
+    hip.synchronize(stream)
+    log(f"calibration copy: {nbytes} bytes read and written")
+    src.free()
+    dst.free()
+
+
 def emit(obj):
     """Writes the one JSON line to the process's original stdout.  main()
     points fd 1 at stderr first: C code loaded here (the reference's GGUF
@@ -744,15 +809,23 @@ def main():
     ap.add_argument("--profile-summary", default="",
                     help="print per-stage tables of this rocprofv3 CSV output directory (of a --launch "
                          "per_stage --no-variants run with the same --steps) and exit; no GPU use")
+    ap.add_argument("--kernel-summary", default="",
+                    help="print per-kernel tables (GEMM and x split) of this rocprofv3 CSV output "
+                         "directory (of a --gemm-only run) and exit; no GPU use")
     args = ap.parse_args()
     if args.profile_summary:
         os.write(_JSON_FD, profile_summary(args.profile_summary, args.steps).encode())
+        return
+    if args.kernel_summary:
+        os.write(_JSON_FD, kernel_summary(args.kernel_summary).encode())
         return
     if args.gemm_only:
         hip.load()
         hip.init(0)
         stream = hip.stream(0)
         keep = {f for f in args.gemm_filter.split(",") if f}
+        if args.calibration_copy_mb > 0:
+            calibration_copy(args.calibration_copy_mb, stream)
         rows = []
         for cfg in GEMM_CONFIGS:
             qt, m, _, n = cfg
@@ -789,13 +862,7 @@ def main():
     log(f"sweep ready: {sw.n()} calls, {sw.bytes / 1e9:.3f} GB, setup {time.time() - t0:.1f}s")
 
     if args.calibration_copy_mb > 0:
-        nbytes = args.calibration_copy_mb << 20
-        src, dst = hip.DeviceBuffer(nbytes), hip.DeviceBuffer(nbytes)
-        hip.load().mlq_hip_memcpy_dtod(dst.ptr, src.ptr, nbytes, stream)
-        hip.synchronize(stream)
-        log(f"calibration copy: {nbytes} bytes read and written")
-        src.free()
-        dst.free()
+        calibration_copy(args.calibration_copy_mb, stream)
 
     # Every way of running the sweep; `--launch` picks the headline.
     #   graph / plain: one launch per call (225), captured as a graph or issued from C;

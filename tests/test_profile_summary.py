@@ -58,3 +58,38 @@ def test_timed_dispatches_and_stages(tmp_path):
 def test_too_few_dispatches_prints_nothing(tmp_path):
     _trace(tmp_path / "kt_kernel_trace.csv", warm=0, timed=1)
     assert "| mlq::" not in bench.profile_summary(str(tmp_path), steps=2)
+
+
+GEMM = "void mlq::(anonymous namespace)::gemm_chunk_kernel<2, 2, 2, 2, true>(mlq::(anonymous namespace)::ChunkArgs)"
+XSPLIT = "void mlq::(anonymous namespace)::xsplit_kernel<2>(float const*, int, int, int, int, _Float16*, float*, float*)"
+COPY = "__amd_rocclr_copyBuffer"
+
+
+def test_kernel_summary_groups_gemm_kernels(tmp_path):
+    """bench.py --kernel-summary: every dispatch of the GEMM and x-split kernels
+    grouped by name (other kernels left out), mean counters per dispatch, and
+    the largest copy reported for calibrating byte counters."""
+    rows, t = [], 0
+    for name, dur in [(XSPLIT, 7), (GEMM, 60), (GEMV, 5), (XSPLIT, 9), (GEMM, 62)]:
+        rows.append({"Kernel_Name": name, "Start_Timestamp": t, "End_Timestamp": t + dur * 1000})
+        t += dur * 1000 + 100
+    with open(tmp_path / "kt_kernel_trace.csv", "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=["Kernel_Name", "Start_Timestamp", "End_Timestamp"])
+        w.writeheader()
+        w.writerows(rows)
+    crow = [(1, COPY, 1048576.0), (2, COPY, 10.0), (3, GEMM, 100.0), (4, GEMM, 300.0), (5, XSPLIT, 50.0),
+            (6, GEMV, 7.0)]
+    with open(tmp_path / "c_counter_collection.csv", "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=["Dispatch_Id", "Kernel_Name", "Counter_Name", "Counter_Value"])
+        w.writeheader()
+        for i, name, v in crow:
+            w.writerow({"Dispatch_Id": i, "Kernel_Name": name, "Counter_Name": "FETCH_SIZE", "Counter_Value": v})
+    out = bench.kernel_summary(str(tmp_path))
+    lines = [l for l in out.splitlines() if l.startswith("| mlq::")]
+    assert len(lines) == 4 and "gemv" not in out  # 2 kernels x (trace, counters)
+    dur = {l.split("|")[1].strip(): float(l.split("|")[3]) for l in lines if l.count("|") == 7}
+    assert dur["mlq::gemm_chunk_kernel<2, 2, 2, 2, true>"] == 61.0
+    assert dur["mlq::xsplit_kernel<2>"] == 8.0
+    cnt = {l.split("|")[1].strip(): float(l.split("|")[3]) for l in lines if l.count("|") == 4}
+    assert cnt["mlq::gemm_chunk_kernel<2, 2, 2, 2, true>"] == 200.0 and cnt["mlq::xsplit_kernel<2>"] == 50.0
+    assert "calibration copy): FETCH_SIZE 1048576.0" in out
