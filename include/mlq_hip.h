@@ -139,12 +139,16 @@ typedef struct mlq_linear_call {
 } mlq_linear_call;
 int mlq_hip_quant_linear_many(const mlq_linear_call* calls, int n, void* stream);
 
-/* Up to 4 GEMVs (rows == 1) that read the same x, in one launch: the fused
- * q/k/v or gate/up projection of a decode step.  Same x, in_features and
- * quant type for every call; outputs disjoint from each other and from x.
- * Per call the result equals mlq_hip_quant_linear bit for bit.  No
- * counterpart in the reference (its forward issues one linear per projection,
- * src/forward.cpp:172-227).  Asynchronous on `stream`. */
+/* Up to 4 linears that read the same x, in one launch: the fused q/k/v or
+ * gate/up projection of a decode step (rows == 1: GEMVs, per call equal to
+ * mlq_hip_quant_linear bit for bit) or of a batched prefill (rows > 1: one
+ * grouped MFMA GEMM over up to 3 weights when each weight but the last is a
+ * whole number of the GEMM's row tiles -- 64 or 128 rows --, else one launch
+ * per call; per call within the linear's tolerance of mlq_hip_quant_linear,
+ * whose K split may differ because the group's total rows pick it).  Same x,
+ * rows, in_features and quant type for every call; outputs disjoint from each
+ * other and from x.  No counterpart in the reference (its forward issues one
+ * linear per projection, src/forward.cpp:172-227).  Asynchronous on `stream`. */
 int mlq_hip_quant_linear_fused(const mlq_linear_call* calls, int n, void* stream);
 
 /* Measurement, not a linear: streams exactly the weights a fused launch of

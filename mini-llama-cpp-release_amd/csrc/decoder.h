@@ -102,6 +102,10 @@ private:
     bool launch_attention_rope(hipStream_t s, int layer);
     void launch_norm(hipStream_t s, const float* delta, const float* w);
     void linear_rows(hipStream_t s, const Linear& w, const float* X, float* Y, int rows);
+    // Up to three linears over the same X (q/k/v, gate/up) as one grouped GEMM
+    // launch when the shapes allow it, else one linear_rows each.
+    void linear_rows_group(hipStream_t s, int n, const Linear* const* w, const float* X, float* const* Y, int rows);
+    void ensure_workspace(hipStream_t s, size_t need);
     void linear_fused(hipStream_t s, const Linear* const* ws, float* const* ys, int n, const float* x,
                       const float* norm_w, bool acc);
     void enqueue_prefill(hipStream_t s, const int32_t* tokens, int n, int start);

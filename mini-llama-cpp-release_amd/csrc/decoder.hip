@@ -1347,19 +1347,7 @@ void Decoder::linear_rows(hipStream_t s, const Linear& w, const float* X, float*
     }
     const LinearShape shape{w.qtype, w.M, w.K, (w.K + 31) / 32, rows};
     if (rows > 1 && gemm_supported(shape)) {
-        const size_t need = gemm_workspace_bytes(shape);
-        if (need > ws_bytes_) {
-            check(hipStreamSynchronize(s), "hipStreamSynchronize");
-            void* p = nullptr;
-            check(hipMalloc(&p, need), "hipMalloc");
-            // Split-K counters start at zero: cleared on this stream, ahead of
-            // the GEMM (a plain hipMemset runs on the null stream, which this
-            // non-blocking stream does not wait for).
-            check(hipMemsetAsync(p, 0, need, s), "hipMemsetAsync");
-            allocs_.push_back(p);
-            ws_ = p;
-            ws_bytes_ = need;
-        }
+        ensure_workspace(s, gemm_workspace_bytes(shape));
         check(launch_gemm(shape, w.data, X, Y, ws_, ws_bytes_, s), "launch_gemm");
         return;
     }
@@ -1368,6 +1356,48 @@ void Decoder::linear_rows(hipStream_t s, const Linear& w, const float* X, float*
     g.y[0] = Y;
     g.ncalls = 1;
     check(launch_gemv_group(shape, g, X, s), "launch_gemv_group");
+}
+
+// The GEMM workspace grows to `need` bytes (a retired one is kept until the
+// decoder closes: launches queued before the growth may still use it).
+void Decoder::ensure_workspace(hipStream_t s, size_t need) {
+    if (need <= ws_bytes_) return;
+    check(hipStreamSynchronize(s), "hipStreamSynchronize");
+    void* p = nullptr;
+    check(hipMalloc(&p, need), "hipMalloc");
+    // Split-K counters start at zero: cleared on this stream, ahead of the
+    // GEMM (a plain hipMemset runs on the null stream, which this non-blocking
+    // stream does not wait for).
+    check(hipMemsetAsync(p, 0, need, s), "hipMemsetAsync");
+    allocs_.push_back(p);
+    ws_ = p;
+    ws_bytes_ = need;
+}
+
+void Decoder::linear_rows_group(hipStream_t s, int n, const Linear* const* w, const float* X, float* const* Y,
+                                int rows) {
+    bool grouped = rows > 1 && n > 1;
+    for (int g = 0; grouped && g < n; ++g)
+        grouped = w[g]->qtype != 0 && w[g]->qtype == w[0]->qtype && w[g]->K == w[0]->K;
+    if (grouped) {
+        LinearShape total{w[0]->qtype, 0, w[0]->K, (w[0]->K + 31) / 32, rows};
+        const void* wd[3];
+        int M[3];
+        for (int g = 0; g < n; ++g) {
+            wd[g] = w[g]->data;
+            M[g] = w[g]->M;
+            total.M += M[g];
+        }
+        if (gemm_supported(total)) {
+            ensure_workspace(s, gemm_workspace_bytes(total));
+            const hipError_t e = launch_gemm_group(total, n, wd, Y, M, X, ws_, ws_bytes_, s);
+            if (e != hipErrorNotSupported) {
+                check(e, "launch_gemm_group");
+                return;
+            }
+        }
+    }
+    for (int g = 0; g < n; ++g) linear_rows(s, *w[g], X, Y[g], rows);
 }
 
 bool Decoder::prefill_batched() const {
@@ -1390,9 +1420,11 @@ void Decoder::enqueue_prefill(hipStream_t s, const int32_t* tokens, int n, int s
         hipLaunchKernelGGL(add_rmsnorm_rows_kernel, dim3(n), dim3(kNormThreads), 0, s, X_, l == 0 ? nullptr : FF_,
                            L.attn_norm, c.dim, c.rms_norm_eps, H_);
         check(hipGetLastError(), "add_rmsnorm_rows_kernel");
-        linear_rows(s, L.wq, H_, Q_, n);
-        linear_rows(s, L.wk, H_, K_, n);
-        linear_rows(s, L.wv, H_, V_, n);
+        {
+            const Linear* w[3] = {&L.wq, &L.wk, &L.wv};
+            float* y[3] = {Q_, K_, V_};
+            linear_rows_group(s, 3, w, H_, y, n);
+        }
         const int rope_threads = q_dim / 2 + kv_dim / 2 + kv_dim;
         hipLaunchKernelGGL(rope_kv_rows_kernel, dim3((rope_threads + 255) / 256, n), dim3(256), 0, s, Q_, K_, V_,
                            L.bq, L.bk, L.bv, c.n_heads, c.n_kv_heads, c.head_dim, c.rope_theta, c.rope_neox,
@@ -1415,8 +1447,11 @@ void Decoder::enqueue_prefill(hipStream_t s, const int32_t* tokens, int n, int s
         hipLaunchKernelGGL(add_rmsnorm_rows_kernel, dim3(n), dim3(kNormThreads), 0, s, X_, PROJ_, L.ffn_norm, c.dim,
                            c.rms_norm_eps, H_);
         check(hipGetLastError(), "add_rmsnorm_rows_kernel");
-        linear_rows(s, L.w_gate, H_, GATE_, n);
-        linear_rows(s, L.w_up, H_, UP_, n);
+        {
+            const Linear* w[2] = {&L.w_gate, &L.w_up};
+            float* y[2] = {GATE_, UP_};
+            linear_rows_group(s, 2, w, H_, y, n);
+        }
         const int nh = n * c.hidden_dim;
         hipLaunchKernelGGL(swiglu_kernel, dim3((nh + 255) / 256), dim3(256), 0, s, GATE_, UP_, ACT_, nh);
         check(hipGetLastError(), "swiglu_kernel");

@@ -620,6 +620,15 @@ struct ChunkArgs {
     uint32_t part_bytes;
     unsigned* tile_count;
     int M, N, K, nb, npad, row_tiles, splits, chunks_per_split;
+    // Grouped call (up to three weights reading the same x, e.g. q / k / v):
+    // weight g owns row tiles [tile_g, tile_{g+1}) with tile_0 = 0 and writes
+    // its own y [N][M_g]; W / y / M above are group 0.  A single weight has
+    // tile1 = tile2 = row_tiles.
+    const uint8_t* W1;
+    const uint8_t* W2;
+    float* y1;
+    float* y2;
+    int M1, M2, tile1, tile2;
 };
 
 template <int QT, int RW, int TT, int P, bool XS>
@@ -643,9 +652,13 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_chunk_kernel(const ChunkArg
     const int wg = blockIdx.x;
     const int split = wg % a.splits;
     const int tile = wg / a.splits;
-    const int m_base = (tile % a.row_tiles) * (64 * RW);
+    const int rt = tile % a.row_tiles;
+    const int gi = (rt >= a.tile1 ? 1 : 0) + (rt >= a.tile2 ? 1 : 0);  // this tile's weight of the group
+    const uint8_t* const Wg = gi == 0 ? a.W : gi == 1 ? a.W1 : a.W2;
+    float* const yg = gi == 0 ? a.y : gi == 1 ? a.y1 : a.y2;
+    const int m_base = (rt - (gi == 0 ? 0 : gi == 1 ? a.tile1 : a.tile2)) * (64 * RW);
     const int n_base = (tile / a.row_tiles) * BN;
-    const int M = a.M, N = a.N, nb = a.nb;
+    const int M = gi == 0 ? a.M : gi == 1 ? a.M1 : a.M2, N = a.N, nb = a.nb;
     const int nchunk_all = nb / kChunkBlocks;
     const int c0 = split * a.chunks_per_split;
     const int nchunk = min(nchunk_all, c0 + a.chunks_per_split) - c0;
@@ -659,7 +672,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_chunk_kernel(const ChunkArg
     // (lanes past the wave's units re-read its last unit, tokens past N read
     // token 0 and are zeroed) so that no branch forces an early wait; only
     // the LDS store is predicated.
-    const uint8_t* wsplit = a.W + static_cast<size_t>(c0) * kChunkBlocks * F::BB;
+    const uint8_t* wsplit = Wg + static_cast<size_t>(c0) * kChunkBlocks * F::BB;
     uint32_t goff[NWL];
     int loff[NWL];
 #pragma unroll
@@ -965,7 +978,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_chunk_kernel(const ChunkArg
 #pragma unroll
                 for (int r = 0; r < RW; ++r) {
                     const int m = m_base + (wave * RW + r) * 16 + i16;
-                    if (m < M) a.y[static_cast<size_t>(n) * M + m] = acc[r][t][q] * sn;
+                    if (m < M) yg[static_cast<size_t>(n) * M + m] = acc[r][t][q] * sn;
                 }
             }
         return;
@@ -1025,7 +1038,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_chunk_kernel(const ChunkArg
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const int n = n_base + t * 16 + 4 * g + q;
-            if (n < N && m < M) a.y[static_cast<size_t>(n) * M + m] = sum[k][q] * tok_scale(t, q);
+            if (n < N && m < M) yg[static_cast<size_t>(n) * M + m] = sum[k][q] * tok_scale(t, q);
         }
     }
     if (tid == 0) __hip_atomic_store(a.tile_count + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1191,9 +1204,17 @@ size_t chunk_workspace_bytes(const LinearShape& s) { return chunk_layout(s, choo
 // (the earlier default) cost 2.5-15 % (4096 x 4096 Q4_0 12.1 -> 11.8 us,
 // 11008 x 4096 Q8_0 26.6 -> 22.5 us): the ring's VGPRs halve the waves per SIMD,
 // and the loop is not waiting on the weights.
+// Weights of a grouped call: n <= 3 linears with the same qtype, K and rows.
+struct ChunkGroup {
+    int n;
+    const void* w[3];
+    float* y[3];
+    int M[3];
+};
+
 template <int QT, int RW, int TT, bool XS, int P = 2>
 hipError_t launch_chunk_t(const LinearShape& s, const ChunkCfg& c, const void* w, const float* x, float* y,
-                          char* ws, hipStream_t stream) {
+                          char* ws, hipStream_t stream, const ChunkGroup* grp = nullptr) {
     constexpr int lds = ChunkLds<QT, RW, TT, XS>::bytes;
     auto kern = gemm_chunk_kernel<QT, RW, TT, P, XS>;
     static bool attr = [&] {
@@ -1214,6 +1235,24 @@ hipError_t launch_chunk_t(const LinearShape& s, const ChunkCfg& c, const void* w
     a.tile_count = reinterpret_cast<unsigned*>(ws);
     a.M = s.M, a.N = s.rows, a.K = s.K, a.nb = s.nb, a.npad = c.npad;
     a.row_tiles = c.row_tiles, a.splits = c.splits, a.chunks_per_split = c.cps;
+    a.W1 = a.W2 = nullptr;
+    a.y1 = a.y2 = nullptr;
+    a.M1 = a.M2 = 0;
+    a.tile1 = a.tile2 = c.row_tiles;
+    if (grp != nullptr) {
+        const int bm = 64 * RW;
+        a.W = static_cast<const uint8_t*>(grp->w[0]);
+        a.y = grp->y[0];
+        a.M = grp->M[0];
+        if (grp->n >= 2) {
+            a.W1 = static_cast<const uint8_t*>(grp->w[1]), a.y1 = grp->y[1], a.M1 = grp->M[1];
+            a.tile1 = grp->M[0] / bm;
+        }
+        if (grp->n >= 3) {
+            a.W2 = static_cast<const uint8_t*>(grp->w[2]), a.y2 = grp->y[2], a.M2 = grp->M[2];
+            a.tile2 = a.tile1 + grp->M[1] / bm;
+        }
+    }
     if (XS) {
         hipLaunchKernelGGL((xsplit_kernel<QT>), dim3(c.npad), dim3(256), 0, stream, x, s.rows, s.K, s.nb, c.npad,
                            reinterpret_cast<_Float16*>(ws + l.xs), reinterpret_cast<float*>(ws + l.bsum),
@@ -1226,11 +1265,11 @@ hipError_t launch_chunk_t(const LinearShape& s, const ChunkCfg& c, const void* w
 
 template <int QT>
 hipError_t launch_chunk_q(const LinearShape& s, const ChunkCfg& c, const void* w, const float* x, float* y,
-                          char* ws, hipStream_t stream) {
-    if (c.tt == 1) return launch_chunk_t<QT, 1, 1, false>(s, c, w, x, y, ws, stream);
-    if (c.tt == 2 && !c.xs) return launch_chunk_t<QT, 2, 2, false>(s, c, w, x, y, ws, stream);
-    if (c.tt == 2) return launch_chunk_t<QT, 2, 2, true>(s, c, w, x, y, ws, stream);
-    return launch_chunk_t<QT, 2, 4, true>(s, c, w, x, y, ws, stream);
+                          char* ws, hipStream_t stream, const ChunkGroup* grp = nullptr) {
+    if (c.tt == 1) return launch_chunk_t<QT, 1, 1, false>(s, c, w, x, y, ws, stream, grp);
+    if (c.tt == 2 && !c.xs) return launch_chunk_t<QT, 2, 2, false>(s, c, w, x, y, ws, stream, grp);
+    if (c.tt == 2) return launch_chunk_t<QT, 2, 2, true>(s, c, w, x, y, ws, stream, grp);
+    return launch_chunk_t<QT, 2, 4, true>(s, c, w, x, y, ws, stream, grp);
 }
 
 bool use_chunk(const LinearShape& s, const float* x) {
@@ -1275,6 +1314,33 @@ hipError_t launch_gemm(const LinearShape& s, const void* w, const float* x, floa
         case 1: return launch_q<1>(s, c, l, w, x, y, base, stream);
         case 2: return launch_q<2>(s, c, l, w, x, y, base, stream);
         default: return launch_q<3>(s, c, l, w, x, y, base, stream);
+    }
+}
+
+hipError_t launch_gemm_group(const LinearShape& s, int n, const void* const* w, float* const* y, const int* M,
+                             const float* x, void* ws, size_t ws_bytes, hipStream_t stream) {
+    if (n < 1 || n > 3 || w == nullptr || y == nullptr || M == nullptr) return hipErrorInvalidValue;
+    LinearShape st = s;
+    st.M = 0;
+    for (int g = 0; g < n; ++g) {
+        if (M[g] <= 0) return hipErrorInvalidValue;
+        st.M += M[g];
+    }
+    if (!use_chunk(st, x)) return hipErrorNotSupported;
+    const ChunkCfg c = choose_chunk(st);
+    const int bm = 64 * c.rw;
+    for (int g = 0; g + 1 < n; ++g)
+        if (M[g] % bm != 0) return hipErrorNotSupported;  // a row tile may not straddle two weights
+    if (ws == nullptr) return hipErrorInvalidValue;
+    if (ws_bytes < chunk_workspace_bytes(st)) return hipErrorInvalidValue;
+    ChunkGroup grp{};
+    grp.n = n;
+    for (int g = 0; g < n; ++g) grp.w[g] = w[g], grp.y[g] = y[g], grp.M[g] = M[g];
+    char* base = static_cast<char*>(ws);
+    switch (st.qtype) {
+        case 1: return launch_chunk_q<1>(st, c, w[0], x, y[0], base, stream, &grp);
+        case 2: return launch_chunk_q<2>(st, c, w[0], x, y[0], base, stream, &grp);
+        default: return launch_chunk_q<3>(st, c, w[0], x, y[0], base, stream, &grp);
     }
 }
 

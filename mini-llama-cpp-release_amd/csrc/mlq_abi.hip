@@ -635,19 +635,19 @@ int mlq_hip_quant_linear_fused(const mlq_linear_call* calls, int n, void* stream
     if (rc != MLQ_OK) return rc;
     mlq::GemvGroup g{};
     long long rows = 0;
+    const int nrows = calls[0].rows;
     for (int i = 0; i < n; ++i) {
         const mlq_linear_call& c = calls[i];
         const std::string at = std::string(caller) + ": call " + std::to_string(i);
         if (c.w == nullptr) return fail(MLQ_ERR_INVALID, at + ": null weight handle");
         if (c.w->device != device) return fail(MLQ_ERR_DEVICE, at + ": weight on a different device");
-        if (c.rows != 1) return fail(MLQ_ERR_INVALID, at + ": rows must be 1 (a fused launch is a GEMV)");
-        if (c.x != calls[0].x || c.w->K != w0->K || c.w->qtype != w0->qtype) {
-            return fail(MLQ_ERR_INVALID, at + ": differs from call 0 in input, in_features or quant type");
+        if (c.x != calls[0].x || c.w->K != w0->K || c.w->qtype != w0->qtype || c.rows != nrows) {
+            return fail(MLQ_ERR_INVALID, at + ": differs from call 0 in input, rows, in_features or quant type");
         }
-        if ((rc = validate_linear(c.w->qtype, c.w->M, c.w->K, c.w->n_blocks, 1)) != MLQ_OK) return rc;
+        if ((rc = validate_linear(c.w->qtype, c.w->M, c.w->K, c.w->n_blocks, c.rows)) != MLQ_OK) return rc;
         const char* lin = caller_for(c.w->qtype);
-        const size_t xb = static_cast<size_t>(c.w->K) * sizeof(float);
-        const size_t yb = static_cast<size_t>(c.w->M) * sizeof(float);
+        const size_t xb = static_cast<size_t>(c.rows) * c.w->K * sizeof(float);
+        const size_t yb = static_cast<size_t>(c.rows) * c.w->M * sizeof(float);
         if ((rc = check_device_ptr(c.x, device, lin, "input", xb)) != MLQ_OK) return rc;
         if ((rc = check_device_ptr(c.y, device, lin, "output", yb)) != MLQ_OK) return rc;
         const uintptr_t ylo = reinterpret_cast<uintptr_t>(c.y), yhi = ylo + yb;
@@ -655,7 +655,7 @@ int mlq_hip_quant_linear_fused(const mlq_linear_call* calls, int n, void* stream
         if (ylo < xhi && xlo < yhi) return fail(MLQ_ERR_INVALID, at + ": output overlaps the input");
         for (int j = 0; j < i; ++j) {
             const uintptr_t olo = reinterpret_cast<uintptr_t>(calls[j].y);
-            const uintptr_t ohi = olo + static_cast<size_t>(calls[j].w->M) * sizeof(float);
+            const uintptr_t ohi = olo + static_cast<size_t>(nrows) * calls[j].w->M * sizeof(float);
             if (ylo < ohi && olo < yhi) {
                 return fail(MLQ_ERR_INVALID, at + ": output overlaps the output of call " + std::to_string(j));
             }
@@ -666,9 +666,36 @@ int mlq_hip_quant_linear_fused(const mlq_linear_call* calls, int n, void* stream
         rows += c.w->M;
     }
     if (rows > (1ll << 30)) return fail(MLQ_ERR_LIMIT, std::string(caller) + ": too many rows");
+    hipStream_t s = resolve_stream(device, stream);
+    if (nrows > 1) {
+        // Batched rows: one grouped GEMM launch where the shapes allow it (at
+        // most three weights, each but the last a whole number of row tiles),
+        // else one GEMM (or GEMV batch) per call.
+        mlq::LinearShape total{w0->qtype, static_cast<int>(rows), w0->K, w0->nb, nrows};
+        if (n <= 3 && mlq::gemm_supported(total)) {
+            const void* wd[3];
+            float* yd[3];
+            int M[3];
+            for (int i = 0; i < n; ++i) wd[i] = calls[i].w->ptr, yd[i] = calls[i].y, M[i] = calls[i].w->M;
+            const size_t need = mlq::gemm_workspace_bytes(total);
+            void* ws = nullptr;
+            if ((rc = stream_workspace(device, s, need, &ws)) != MLQ_OK) return rc;
+            const hipError_t e = mlq::launch_gemm_group(total, n, wd, yd, M, calls[0].x, ws, need, s);
+            if (e != hipErrorNotSupported) {
+                if (e != hipSuccess) return hip_fail(e, caller);
+                return MLQ_OK;
+            }
+        }
+        for (int i = 0; i < n; ++i) {
+            const mlq_linear_call& c = calls[i];
+            mlq::LinearShape shape{c.w->qtype, c.w->M, c.w->K, c.w->nb, c.rows};
+            if ((rc = dispatch(device, shape, c.w->ptr, c.x, c.y, s)) != MLQ_OK) return rc;
+        }
+        return MLQ_OK;
+    }
     g.ncalls = n;
     mlq::LinearShape shape{w0->qtype, static_cast<int>(rows), w0->K, w0->nb, 1};
-    hipError_t e = mlq::launch_gemv_group(shape, g, calls[0].x, resolve_stream(device, stream));
+    hipError_t e = mlq::launch_gemv_group(shape, g, calls[0].x, s);
     if (e != hipSuccess) return hip_fail(e, caller);
     return MLQ_OK;
 }

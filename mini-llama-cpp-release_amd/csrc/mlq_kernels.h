@@ -106,6 +106,17 @@ size_t gemm_workspace_bytes(const LinearShape& s);
 hipError_t launch_gemm(const LinearShape& s, const void* w, const float* x, float* y, void* ws,
                        size_t ws_bytes, hipStream_t stream);
 const char* gemm_kernel_name(const LinearShape& s);
+// Up to three linears that read the same x (same qtype, K and rows; e.g. q, k
+// and v of one layer) as one GEMM launch: linear g has M[g] rows and writes
+// y[g] ([rows][M[g]]); s.M is ignored (the total is the sum).  A row gets the
+// arithmetic of a single call of its linear, with the tile shape and K split
+// that the group's total M selects.
+// hipErrorNotSupported when the shape has no grouped path (no chunk kernel, or
+// a weight other than the last whose M is not a multiple of the tile height):
+// then launch the linears one by one.  The workspace is sized for a LinearShape
+// whose M is the total.
+hipError_t launch_gemm_group(const LinearShape& s, int n, const void* const* w, float* const* y, const int* M,
+                             const float* x, void* ws, size_t ws_bytes, hipStream_t stream);
 
 // Persistent GEMV over a chain of linears (sequence.hip).  A stage is up to
 // kSeqMaxCalls GEMVs reading the same x; their rows are concatenated in call

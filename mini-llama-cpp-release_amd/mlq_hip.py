@@ -333,7 +333,8 @@ def stream_floor(arr: ctypes.Array, sink: "DeviceBuffer", stream=None) -> None:
 
 
 def linear_fused(arr: ctypes.Array, stream=None) -> None:
-    """One launch for up to 4 GEMVs that share x (asynchronous on `stream`)."""
+    """One launch for up to 4 linears that share x: GEMVs (rows 1) or a grouped
+    GEMM (rows > 1); asynchronous on `stream`."""
     _check(load().mlq_hip_quant_linear_fused(arr, len(arr), stream))
 
 

@@ -108,3 +108,51 @@ def test_graph_replay_after_workspace_growth(hip, orc):
     g.destroy()
     hip.stream_destroy(sp)
     wt.free()
+
+
+def _fused_rows(hip, orc, qt, ms, k, n, seed):
+    """mlq_hip_quant_linear_fused with `n` token rows over weights of ms rows
+    sharing x: every output against the oracle, and the per-call results of
+    mlq_hip_quant_linear for comparison."""
+    rng = np.random.default_rng(900 + seed)
+    x = rng.standard_normal((n, k), dtype=np.float32)
+    blocks = [orc.quantize(qt, (rng.standard_normal((m, k), dtype=np.float32) * np.float32(0.02)), threads=THREADS)
+              for m in ms]
+    ws = [hip.Weight.upload(qt, b, m, k) for b, m in zip(blocks, ms)]
+    xb = hip.DeviceBuffer.from_array(x)
+    ys = [hip.DeviceBuffer(4 * n * m) for m in ms]
+    print(f"fused gemm qt={qt} Ms={ms} K={k} N={n}", flush=True)
+    hip.linear_fused(hip.make_calls([(w, xb, y, n) for w, y in zip(ws, ys)]))
+    hip.synchronize()
+    got = [y.download(np.float32, n * m).reshape(n, m) for y, m in zip(ys, ms)]
+    single = [w.linear_host(x) for w in ws]
+    for g, b, m in zip(got, blocks, ms):
+        check_close(g, orc.linear(qt, x, b, m, threads=THREADS), x, qt, b, f"fused qt={qt} M={m} N={n}")
+    for w in ws:
+        w.free()
+    xb.free()
+    for y in ys:
+        y.free()
+    return got, single
+
+
+@pytest.mark.parametrize("ms,k,n", [((256, 128, 72), 896, 16), ((256, 128, 72), 896, 40), ((256, 128, 72), 896, 300),
+                                    ((128, 256), 4096, 64), ((100, 128, 64), 896, 40), ((64, 64, 64, 64), 896, 20)],
+                         ids=["g3_n16", "g3_n40", "g3_n300", "g2_n64", "ragged_first", "four_calls"])
+def test_fused_batched_rows(hip, orc, ms, k, n):
+    """Batched rows through the fused entry: the grouped GEMM (up to three
+    weights, each but the last a whole number of row tiles) or, where the
+    shapes do not allow it (a first weight of 100 rows, four calls), one
+    launch per call -- every output within the tolerance of the oracle."""
+    for fmt, qt in FMTS.items():
+        _fused_rows(hip, orc, qt, ms, k, n, seed=len(ms) + n)
+
+
+def test_fused_batched_qkv_512_rows_bit_identical(hip, orc):
+    """q/k/v-shaped group at 512 rows: one K split at both the single-call and
+    the group's total M, so the grouped launch must give every row the bits of
+    mlq_hip_quant_linear."""
+    for fmt in ("q4_0", "q8_0"):
+        got, single = _fused_rows(hip, orc, FMTS[fmt], (4096, 4096, 4096), 4096, 512, seed=7)
+        for i, (g, s) in enumerate(zip(got, single)):
+            assert np.array_equal(g.view(np.uint32), s.view(np.uint32)), f"{fmt} call {i}"

@@ -299,8 +299,8 @@ def test_fused_validation(hip):
         fused([(l1.w, x, y[0], 1), (l1.w, x, y[0], 1)])
     with pytest.raises(hip.MlqError, match="overlaps the input"):
         fused([(l1.w, x, x, 1)])
-    with pytest.raises(hip.MlqError, match="rows must be 1"):
-        fused([(l1.w, x, y[0], 2)])
+    with pytest.raises(hip.MlqError, match="differs from call 0"):
+        fused([(l1.w, x, y[0], 1), (l1.w, x, y[1], 2)])
 
 
 def test_stream_floor_runs_and_validates(hip):

@@ -39,7 +39,9 @@ def test_noalloc_equals_existing_entry(hip, fmt):
     for rows in (64, 16, 1, 512, 3):  # each call after a larger one, then a larger one again
         print(f"noalloc {fmt} {m}x{k} rows={rows}", flush=True)
         x = hip.DeviceBuffer(4 * rows * k)
-        hip.fill_normal(x, rows * k, 100 + rows, 0.0, 1.0)
+        # x on the calls' own stream: filled on the device's default stream it
+        # could still be in flight when the first call on `s` reads it
+        hip.fill_normal(x, rows * k, 100 + rows, 0.0, 1.0, stream=s)
         y_ref, y = hip.DeviceBuffer(4 * rows * m), hip.DeviceBuffer(4 * rows * m)
         w.linear_device(x, y_ref, rows=rows, stream=s)  # existing entry (stream workspace)
         y.fill(0)
