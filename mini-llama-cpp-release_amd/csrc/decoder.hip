@@ -572,30 +572,35 @@ __global__ __launch_bounds__(256) void rope_kv_rows_kernel(float* __restrict__ Q
     }
 }
 
-// Causal attention of prefill rows: workgroup (head h, rows r0..r0+3) attends
-// from positions start + r over cache rows 0..start + r (all written before),
-// with the same coalesced reads and online softmax as attention_rope_kernel.
-// Each cache row is read once for the four query rows (each keeps its own
-// running maximum, sum and weighted V; rows past a query's position enter
-// through selects).  Measured on MI355X, LLaMA-7B shape (32 heads x 128,
-// 256 rows): 127 -> 64 us at positions 0..255 and 243 -> 147 us at
-// 256..511 per layer, against one workgroup of 512 threads per row;
-// 256-thread workgroups beat 512 (and 8 or 16 rows per workgroup).
+// Causal attention of prefill rows: workgroup (head h, query rows r0 ..
+// r0 + QR - 1) attends from positions start + r over cache rows 0 .. start + r
+// (all written before).  A cache row is read by a group of LPR lanes, V4
+// float4s per lane (float4 li + LPR v: each load is a coalesced row segment),
+// ROWS = 256 / LPR rows per pass plus A - 1 passes in flight.  Each cache row
+// is read once for the QR query rows.  Per pass a lane group takes the scores
+// of its A rows, then updates its running maximum, sum and weighted V once
+// (one rescale per pass, not per row); rows past a query's position enter
+// through selects.  At the end the groups of a wave are merged with a
+// butterfly of shuffles and the waves through LDS, in a fixed order.  The
+// result equals the reference's max - exp - sum - divide - weighted sum to
+// rounding (src/forward.cpp:584-611 and src/ops.cpp:43-71 for one row).  Several float4s per lane
+// put more rows in each wave instruction: the score reductions and the
+// softmax arithmetic, which every lane of a group repeats, are shared by
+// more rows.
 constexpr int kPrefillAttnThreads = 256;
-constexpr int kPrefillAttnRows = 4;
-template <int LPR>
+template <int LPR, int V4, int QR, int A>
 __global__ __launch_bounds__(kPrefillAttnThreads) void attention_rows_kernel(const float* __restrict__ Q,
                                                                              const float* __restrict__ kc,
                                                                              const float* __restrict__ vc, int n_heads,
                                                                              int n_kv, int max_seq, int layer,
                                                                              int start, int n, float* __restrict__ out) {
-    constexpr int HD = 4 * LPR;
+    constexpr int HD = 4 * LPR * V4;
     constexpr int NT = kPrefillAttnThreads;
-    constexpr int QR = kPrefillAttnRows;
     constexpr int ROWS = NT / LPR;
-    constexpr int AHEAD = kFlashAhead;
-    __shared__ float gm[QR][ROWS], gl[QR][ROWS];
-    __shared__ float4 gacc[QR][ROWS][LPR];
+    constexpr int NW = NT / 64;
+    static_assert(LPR <= 64 && 64 % LPR == 0, "lane groups within a wave");
+    __shared__ float gm[QR][NW], gl[QR][NW];
+    __shared__ float4 gacc[QR][NW][LPR * V4];
     const int tid = threadIdx.x;
     const int h = blockIdx.x;
     const int r0 = blockIdx.y * QR;
@@ -607,81 +612,136 @@ __global__ __launch_bounds__(kPrefillAttnThreads) void attention_rows_kernel(con
     const int lr = tid / LPR;
     const int li = tid % LPR;
     // Query rows past n repeat row n - 1 (their results are not stored).
-    float4 qv[QR];
+    float4 qv[QR][V4];
     int posq[QR];
 #pragma unroll
     for (int q = 0; q < QR; ++q) {
         const int row = min(r0 + q, n - 1);
         posq[q] = start + row;
-        qv[q] = *reinterpret_cast<const float4*>(Q + static_cast<size_t>(row) * n_heads * HD + h * HD + 4 * li);
+        const float* qrow = Q + static_cast<size_t>(row) * n_heads * HD + h * HD;
+#pragma unroll
+        for (int v = 0; v < V4; ++v) qv[q][v] = *reinterpret_cast<const float4*>(qrow + 4 * (li + LPR * v));
     }
     const int pos = posq[QR - 1];  // the last query row sees the most cache rows
     const float scale = 1.0f / sqrtf(static_cast<float>(HD));
     float m[QR], l[QR];
-    float4 acc[QR];
+    float4 acc[QR][V4];
 #pragma unroll
     for (int q = 0; q < QR; ++q) {
         m[q] = -INFINITY;
         l[q] = 0.0f;
-        acc[q] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+        for (int v = 0; v < V4; ++v) acc[q][v] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
-    auto pass = [&](int t0, const float4 (&kc4)[AHEAD], const float4 (&vc4)[AHEAD]) {
+    // Cache rows past pos re-read row pos (they are masked for every query).
+    auto load_rows = [&](int t0, float4 (&kr)[A][V4], float4 (&vr)[A][V4]) {
 #pragma unroll
-        for (int j = 0; j < AHEAD; ++j) {
-            const int t = t0 + j * ROWS;
-            float dot[QR];
+        for (int j = 0; j < A; ++j) {
+            const int tj = min(t0 + j * ROWS, pos);
 #pragma unroll
-            for (int q = 0; q < QR; ++q)
-                dot[q] = lane_group_sum<LPR>(qv[q].x * kc4[j].x + qv[q].y * kc4[j].y + qv[q].z * kc4[j].z +
-                                             qv[q].w * kc4[j].w);
-#pragma unroll
-            for (int q = 0; q < QR; ++q) {
-                const bool in = t <= posq[q];
-                const float sc = in ? dot[q] * scale : 0.0f;
-                const float mn = in ? fmaxf(m[q], sc) : m[q];
-                const float c_old = in ? expf(m[q] - mn) : 1.0f;
-                const float p = in ? expf(sc - mn) : 0.0f;
-                l[q] = l[q] * c_old + p;
-                acc[q].x = acc[q].x * c_old + p * vc4[j].x;
-                acc[q].y = acc[q].y * c_old + p * vc4[j].y;
-                acc[q].z = acc[q].z * c_old + p * vc4[j].z;
-                acc[q].w = acc[q].w * c_old + p * vc4[j].w;
-                m[q] = mn;
+            for (int v = 0; v < V4; ++v) {
+                kr[j][v] = *reinterpret_cast<const float4*>(kbase + tj * t_stride + 4 * (li + LPR * v));
+                vr[j][v] = *reinterpret_cast<const float4*>(vbase + tj * t_stride + 4 * (li + LPR * v));
             }
         }
     };
-    // Cache rows past pos re-read row pos (they are masked for every query).
-    float4 kr[AHEAD], vr[AHEAD];
+    auto pass = [&](int t0, const float4 (&kc4)[A][V4], const float4 (&vc4)[A][V4]) {
 #pragma unroll
-    for (int j = 0; j < AHEAD; ++j) {
-        const int tj = min(lr + j * ROWS, pos);
-        kr[j] = *reinterpret_cast<const float4*>(kbase + tj * t_stride + 4 * li);
-        vr[j] = *reinterpret_cast<const float4*>(vbase + tj * t_stride + 4 * li);
-    }
-    for (int t0 = lr; t0 <= pos; t0 += AHEAD * ROWS) {
-        float4 kc4[AHEAD], vc4[AHEAD];
+        for (int q = 0; q < QR; ++q) {
+            float sc[A];
+            float bm = -INFINITY;
 #pragma unroll
-        for (int j = 0; j < AHEAD; ++j) {
-            kc4[j] = kr[j];
-            vc4[j] = vr[j];
-        }
-        if (t0 + AHEAD * ROWS <= pos) {
+            for (int j = 0; j < A; ++j) {
+                float d = 0.0f;
 #pragma unroll
-            for (int j = 0; j < AHEAD; ++j) {
-                const int tj = min(t0 + (AHEAD + j) * ROWS, pos);
-                kr[j] = *reinterpret_cast<const float4*>(kbase + tj * t_stride + 4 * li);
-                vr[j] = *reinterpret_cast<const float4*>(vbase + tj * t_stride + 4 * li);
+                for (int v = 0; v < V4; ++v)
+                    d += qv[q][v].x * kc4[j][v].x + qv[q][v].y * kc4[j][v].y + qv[q][v].z * kc4[j][v].z +
+                         qv[q][v].w * kc4[j][v].w;
+                d = lane_group_sum<LPR>(d);
+                const bool in = t0 + j * ROWS <= posq[q];
+                sc[j] = in ? d * scale : -INFINITY;
+                bm = fmaxf(bm, sc[j]);
             }
+            const float mn = fmaxf(m[q], bm);
+            const float base = mn == -INFINITY ? 0.0f : mn;  // no row of this query yet
+            const float c_old = expf(m[q] - base);            // 0 while the running state is empty
+            float p[A];
+            float ps = 0.0f;
+#pragma unroll
+            for (int j = 0; j < A; ++j) {
+                p[j] = expf(sc[j] - base);  // 0 for masked rows
+                ps += p[j];
+            }
+            l[q] = l[q] * c_old + ps;
+#pragma unroll
+            for (int v = 0; v < V4; ++v) {
+                float4 a = acc[q][v];
+                a.x *= c_old;
+                a.y *= c_old;
+                a.z *= c_old;
+                a.w *= c_old;
+#pragma unroll
+                for (int j = 0; j < A; ++j) {
+                    a.x = __builtin_fmaf(p[j], vc4[j][v].x, a.x);
+                    a.y = __builtin_fmaf(p[j], vc4[j][v].y, a.y);
+                    a.z = __builtin_fmaf(p[j], vc4[j][v].z, a.z);
+                    a.w = __builtin_fmaf(p[j], vc4[j][v].w, a.w);
+                }
+                acc[q][v] = a;
+            }
+            m[q] = mn;
         }
+    };
+    float4 kr[A][V4], vr[A][V4];
+    load_rows(lr, kr, vr);
+    for (int t0 = lr; t0 <= pos; t0 += A * ROWS) {
+        float4 kc4[A][V4], vc4[A][V4];
+#pragma unroll
+        for (int j = 0; j < A; ++j)
+#pragma unroll
+            for (int v = 0; v < V4; ++v) {
+                kc4[j][v] = kr[j][v];
+                vc4[j][v] = vr[j][v];
+            }
+        if (t0 + A * ROWS <= pos) load_rows(t0 + A * ROWS, kr, vr);
         pass(t0, kc4, vc4);
     }
+    // Merge the lane groups of each wave (butterfly over the group index),
+    // then the waves through LDS.  An empty state (m = -inf) has l = 0 and
+    // acc = 0 and gets weight 0.
 #pragma unroll
-    for (int q = 0; q < QR; ++q) {
-        if (li == 0) {
-            gm[q][lr] = m[q];
-            gl[q][lr] = l[q];
+    for (int o = LPR; o < 64; o <<= 1) {
+#pragma unroll
+        for (int q = 0; q < QR; ++q) {
+            const float mp = __shfl_xor(m[q], o, 64);
+            const float lp = __shfl_xor(l[q], o, 64);
+            const float mn = fmaxf(m[q], mp);
+            const float base = mn == -INFINITY ? 0.0f : mn;
+            const float a = expf(m[q] - base), b = expf(mp - base);
+            l[q] = l[q] * a + lp * b;
+#pragma unroll
+            for (int v = 0; v < V4; ++v) {
+                float4 t = acc[q][v];
+                t.x = t.x * a + __shfl_xor(t.x, o, 64) * b;
+                t.y = t.y * a + __shfl_xor(t.y, o, 64) * b;
+                t.z = t.z * a + __shfl_xor(t.z, o, 64) * b;
+                t.w = t.w * a + __shfl_xor(t.w, o, 64) * b;
+                acc[q][v] = t;
+            }
+            m[q] = mn;
         }
-        gacc[q][lr][li] = acc[q];
+    }
+    const int w = tid >> 6;
+    if ((tid & 63) < LPR) {
+#pragma unroll
+        for (int q = 0; q < QR; ++q) {
+            if (li == 0) {
+                gm[q][w] = m[q];
+                gl[q][w] = l[q];
+            }
+#pragma unroll
+            for (int v = 0; v < V4; ++v) gacc[q][w][li + LPR * v] = acc[q][v];
+        }
     }
     __syncthreads();
     for (int e0 = tid; e0 < QR * HD; e0 += NT) {
@@ -689,14 +749,14 @@ __global__ __launch_bounds__(kPrefillAttnThreads) void attention_rows_kernel(con
         const int d = e0 % HD;
         float mx = -INFINITY;
 #pragma unroll
-        for (int g = 0; g < ROWS; ++g) mx = fmaxf(mx, gm[q][g]);
+        for (int g = 0; g < NW; ++g) mx = fmaxf(mx, gm[q][g]);
         const int c4 = d / 4;
         const int e = d % 4;
         float num = 0.0f;
         float den = 0.0f;
 #pragma unroll
-        for (int g = 0; g < ROWS; ++g) {
-            const bool rows = gm[q][g] != -INFINITY;  // false: a group without rows
+        for (int g = 0; g < NW; ++g) {
+            const bool rows = gm[q][g] != -INFINITY;  // false: a wave without rows
             const float wgt = rows ? expf(gm[q][g] - mx) : 0.0f;
             const float4 a = gacc[q][g][c4];
             num += rows ? wgt * (e == 0 ? a.x : e == 1 ? a.y : e == 2 ? a.z : a.w) : 0.0f;
@@ -1430,16 +1490,21 @@ void Decoder::enqueue_prefill(hipStream_t s, const int32_t* tokens, int n, int s
                            L.bq, L.bk, L.bv, c.n_heads, c.n_kv_heads, c.head_dim, c.rope_theta, c.rope_neox,
                            c.max_seq_len, l, start, kcache_, vcache_);
         check(hipGetLastError(), "rope_kv_rows_kernel");
-#define MLQ_ATTN_ROWS(LPR)                                                                                   \
-    hipLaunchKernelGGL((attention_rows_kernel<LPR>), dim3(c.n_heads, (n + kPrefillAttnRows - 1) / kPrefillAttnRows), \
+#define MLQ_ATTN_ROWS(LPR, V4, QR, A)                                                                           \
+    hipLaunchKernelGGL((attention_rows_kernel<LPR, V4, QR, A>), dim3(c.n_heads, (n + QR - 1) / QR),            \
                        dim3(kPrefillAttnThreads), 0, s, Q_, kcache_, vcache_, c.n_heads, c.n_kv_heads, c.max_seq_len, l, \
                        start, n, ATT_)
+        // (lanes per cache row, float4s per lane, query rows per workgroup,
+        // passes in flight).  LLaMA-7B shape (32 heads x 128, 512 rows, MI355X):
+        // prefill 27.7 ms with one float4 per lane (32 lanes per row, per-row
+        // softmax update) -> 25.4-25.6 ms at (16, 2, 4, 2); (8, 4, 4, 1) 25.7,
+        // (8, 4, 2, 1) 25.5-25.9, 8 query rows 26.2-28.7, (32, 1, 4, 2-4) 26.5-26.9.
         switch (c.head_dim) {
-            case 16: MLQ_ATTN_ROWS(4); break;
-            case 32: MLQ_ATTN_ROWS(8); break;
-            case 64: MLQ_ATTN_ROWS(16); break;
-            case 128: MLQ_ATTN_ROWS(32); break;
-            default: MLQ_ATTN_ROWS(64); break;
+            case 16: MLQ_ATTN_ROWS(4, 1, 4, 2); break;
+            case 32: MLQ_ATTN_ROWS(8, 1, 4, 2); break;
+            case 64: MLQ_ATTN_ROWS(8, 2, 4, 2); break;
+            case 128: MLQ_ATTN_ROWS(16, 2, 4, 2); break;
+            default: MLQ_ATTN_ROWS(32, 2, 4, 2); break;
         }
 #undef MLQ_ATTN_ROWS
         check(hipGetLastError(), "attention_rows_kernel");

@@ -230,6 +230,23 @@ def test_batched_prefill_matches_reference(hip, orc, ref, tmp_path, name):
     dec.close()
 
 
+@pytest.mark.parametrize("dim,heads,kv_heads", [(256, 4, 2), (256, 1, 1)], ids=["head_dim_64", "head_dim_256"])
+def test_batched_prefill_head_dims(hip, orc, ref, tmp_path, dim, heads, kv_heads):
+    """The prefill attention's other lane layouts (head_dim 64: 8 lanes of two
+    float4s per cache row; 256: 32 lanes of two), over many passes of cache
+    rows and a second batch at a later start."""
+    path = mf.write_model(orc, str(tmp_path / "hd.gguf"), dim=dim, heads=heads, kv_heads=kv_heads, hidden=352,
+                          ctx=256, fmts=("q4_0",), lm="q4_0", seed=12)
+    dec = hip.Decoder(path)
+    rd = ref.decoder(path)
+    toks = np.random.default_rng(13).integers(0, 300, 230).tolist()
+    worst = close(dec.prefill(toks[:150]), rd.batch(toks[:150]), f"head_dim {dim // heads} batch 0..149")
+    worst = max(worst, close(dec.prefill(toks[150:230], 150), rd.batch(toks[150:230], 150),
+                             f"head_dim {dim // heads} batch 150..229"))
+    say(f"  head_dim {dim // heads}: worst relative logit difference {worst:.2e}")
+    dec.close()
+
+
 def test_batched_prefill_longer_than_one_pass(hip, orc, ref, tmp_path):
     """A prompt of more rows than one batched pass holds (chunks of 512)."""
     path = mf.write_model(orc, str(tmp_path / "long.gguf"), ctx=640, vocab=300, layers=2, seed=9)
