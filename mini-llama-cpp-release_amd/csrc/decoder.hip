@@ -766,6 +766,232 @@ __global__ __launch_bounds__(kPrefillAttnThreads) void attention_rows_kernel(con
     }
 }
 
+// Causal attention of prefill rows on MFMA (head_dim HD = 64 or 128).
+// Workgroup (head h, 16 W query rows; the blocks with the most cache rows are
+// launched first), wave w: query rows 16 w .. 16 w + 15.
+// Key blocks of 32 cache rows are staged in LDS as fp16 hi + lo (K as rows,
+// V transposed), so every f32 product becomes hi*hi + hi*lo + lo*hi in
+// v_mfma_f32_16x16x32_f16 (the dropped lo*lo term is 2^-22 of the product):
+//  * scores, transposed: S^T[key][query] = K . Q^T (A = K rows of the block,
+//    B = the wave's query rows, held in registers), then times 1/sqrt(HD);
+//  * online softmax per query (lane column): the block's maximum and sum over
+//    the lane's 8 keys and the three other lanes of its column (shuffles);
+//  * O^T[d][query] += V^T . P^T: the lane's own 8 probabilities are the B
+//    operand (its keys are the slots 8g .. 8g + 7 of the transposed V tile:
+//    keys 4g .. 4g + 3 and 16 + 4g .. 16 + 4g + 3), so P never leaves
+//    registers.
+// Keys past a query's position get probability 0; cache rows past the
+// block's last position re-read that row (finite, weight 0).  The result
+// equals the reference's max - exp - sum - divide - weighted sum to rounding
+// (src/forward.cpp:584-611 and src/ops.cpp:43-71 for one row).
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
+constexpr int kMfmaAttnKeys = 32;  // cache rows per block
+
+// v = hi + lo to 2^-22 of v: hi = fp16(v), lo = fp16(v - hi).
+__device__ __forceinline__ _Float16 f16_hi(float v) { return static_cast<_Float16>(v); }
+__device__ __forceinline__ _Float16 f16_lo(float v, _Float16 hi) {
+    return static_cast<_Float16>(v - static_cast<float>(hi));
+}
+
+// Slot of key k (0..31) in a transposed V tile (the P^T operand's order).
+__device__ __forceinline__ int attn_slot(int k) { return k < 16 ? 8 * (k >> 2) + (k & 3) : 8 * ((k - 16) >> 2) + 4 + (k & 3); }
+
+template <int HD, int W, int PF>
+__global__ __launch_bounds__(64 * W) void attention_rows_mfma_kernel(const float* __restrict__ Q,
+                                                                  const float* __restrict__ kc,
+                                                                  const float* __restrict__ vc, int n_heads, int n_kv,
+                                                                  int max_seq, int layer, int start, int n,
+                                                                  float* __restrict__ out) {
+    constexpr int KB = kMfmaAttnKeys;
+    constexpr int DC = HD / 32;  // d chunks of the score products
+    constexpr int DT = HD / 16;  // d tiles of the output
+    constexpr int KROW = HD + 8;  // halves per K row in LDS (16-byte aligned, banks spread)
+    constexpr int VROW = KB + 8;  // halves per V^T row
+    constexpr int NT = 64 * W;
+    constexpr int TPK = NT / KB;        // threads per K row
+    constexpr int KPT = HD / TPK;       // K elements per thread
+    constexpr int VPT = KB * HD / NT;   // V elements per thread (one d, VPT consecutive keys)
+    static_assert(KPT % 8 == 0 && VPT % 4 == 0, "staging map");
+    static_assert(HD == 64 || HD == 128, "head_dim");
+    __shared__ __attribute__((aligned(16))) _Float16 khi[KB * KROW], klo[KB * KROW];
+    __shared__ __attribute__((aligned(16))) _Float16 vhi[HD * VROW], vlo[HD * VROW];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int i16 = lane & 15;
+    const int g = lane >> 4;
+    const int wave = tid >> 6;
+    const int h = blockIdx.x;
+    const int kvh = h / (n_heads / n_kv);
+    const size_t layer_base = static_cast<size_t>(layer) * max_seq * n_kv * HD;
+    const size_t t_stride = static_cast<size_t>(n_kv) * HD;
+    const float* kbase = kc + layer_base + kvh * HD;
+    const float* vbase = vc + layer_base + kvh * HD;
+    const int qb0 = (gridDim.y - 1 - blockIdx.y) * 16 * W;
+    const int last_pos = start + min(qb0 + 16 * W, n) - 1;  // the workgroup's last query position
+    // This lane's query (rows past n repeat row n - 1; not stored).
+    const int qrow = min(qb0 + 16 * wave + i16, n - 1);
+    const int qpos = start + qrow;
+    h8_t qh[DC], ql[DC];
+    {
+        const float* qp = Q + static_cast<size_t>(qrow) * n_heads * HD + h * HD + 8 * g;
+#pragma unroll
+        for (int c = 0; c < DC; ++c) {
+            const float4 a = *reinterpret_cast<const float4*>(qp + 32 * c);
+            const float4 b = *reinterpret_cast<const float4*>(qp + 32 * c + 4);
+            const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const _Float16 hh = f16_hi(v[j]);
+                qh[c][j] = hh;
+                ql[c][j] = f16_lo(v[j], hh);
+            }
+        }
+    }
+    // Staging maps: K thread -> key tid / TPK, elements (tid % TPK) * KPT ..;
+    // V thread -> d = tid % HD, keys (tid / HD) * VPT ...
+    const int k_key = tid / TPK;
+    const int k_d0 = (tid % TPK) * KPT;
+    const int v_d = tid % HD;
+    const int v_k0 = (tid / HD) * VPT;
+    // PF key blocks in flight: block kb is staged from register set kb % PF.
+    float kreg[PF][KPT], vreg[PF][VPT];
+    auto load_block = [&](int kb, int u) {
+        const int t = min(kb * KB + k_key, last_pos);
+        const float* kp = kbase + static_cast<size_t>(t) * t_stride + k_d0;
+#pragma unroll
+        for (int i = 0; i < KPT; i += 4) {
+            const float4 a = *reinterpret_cast<const float4*>(kp + i);
+            kreg[u][i] = a.x;
+            kreg[u][i + 1] = a.y;
+            kreg[u][i + 2] = a.z;
+            kreg[u][i + 3] = a.w;
+        }
+#pragma unroll
+        for (int i = 0; i < VPT; ++i) {
+            const int tv = min(kb * KB + v_k0 + i, last_pos);
+            vreg[u][i] = vbase[static_cast<size_t>(tv) * t_stride + v_d];
+        }
+    };
+    auto store_block = [&](int u) {
+        h8_t hk, lk;
+#pragma unroll
+        for (int i = 0; i < KPT; i += 8) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const _Float16 hh = f16_hi(kreg[u][i + j]);
+                hk[j] = hh;
+                lk[j] = f16_lo(kreg[u][i + j], hh);
+            }
+            *reinterpret_cast<h8_t*>(khi + k_key * KROW + k_d0 + i) = hk;
+            *reinterpret_cast<h8_t*>(klo + k_key * KROW + k_d0 + i) = lk;
+        }
+        typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
+#pragma unroll
+        for (int i = 0; i < VPT; i += 4) {  // four consecutive keys share four consecutive slots
+            h4_t hv, lv;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const _Float16 hh = f16_hi(vreg[u][i + j]);
+                hv[j] = hh;
+                lv[j] = f16_lo(vreg[u][i + j], hh);
+            }
+            const int slot = attn_slot(v_k0 + i);
+            *reinterpret_cast<h4_t*>(vhi + v_d * VROW + slot) = hv;
+            *reinterpret_cast<h4_t*>(vlo + v_d * VROW + slot) = lv;
+        }
+    };
+    const float scale = 1.0f / sqrtf(static_cast<float>(HD));
+    const f4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
+    f4_t o[DT];
+#pragma unroll
+    for (int t = 0; t < DT; ++t) o[t] = zero;
+    float m = -INFINITY, l = 0.0f;
+    const int nkb = last_pos / KB + 1;
+#pragma unroll
+    for (int u = 0; u < PF; ++u)
+        if (u < nkb) load_block(u, u);
+    auto step = [&](int kb, int u) {
+        __syncthreads();  // the previous block's readers are done
+        store_block(u);
+        __syncthreads();
+        if (kb + PF < nkb) load_block(kb + PF, u);
+        // S^T for the two 16-key tiles: three product terms in separate
+        // accumulators (independent MFMA chains), summed after.
+        f4_t s[2];
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+            f4_t a0 = zero, a1 = zero, a2 = zero;
+            const _Float16* kh = khi + (16 * kt + i16) * KROW + 8 * g;
+            const _Float16* kl = klo + (16 * kt + i16) * KROW + 8 * g;
+#pragma unroll
+            for (int c = 0; c < DC; ++c) {
+                const h8_t ah = *reinterpret_cast<const h8_t*>(kh + 32 * c);
+                const h8_t al = *reinterpret_cast<const h8_t*>(kl + 32 * c);
+                a0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, qh[c], a0, 0, 0, 0);
+                a1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, ql[c], a1, 0, 0, 0);
+                a2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, qh[c], a2, 0, 0, 0);
+            }
+            s[kt] = a0 + (a1 + a2);
+        }
+        // Scores of this lane: keys kb*32 + 16 kt + 4 g + q for query qpos.
+        float sc[8];
+        float bm = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int key = kb * KB + 16 * kt + 4 * g + q;
+                const float v = key <= qpos ? s[kt][q] * scale : -INFINITY;
+                sc[4 * kt + q] = v;
+                bm = fmaxf(bm, v);
+            }
+        bm = fmaxf(bm, __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, bm), 0x401F)));
+        bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+        const float mn = fmaxf(m, bm);
+        const float base = mn == -INFINITY ? 0.0f : mn;
+        const float c_old = expf(m - base);
+        float ps = 0.0f;
+        h8_t ph, pl;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float p = expf(sc[j] - base);
+            ps += p;
+            const _Float16 hh = f16_hi(p);
+            ph[j] = hh;
+            pl[j] = f16_lo(p, hh);
+        }
+        ps += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, ps), 0x401F));
+        ps += __shfl_xor(ps, 32, 64);
+        l = l * c_old + ps;
+        m = mn;
+#pragma unroll
+        for (int t = 0; t < DT; ++t) {
+            f4_t a0 = o[t] * c_old, a1 = zero, a2 = zero;
+            const h8_t vh = *reinterpret_cast<const h8_t*>(vhi + (16 * t + i16) * VROW + 8 * g);
+            const h8_t vl = *reinterpret_cast<const h8_t*>(vlo + (16 * t + i16) * VROW + 8 * g);
+            a0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, ph, a0, 0, 0, 0);
+            a1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, pl, a1, 0, 0, 0);
+            a2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(vl, ph, a2, 0, 0, 0);
+            o[t] = a0 + (a1 + a2);
+        }
+    };
+    for (int kb0 = 0; kb0 < nkb; kb0 += PF) {
+#pragma unroll
+        for (int u = 0; u < PF; ++u)
+            if (kb0 + u < nkb) step(kb0 + u, u);
+    }
+    // O^T[d = 16 t + 4 g + q][this lane's query] / l.
+    if (qb0 + 16 * wave + i16 < n) {
+        const float inv = 1.0f / l;
+        float* op = out + static_cast<size_t>(qrow) * n_heads * HD + h * HD + 4 * g;
+#pragma unroll
+        for (int t = 0; t < DT; ++t)
+            *reinterpret_cast<float4*>(op + 16 * t) =
+                make_float4(o[t][0] * inv, o[t][1] * inv, o[t][2] * inv, o[t][3] * inv);
+    }
+}
+
 // Y[r][M] = W[M][K] . X[r] for F32 weights: one wave per (row of W, row of X).
 __global__ __launch_bounds__(256) void gemm_f32_kernel(const float* __restrict__ W, const float* __restrict__ X,
                                                        float* __restrict__ Y, int M, int K) {
@@ -1490,6 +1716,9 @@ void Decoder::enqueue_prefill(hipStream_t s, const int32_t* tokens, int n, int s
                            L.bq, L.bk, L.bv, c.n_heads, c.n_kv_heads, c.head_dim, c.rope_theta, c.rope_neox,
                            c.max_seq_len, l, start, kcache_, vcache_);
         check(hipGetLastError(), "rope_kv_rows_kernel");
+#define MLQ_ATTN_MFMA(HD, W)                                                                                      \
+    hipLaunchKernelGGL((attention_rows_mfma_kernel<HD, W, 2>), dim3(c.n_heads, (n + 16 * W - 1) / (16 * W)),        \
+                       dim3(64 * W), 0, s, Q_, kcache_, vcache_, c.n_heads, c.n_kv_heads, c.max_seq_len, l, start, n, ATT_)
 #define MLQ_ATTN_ROWS(LPR, V4, QR, A)                                                                           \
     hipLaunchKernelGGL((attention_rows_kernel<LPR, V4, QR, A>), dim3(c.n_heads, (n + QR - 1) / QR),            \
                        dim3(kPrefillAttnThreads), 0, s, Q_, kcache_, vcache_, c.n_heads, c.n_kv_heads, c.max_seq_len, l, \
@@ -1502,11 +1731,12 @@ void Decoder::enqueue_prefill(hipStream_t s, const int32_t* tokens, int n, int s
         switch (c.head_dim) {
             case 16: MLQ_ATTN_ROWS(4, 1, 4, 2); break;
             case 32: MLQ_ATTN_ROWS(8, 1, 4, 2); break;
-            case 64: MLQ_ATTN_ROWS(8, 2, 4, 2); break;
-            case 128: MLQ_ATTN_ROWS(16, 2, 4, 2); break;
+            case 64: MLQ_ATTN_MFMA(64, 4); break;
+            case 128: MLQ_ATTN_MFMA(128, 4); break;
             default: MLQ_ATTN_ROWS(32, 2, 4, 2); break;
         }
 #undef MLQ_ATTN_ROWS
+#undef MLQ_ATTN_MFMA
         check(hipGetLastError(), "attention_rows_kernel");
         linear_rows(s, L.wo, ATT_, PROJ_, n);
         hipLaunchKernelGGL(add_rmsnorm_rows_kernel, dim3(n), dim3(kNormThreads), 0, s, X_, PROJ_, L.ffn_norm, c.dim,
