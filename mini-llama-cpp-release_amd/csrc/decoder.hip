@@ -521,54 +521,62 @@ __global__ __launch_bounds__(kNormThreads) void add_rmsnorm_rows_kernel(float* _
     for (int i = threadIdx.x; i < dim; i += kNormThreads) H[off + i] = x[i] * scale * w[i];
 }
 
-// rope_kv_kernel for every row (position start + r).
+// rope_kv_kernel for every row (position start + r): workgroups (0 .. R-1,
+// row) rotate the row's q and k heads and write k to the cache; workgroups
+// (R.., row) copy v (+ bias) to the cache.  Thread (hg, r) of rotating
+// workgroup b computes the angle of pair r once (the same expressions as
+// rope_kv_kernel, so the same values) and applies it to heads
+// b HG + hg, (b + R) HG + hg, ... of q and then k (HG = 256 / (hd / 2)): one
+// cosf / sinf / powf per pair index and workgroup instead of one per rotated
+// pair.
 __global__ __launch_bounds__(256) void rope_kv_rows_kernel(float* __restrict__ Q, float* __restrict__ K,
                                                            const float* __restrict__ V, const float* __restrict__ bq,
                                                            const float* __restrict__ bk, const float* __restrict__ bv,
                                                            int n_heads, int n_kv, int hd, float theta, int neox,
                                                            int max_seq, int layer, int start, float* __restrict__ kc,
-                                                           float* __restrict__ vc) {
+                                                           float* __restrict__ vc, int rot_wgs) {
     const int row = blockIdx.y;
     const int pos = start + row;
     const int half = hd / 2;
-    const int nq = n_heads * half;
-    const int nk = n_kv * half;
     const int nv = n_kv * hd;
+    const size_t cache_row = (static_cast<size_t>(layer) * max_seq + pos) * nv;
+    if (static_cast<int>(blockIdx.x) >= rot_wgs) {
+        const int e = (blockIdx.x - rot_wgs) * blockDim.x + threadIdx.x;
+        const float* v = V + static_cast<size_t>(row) * nv;
+        if (e < nv) vc[cache_row + e] = bv != nullptr ? v[e] + bv[e] : v[e];
+        return;
+    }
+    const int HG = static_cast<int>(blockDim.x) / half;  // head groups (hd <= 512)
+    const int hg = threadIdx.x / half;
+    const int r = threadIdx.x % half;
+    if (hg >= HG) return;
     float* q = Q + static_cast<size_t>(row) * n_heads * hd;
     float* k = K + static_cast<size_t>(row) * nv;
-    const float* v = V + static_cast<size_t>(row) * nv;
-    const size_t cache_row = (static_cast<size_t>(layer) * max_seq + pos) * nv;
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < nq + nk) {
-        const bool is_q = i < nq;
-        const int j = is_q ? i : i - nq;
-        const int h = j / half;
-        const int r = j % half;
-        const int i0 = h * hd + (neox ? r : 2 * r);
-        const int i1 = neox ? i0 + half : i0 + 1;
-        const float freq = 1.0f / powf(theta, static_cast<float>(2 * r) / static_cast<float>(hd));
-        const float ang = static_cast<float>(pos) * freq;
-        const float c = cosf(ang);
-        const float s = sinf(ang);
-        float* t = is_q ? q : k;
+    const float freq = 1.0f / powf(theta, static_cast<float>(2 * r) / static_cast<float>(hd));
+    const float ang = static_cast<float>(pos) * freq;
+    const float c = cosf(ang);
+    const float sn = sinf(ang);
+    const int o0 = neox ? r : 2 * r;
+    const int o1 = neox ? r + half : 2 * r + 1;
+    for (int h = blockIdx.x * HG + hg; h < n_heads + n_kv; h += rot_wgs * HG) {
+        const bool is_q = h < n_heads;
+        const int hh = is_q ? h : h - n_heads;
+        float* t = (is_q ? q : k) + hh * hd;
         const float* b = is_q ? bq : bk;
-        float a0 = t[i0];
-        float a1 = t[i1];
+        float a0 = t[o0];
+        float a1 = t[o1];
         if (b != nullptr) {
-            a0 = a0 + b[i0];
-            a1 = a1 + b[i1];
+            a0 = a0 + b[hh * hd + o0];
+            a1 = a1 + b[hh * hd + o1];
         }
-        const float r0 = a0 * c - a1 * s;
-        const float r1 = a0 * s + a1 * c;
-        t[i0] = r0;
-        t[i1] = r1;
+        const float r0 = a0 * c - a1 * sn;
+        const float r1 = a0 * sn + a1 * c;
+        t[o0] = r0;
+        t[o1] = r1;
         if (!is_q) {
-            kc[cache_row + i0] = r0;
-            kc[cache_row + i1] = r1;
+            kc[cache_row + hh * hd + o0] = r0;
+            kc[cache_row + hh * hd + o1] = r1;
         }
-    } else if (i < nq + nk + nv) {
-        const int e = i - nq - nk;
-        vc[cache_row + e] = bv != nullptr ? v[e] + bv[e] : v[e];
     }
 }
 
@@ -1711,10 +1719,12 @@ void Decoder::enqueue_prefill(hipStream_t s, const int32_t* tokens, int n, int s
             float* y[3] = {Q_, K_, V_};
             linear_rows_group(s, 3, w, H_, y, n);
         }
-        const int rope_threads = q_dim / 2 + kv_dim / 2 + kv_dim;
-        hipLaunchKernelGGL(rope_kv_rows_kernel, dim3((rope_threads + 255) / 256, n), dim3(256), 0, s, Q_, K_, V_,
-                           L.bq, L.bk, L.bv, c.n_heads, c.n_kv_heads, c.head_dim, c.rope_theta, c.rope_neox,
-                           c.max_seq_len, l, start, kcache_, vcache_);
+        // Rotating workgroups: about four head steps each.
+        const int rope_hg = 256 / (c.head_dim / 2);
+        const int rot_wgs = std::max(1, (c.n_heads + c.n_kv_heads + 4 * rope_hg - 1) / (4 * rope_hg));
+        hipLaunchKernelGGL(rope_kv_rows_kernel, dim3(rot_wgs + (kv_dim + 255) / 256, n), dim3(256), 0, s, Q_, K_,
+                           V_, L.bq, L.bk, L.bv, c.n_heads, c.n_kv_heads, c.head_dim, c.rope_theta, c.rope_neox,
+                           c.max_seq_len, l, start, kcache_, vcache_, rot_wgs);
         check(hipGetLastError(), "rope_kv_rows_kernel");
 #define MLQ_ATTN_MFMA(HD, W)                                                                                      \
     hipLaunchKernelGGL((attention_rows_mfma_kernel<HD, W, 2>), dim3(c.n_heads, (n + 16 * W - 1) / (16 * W)),        \
