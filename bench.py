@@ -566,6 +566,33 @@ def decode_steps_bench(steps):
             "note": "each step synchronizes and downloads the logits (forward_token)"}
 
 
+def prefill_steps_bench(runs=3, tokens=512):
+    """Batched prefill only (mlq_hip_decoder_prefill, no generation) of a
+    `tokens`-token prompt on the model of decode_bench: one warm-up, then
+    `runs` timed prefills (for kernel profiles of the prefill path)."""
+    import tempfile
+
+    fd, path = tempfile.mkstemp(suffix=".gguf")
+    os.close(fd)
+    try:
+        write_llama7b_q4_0(path)
+        dec = hip.Decoder(path, max_seq_len=max(2048, tokens))
+    finally:
+        os.unlink(path)
+    prompt = (np.arange(tokens) * 7 % 32000).tolist()
+    dec.prefill(prompt)
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        dec.prefill(prompt)
+        times.append(time.perf_counter() - t0)
+    dec.close()
+    med = sorted(times)[len(times) // 2]
+    return {"prefill_tokens": tokens, "runs": runs, "ms": [round(t * 1e3, 3) for t in times],
+            "tokens_per_s_median": round(tokens / med, 1),
+            "note": "one warm-up prefill, then the timed ones; each returns the last row's logits to the host"}
+
+
 PICK_CONFIGS = ([("c2_qwen_lm_head", qt, 151936, 896) for qt in (hip.Q8_0, hip.Q4_0, hip.Q4_1)] +
                 [("c3_llama_lm_head", qt, 32000, 4096) for qt in (hip.Q8_0, hip.Q4_0, hip.Q4_1)])
 
@@ -836,6 +863,9 @@ def main():
     ap.add_argument("--decode-steps", type=int, default=0,
                     help="with --decode-only: instead run this many single forward() steps (one launch "
                          "sequence per token, no recorded graph) on the same model, for kernel profiles")
+    ap.add_argument("--prefill-runs", type=int, default=0,
+                    help="with --decode-only: instead run only batched prefills of a 512-token prompt "
+                         "(one warm-up, then this many timed), for kernel profiles of the prefill path")
     ap.add_argument("--gemm-only", action="store_true",
                     help="run only the prefill GEMM table (config 4) and print it as one JSON line")
     ap.add_argument("--gemm-filter", default="",
@@ -877,6 +907,8 @@ def main():
         hip.init(0)
         if args.decode_steps > 0:
             emit(decode_steps_bench(args.decode_steps))
+        elif args.prefill_runs > 0:
+            emit(prefill_steps_bench(args.prefill_runs))
         else:
             emit(decode_bench())
         return
