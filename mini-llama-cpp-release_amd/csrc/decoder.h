@@ -10,6 +10,8 @@
 // token, with the greedy pick of one step feeding the next.
 #pragma once
 
+#include "mlq_kernels.h"
+
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -106,6 +108,18 @@ private:
     // launch when the shapes allow it, else one linear_rows each.
     void linear_rows_group(hipStream_t s, int n, const Linear* const* w, const float* X, float* const* Y, int rows);
     void ensure_workspace(hipStream_t s, size_t need);
+    // A prefill GEMM (1-3 linears over one x) whose producer writes the split
+    // x straight into the workspace (gemm_split_x).
+    struct SplitTarget {
+        int ng = 0;
+        const void* w[3] = {};
+        int M[3] = {};
+        LinearShape shape{};
+        GemmSplitX sx{};
+    };
+    bool split_target(int ng, const Linear* const* w, int rows, SplitTarget& t) const;
+    void gemm_split(hipStream_t s, const SplitTarget& t, float* const* Y);
+    void norm_into(hipStream_t s, const SplitTarget* t, float* X, const float* D, const float* w, int n);
     void linear_fused(hipStream_t s, const Linear* const* ws, float* const* ys, int n, const float* x,
                       const float* norm_w, bool acc);
     void enqueue_prefill(hipStream_t s, const int32_t* tokens, int n, int start);

@@ -12,6 +12,7 @@
 #include "gguf_index.h"
 #include "mlq_kernels.h"
 #include "pick_key.h"
+#include "xsplit_device.h"
 
 #include "../../include/mlq_hip.h"
 
@@ -519,6 +520,105 @@ __global__ __launch_bounds__(kNormThreads) void add_rmsnorm_rows_kernel(float* _
     ss = wg_reduce<kNormThreads, false>(ss, part);
     const float scale = 1.0f / sqrtf(ss / static_cast<float>(dim) + eps);
     for (int i = threadIdx.x; i < dim; i += kNormThreads) H[off + i] = x[i] * scale * w[i];
+}
+
+// Row kernels whose output goes straight to a prefill GEMM as its split x
+// (xsplit_device.h; the GEMM then makes no split launch of its own).
+// Workgroup `row` of 256 threads holds the row's half blocks in registers
+// (thread t: half blocks t + 256 c); rows n .. npad - 1 write a zero split
+// (the GEMM's padded token tile).  C = ceil(2 nb / 256) half blocks per
+// thread (dim = 32 nb <= 256 * 16 * kXsCache).
+//
+// add_rmsnorm_rows_kernel's step for a GEMM input: X[r] += D[r] (when given),
+// then the split of rmsnorm(X[r]) * w.
+template <int QT, int C>
+__global__ __launch_bounds__(256) void add_rmsnorm_split_rows_kernel(float* __restrict__ X,
+                                                                     const float* __restrict__ D,
+                                                                     const float* __restrict__ w, int dim, float eps,
+                                                                     int n, int nb, _Float16* __restrict__ xs,
+                                                                     float* __restrict__ bsum,
+                                                                     float* __restrict__ scale) {
+    __shared__ float part[4];
+    const int row = blockIdx.x;
+    const bool valid = row < n;
+    const size_t off = static_cast<size_t>(valid ? row : 0) * dim;
+    float v[C][16], wv[C][16];
+    float ss = 0.0f;
+    // The norm weights are requested with the row (they do not depend on it).
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+        const int k0 = 16 * (static_cast<int>(threadIdx.x) + 256 * c);
+        const bool in = k0 < dim;
+#pragma unroll
+        for (int i = 0; i < 16; i += 4) {
+            const float4 a = in ? *reinterpret_cast<const float4*>(w + k0 + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            wv[c][i] = a.x;
+            wv[c][i + 1] = a.y;
+            wv[c][i + 2] = a.z;
+            wv[c][i + 3] = a.w;
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+        const int k0 = 16 * (static_cast<int>(threadIdx.x) + 256 * c);
+        const bool in = valid && k0 < dim;
+#pragma unroll
+        for (int i = 0; i < 16; i += 4) {
+            float4 a = in ? *reinterpret_cast<const float4*>(X + off + k0 + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (in && D != nullptr) {
+                const float4 d = *reinterpret_cast<const float4*>(D + off + k0 + i);
+                a = make_float4(a.x + d.x, a.y + d.y, a.z + d.z, a.w + d.w);
+                *reinterpret_cast<float4*>(X + off + k0 + i) = a;
+            }
+            v[c][i] = a.x;
+            v[c][i + 1] = a.y;
+            v[c][i + 2] = a.z;
+            v[c][i + 3] = a.w;
+            ss += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w;
+        }
+    }
+    ss = wg_reduce<256, false>(ss, part);
+    const float sc = 1.0f / sqrtf(ss / static_cast<float>(dim) + eps);
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+        const int k0 = 16 * (static_cast<int>(threadIdx.x) + 256 * c);
+        if (valid && k0 < dim) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) v[c][i] = v[c][i] * sc * wv[c][i];
+        }
+    }
+    __syncthreads();  // part is reused by the split's maximum
+    xsplit_emit_row<QT, C>(row, nb, v, xs, bsum, scale, part);
+}
+
+// swiglu_kernel's step for a GEMM input: the split of silu(g) * u per row.
+template <int QT, int C>
+__global__ __launch_bounds__(256) void swiglu_split_rows_kernel(const float* __restrict__ G,
+                                                                const float* __restrict__ U, int hidden, int n,
+                                                                int nb, _Float16* __restrict__ xs,
+                                                                float* __restrict__ bsum, float* __restrict__ scale) {
+    __shared__ float red[4];
+    const int row = blockIdx.x;
+    const bool valid = row < n;
+    const size_t off = static_cast<size_t>(valid ? row : 0) * hidden;
+    float v[C][16];
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+        const int k0 = 16 * (static_cast<int>(threadIdx.x) + 256 * c);
+        const bool in = valid && k0 < hidden;
+#pragma unroll
+        for (int i = 0; i < 16; i += 4) {
+            const float4 g = in ? *reinterpret_cast<const float4*>(G + off + k0 + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            const float4 u = in ? *reinterpret_cast<const float4*>(U + off + k0 + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            const float gv[4] = {g.x, g.y, g.z, g.w}, uv[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float sig = 1.0f / (1.0f + expf(-gv[e]));
+                v[c][i + e] = in ? gv[e] * sig * uv[e] : 0.0f;
+            }
+        }
+    }
+    xsplit_emit_row<QT, C>(row, nb, v, xs, bsum, scale, red);
 }
 
 // rope_kv_kernel for every row (position start + r): workgroups (0 .. R-1,
@@ -1702,22 +1802,104 @@ bool Decoder::prefill_batched() const {
 // forward_batch over tokens[0..n) (device pointer) at positions start..:
 // every layer for all rows at once; X_ row n-1 ends as the last token's
 // residual stream (its final norm and lm_head are the caller's).
+// Where the GEMM of `ng` weights over `rows` rows reads a split x that the
+// kernel producing its input can write itself (same qtype and K for all, a
+// chunk GEMM that splits x, K <= 16 384); false: the usual plain-x path.
+bool Decoder::split_target(int ng, const Linear* const* w, int rows, SplitTarget& t) const {
+    for (int g = 0; g < ng; ++g) {
+        if (w[g]->qtype == 0 || w[g]->qtype != w[0]->qtype || w[g]->K != w[0]->K) return false;
+        t.M[g] = w[g]->M;
+        t.w[g] = w[g]->data;
+    }
+    const int K = w[0]->K;
+    if (K % 32 != 0 || K > 256 * kXsCache * 16) return false;
+    t.ng = ng;
+    t.shape = LinearShape{w[0]->qtype, 0, K, K / 32, rows};
+    for (int g = 0; g < ng; ++g) t.shape.M += t.M[g];
+    t.sx = gemm_split_x(t.shape, ng, t.M);
+    return t.sx.ok;
+}
+
+namespace {
+// C = half blocks per thread, from the row width (at most kXsCache).
+template <int QT>
+void launch_norm_split(hipStream_t s, int npad, float* X, const float* D, const float* w, int dim, float eps, int n,
+                       char* ws, const GemmSplitX& sx) {
+    auto go = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, dim3(npad), dim3(256), 0, s, X, D, w, dim, eps, n, dim / 32,
+                           reinterpret_cast<_Float16*>(ws + sx.xs), reinterpret_cast<float*>(ws + sx.bsum),
+                           reinterpret_cast<float*>(ws + sx.scale));
+    };
+    switch ((dim / 16 + 255) / 256) {
+        case 1: go(add_rmsnorm_split_rows_kernel<QT, 1>); break;
+        case 2: go(add_rmsnorm_split_rows_kernel<QT, 2>); break;
+        case 3: go(add_rmsnorm_split_rows_kernel<QT, 3>); break;
+        default: go(add_rmsnorm_split_rows_kernel<QT, 4>); break;
+    }
+}
+template <int QT>
+void launch_swiglu_split(hipStream_t s, int npad, const float* G, const float* U, int hidden, int n, char* ws,
+                         const GemmSplitX& sx) {
+    auto go = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, dim3(npad), dim3(256), 0, s, G, U, hidden, n, hidden / 32,
+                           reinterpret_cast<_Float16*>(ws + sx.xs), reinterpret_cast<float*>(ws + sx.bsum),
+                           reinterpret_cast<float*>(ws + sx.scale));
+    };
+    switch ((hidden / 16 + 255) / 256) {
+        case 1: go(swiglu_split_rows_kernel<QT, 1>); break;
+        case 2: go(swiglu_split_rows_kernel<QT, 2>); break;
+        case 3: go(swiglu_split_rows_kernel<QT, 3>); break;
+        default: go(swiglu_split_rows_kernel<QT, 4>); break;
+    }
+}
+}  // namespace
+
+// The GEMM of a split target whose split x is in the workspace.
+void Decoder::gemm_split(hipStream_t s, const SplitTarget& t, float* const* Y) {
+    check(launch_gemm_group(t.shape, t.ng, t.w, Y, t.M, nullptr, ws_, ws_bytes_, s, true), "launch_gemm_group");
+}
+
+// X += D (when given), then the rmsnorm of X times w into the GEMM of `t`:
+// written split into the workspace when t is a split target, else as H.
+void Decoder::norm_into(hipStream_t s, const SplitTarget* t, float* X, const float* D, const float* w, int n) {
+    const DecoderConfig& c = cfg_;
+    if (t == nullptr) {
+        hipLaunchKernelGGL(add_rmsnorm_rows_kernel, dim3(n), dim3(kNormThreads), 0, s, X, D, w, c.dim,
+                           c.rms_norm_eps, H_);
+        check(hipGetLastError(), "add_rmsnorm_rows_kernel");
+        return;
+    }
+    ensure_workspace(s, t->sx.ws_bytes);
+    char* ws = static_cast<char*>(ws_);
+    switch (t->shape.qtype) {
+        case 1: launch_norm_split<1>(s, t->sx.npad, X, D, w, c.dim, c.rms_norm_eps, n, ws, t->sx); break;
+        case 2: launch_norm_split<2>(s, t->sx.npad, X, D, w, c.dim, c.rms_norm_eps, n, ws, t->sx); break;
+        default: launch_norm_split<3>(s, t->sx.npad, X, D, w, c.dim, c.rms_norm_eps, n, ws, t->sx); break;
+    }
+    check(hipGetLastError(), "add_rmsnorm_split_rows_kernel");
+}
+
 void Decoder::enqueue_prefill(hipStream_t s, const int32_t* tokens, int n, int start) {
     const DecoderConfig& c = cfg_;
-    const int q_dim = c.n_heads * c.head_dim;
     const int kv_dim = c.n_kv_heads * c.head_dim;
     hipLaunchKernelGGL(embed_rows_kernel, dim3((c.dim + 255) / 256, n), dim3(256), 0, s, embedding_, c.vocab_size,
                        c.dim, tokens, state_, X_);
     check(hipGetLastError(), "embed_rows_kernel");
     for (int l = 0; l < c.n_layers; ++l) {
         const Layer& L = layers_[l];
-        hipLaunchKernelGGL(add_rmsnorm_rows_kernel, dim3(n), dim3(kNormThreads), 0, s, X_, l == 0 ? nullptr : FF_,
-                           L.attn_norm, c.dim, c.rms_norm_eps, H_);
-        check(hipGetLastError(), "add_rmsnorm_rows_kernel");
+        // q/k/v: the attention RMSNorm writes the grouped GEMM's split x
+        // itself where the GEMM splits x (saves the split launch per GEMM).
         {
             const Linear* w[3] = {&L.wq, &L.wk, &L.wv};
             float* y[3] = {Q_, K_, V_};
-            linear_rows_group(s, 3, w, H_, y, n);
+            SplitTarget t;
+            if (split_target(3, w, n, t)) {
+                norm_into(s, &t, X_, l == 0 ? nullptr : FF_, L.attn_norm, n);
+                gemm_split(s, t, y);
+            } else {
+                norm_into(s, nullptr, X_, l == 0 ? nullptr : FF_, L.attn_norm, n);
+                linear_rows_group(s, 3, w, H_, y, n);
+            }
         }
         // Rotating workgroups: about four head steps each.
         const int rope_hg = 256 / (c.head_dim / 2);
@@ -1749,18 +1931,39 @@ void Decoder::enqueue_prefill(hipStream_t s, const int32_t* tokens, int n, int s
 #undef MLQ_ATTN_MFMA
         check(hipGetLastError(), "attention_rows_kernel");
         linear_rows(s, L.wo, ATT_, PROJ_, n);
-        hipLaunchKernelGGL(add_rmsnorm_rows_kernel, dim3(n), dim3(kNormThreads), 0, s, X_, PROJ_, L.ffn_norm, c.dim,
-                           c.rms_norm_eps, H_);
-        check(hipGetLastError(), "add_rmsnorm_rows_kernel");
         {
             const Linear* w[2] = {&L.w_gate, &L.w_up};
             float* y[2] = {GATE_, UP_};
-            linear_rows_group(s, 2, w, H_, y, n);
+            SplitTarget t;
+            if (split_target(2, w, n, t)) {
+                norm_into(s, &t, X_, PROJ_, L.ffn_norm, n);
+                gemm_split(s, t, y);
+            } else {
+                norm_into(s, nullptr, X_, PROJ_, L.ffn_norm, n);
+                linear_rows_group(s, 2, w, H_, y, n);
+            }
         }
-        const int nh = n * c.hidden_dim;
-        hipLaunchKernelGGL(swiglu_kernel, dim3((nh + 255) / 256), dim3(256), 0, s, GATE_, UP_, ACT_, nh);
-        check(hipGetLastError(), "swiglu_kernel");
-        linear_rows(s, L.w_down, ACT_, FF_, n);
+        {
+            const Linear* w[1] = {&L.w_down};
+            float* y[1] = {FF_};
+            SplitTarget t;
+            if (split_target(1, w, n, t)) {
+                ensure_workspace(s, t.sx.ws_bytes);
+                char* ws = static_cast<char*>(ws_);
+                switch (t.shape.qtype) {
+                    case 1: launch_swiglu_split<1>(s, t.sx.npad, GATE_, UP_, c.hidden_dim, n, ws, t.sx); break;
+                    case 2: launch_swiglu_split<2>(s, t.sx.npad, GATE_, UP_, c.hidden_dim, n, ws, t.sx); break;
+                    default: launch_swiglu_split<3>(s, t.sx.npad, GATE_, UP_, c.hidden_dim, n, ws, t.sx); break;
+                }
+                check(hipGetLastError(), "swiglu_split_rows_kernel");
+                gemm_split(s, t, y);
+            } else {
+                const int nh = n * c.hidden_dim;
+                hipLaunchKernelGGL(swiglu_kernel, dim3((nh + 255) / 256), dim3(256), 0, s, GATE_, UP_, ACT_, nh);
+                check(hipGetLastError(), "swiglu_kernel");
+                linear_rows(s, L.w_down, ACT_, FF_, n);
+            }
+        }
     }
     // Residual of the last layer into the rows' streams.
     hipLaunchKernelGGL(add_rmsnorm_rows_kernel, dim3(n), dim3(kNormThreads), 0, s, X_, FF_, final_norm_, c.dim,

@@ -36,6 +36,7 @@
 // needs an even block count per row; other shapes use the GEMV kernels per row.
 
 #include "mlq_kernels.h"
+#include "xsplit_device.h"
 
 #include <hip/hip_runtime.h>
 
@@ -73,14 +74,14 @@ __device__ __forceinline__ int slot_k(int g, int j) {
 // t, t + 256, ... (16 consecutive floats each, so a wave reads 4 KB contiguous).
 // The first kXsCache of them stay in registers between the two passes (the
 // max|x| of the row, then the scaled split), so rows up to 16 384 elements are
-// read once; longer rows re-read the rest (L2 hits).
-constexpr int kXsCache = 4;
-
+// read once; longer rows re-read the rest (L2 hits).  The split itself is
+// xsplit_device.h's, which kernels producing a GEMM input also use.
 template <int QT>
 __global__ __launch_bounds__(256) void xsplit_kernel(const float* __restrict__ x, int N, int K,
                                                      int nb, int npad, _Float16* __restrict__ xs,
                                                      float* __restrict__ bsum,
                                                      float* __restrict__ scale) {
+    (void)npad;
     const int n = blockIdx.x;
     const bool valid = n < N;
     const float* xr = x + static_cast<size_t>(valid ? n : 0) * K;
@@ -108,102 +109,35 @@ __global__ __launch_bounds__(256) void xsplit_kernel(const float* __restrict__ x
     };
 
     float cache[kXsCache][16];
+#pragma unroll
+    for (int c = 0; c < kXsCache; ++c) load16(threadIdx.x + 256 * c, cache[c]);
+    if (nhb <= 256 * kXsCache) {
+        xsplit_emit_row<QT, kXsCache>(n, nb, cache, xs, bsum, scale, red);
+        return;
+    }
     float mx = 0.0f;
 #pragma unroll
-    for (int c = 0; c < kXsCache; ++c) {
-        load16(threadIdx.x + 256 * c, cache[c]);
+    for (int c = 0; c < kXsCache; ++c)
 #pragma unroll
         for (int i = 0; i < 16; ++i) mx = fmaxf(mx, fabsf(cache[c][i]));
-    }
     for (int hb = threadIdx.x + 256 * kXsCache; hb < nhb; hb += 256) {
         float v[16];
         load16(hb, v);
 #pragma unroll
         for (int i = 0; i < 16; ++i) mx = fmaxf(mx, fabsf(v[i]));
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
-    __syncthreads();
-    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-
-    // power-of-two scale: mx * inv in [2^13, 2^14)
-    float inv = 1.0f, sc = 1.0f;
-    if (mx > 0.0f && mx <= 3.0e38f) {
-        int ex = 0;
-        (void)frexpf(mx, &ex);  // mx in [2^(ex-1), 2^ex)
-        const int e = min(126, max(-126, 14 - ex));
-        inv = ldexpf(1.0f, e);
-        sc = ldexpf(1.0f, -e);
-    }
+    mx = xsplit_row_max(mx, red);
+    float inv, sc;
+    xsplit_scale(mx, inv, sc);
     if (threadIdx.x == 0) scale[n] = sc;
-
-    // Scale, split and store one half block.  Called uniformly by all lanes
-    // (the shuffle pairs half blocks hb and hb ^ 1, held by adjacent lanes).
-    auto emit = [&](int hb, float (&v)[16]) {
-        const bool have = hb < nhb;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) v[i] *= inv;
-        float sum = 0.0f;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) sum += (v[4 * q] + v[4 * q + 1]) + (v[4 * q + 2] + v[4 * q + 3]);
-        const float other = __shfl_xor(sum, 1, 64);
-        const int b = hb >> 1;
-        const int half = hb & 1;
-        if (!have) return;
-        if (half == 0) {
-            // block sum in the order (elements 0..15) + (16..31), 4-element groups
-            bsum[static_cast<size_t>(n) * nb + b] = sum + other;
-        }
-        _Float16 hi[16], lo[16];
-        // hi/lo in slot order of this half block
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            int e;  // element (0..15 within the half) that lands in the j-th slot of the half
-            if (QT == 1) {
-                e = j;
-            } else {
-                const int t = j & 3;
-                e = 4 * (j >> 2) + ((t == 1) ? 2 : (t == 2) ? 1 : t);
-            }
-            const float f = v[e];
-            const _Float16 h = static_cast<_Float16>(f);
-            hi[j] = h;
-            lo[j] = static_cast<_Float16>(f - static_cast<float>(h));
-        }
-        _Float16* dst = xs + (static_cast<size_t>(n) * nb + b) * 64;
-        if (QT == 1) {
-            // slots 16*half .. +15 (two 16-byte chunks) for hi, +32 for lo
-#pragma unroll
-            for (int c = 0; c < 2; ++c) {
-                *reinterpret_cast<f16x8*>(dst + 16 * half + 8 * c) =
-                    f16x8{hi[8 * c], hi[8 * c + 1], hi[8 * c + 2], hi[8 * c + 3], hi[8 * c + 4], hi[8 * c + 5],
-                          hi[8 * c + 6], hi[8 * c + 7]};
-                *reinterpret_cast<f16x8*>(dst + 32 + 16 * half + 8 * c) =
-                    f16x8{lo[8 * c], lo[8 * c + 1], lo[8 * c + 2], lo[8 * c + 3], lo[8 * c + 4], lo[8 * c + 5],
-                          lo[8 * c + 6], lo[8 * c + 7]};
-            }
-        } else {
-            // group g's slots 8g + 4*half .. +3 hold this half's elements 4g .. 4g+3
-            typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                *reinterpret_cast<f16x4*>(dst + 8 * g + 4 * half) =
-                    f16x4{hi[4 * g], hi[4 * g + 1], hi[4 * g + 2], hi[4 * g + 3]};
-                *reinterpret_cast<f16x4*>(dst + 32 + 8 * g + 4 * half) =
-                    f16x4{lo[4 * g], lo[4 * g + 1], lo[4 * g + 2], lo[4 * g + 3]};
-            }
-        }
-    };
     const int iters = (nhb + 255) / 256;  // uniform across the workgroup
 #pragma unroll
-    for (int c = 0; c < kXsCache; ++c)
-        if (c < iters) emit(threadIdx.x + 256 * c, cache[c]);
+    for (int c = 0; c < kXsCache; ++c) xsplit_emit_half<QT>(n, nb, threadIdx.x + 256 * c, cache[c], inv, xs, bsum);
     for (int it = kXsCache; it < iters; ++it) {
         float v[16];
         const int hb = threadIdx.x + 256 * it;
         load16(hb, v);
-        emit(hb, v);
+        xsplit_emit_half<QT>(n, nb, hb, v, inv, xs, bsum);
     }
 }
 
@@ -1218,7 +1152,7 @@ struct ChunkGroup {
 
 template <int QT, int RW, int TT, bool XS, int P = 2>
 hipError_t launch_chunk_t(const LinearShape& s, const ChunkCfg& c, const void* w, const float* x, float* y,
-                          char* ws, hipStream_t stream, const ChunkGroup* grp = nullptr) {
+                          char* ws, hipStream_t stream, const ChunkGroup* grp = nullptr, bool presplit = false) {
     constexpr int lds = ChunkLds<QT, RW, TT, XS>::bytes;
     auto kern = gemm_chunk_kernel<QT, RW, TT, P, XS>;
     static bool attr = [&] {
@@ -1257,7 +1191,7 @@ hipError_t launch_chunk_t(const LinearShape& s, const ChunkCfg& c, const void* w
             a.tile2 = a.tile1 + grp->M[1] / bm;
         }
     }
-    if (XS) {
+    if (XS && !presplit) {
         hipLaunchKernelGGL((xsplit_kernel<QT>), dim3(c.npad), dim3(256), 0, stream, x, s.rows, s.K, s.nb, c.npad,
                            reinterpret_cast<_Float16*>(ws + l.xs), reinterpret_cast<float*>(ws + l.bsum),
                            reinterpret_cast<float*>(ws + l.scale));
@@ -1269,11 +1203,11 @@ hipError_t launch_chunk_t(const LinearShape& s, const ChunkCfg& c, const void* w
 
 template <int QT>
 hipError_t launch_chunk_q(const LinearShape& s, const ChunkCfg& c, const void* w, const float* x, float* y,
-                          char* ws, hipStream_t stream, const ChunkGroup* grp = nullptr) {
+                          char* ws, hipStream_t stream, const ChunkGroup* grp = nullptr, bool presplit = false) {
     if (c.tt == 1) return launch_chunk_t<QT, 1, 1, false>(s, c, w, x, y, ws, stream, grp);
     if (c.tt == 2 && !c.xs) return launch_chunk_t<QT, 2, 2, false>(s, c, w, x, y, ws, stream, grp);
-    if (c.tt == 2) return launch_chunk_t<QT, 2, 2, true>(s, c, w, x, y, ws, stream, grp);
-    return launch_chunk_t<QT, 2, 4, true>(s, c, w, x, y, ws, stream, grp);
+    if (c.tt == 2) return launch_chunk_t<QT, 2, 2, true>(s, c, w, x, y, ws, stream, grp, presplit);
+    return launch_chunk_t<QT, 2, 4, true>(s, c, w, x, y, ws, stream, grp, presplit);
 }
 
 bool use_chunk(const LinearShape& s, const float* x) {
@@ -1321,8 +1255,32 @@ hipError_t launch_gemm(const LinearShape& s, const void* w, const float* x, floa
     }
 }
 
+GemmSplitX gemm_split_x(const LinearShape& s, int n, const int* M) {
+    GemmSplitX r{};
+    if (n < 1 || n > 3 || M == nullptr) return r;
+    LinearShape st = s;
+    st.M = 0;
+    for (int g = 0; g < n; ++g) {
+        if (M[g] <= 0) return r;
+        st.M += M[g];
+    }
+    if (!chunk_supported(st)) return r;
+    const ChunkCfg c = choose_chunk(st);
+    if (!c.xs || !use_chunk(st, nullptr)) return r;
+    for (int g = 0; g + 1 < n; ++g)
+        if (M[g] % (64 * c.rw) != 0) return r;
+    const ChunkWs l = chunk_layout(st, c);
+    r.ok = true;
+    r.npad = c.npad;
+    r.xs = l.xs;
+    r.bsum = l.bsum;
+    r.scale = l.scale;
+    r.ws_bytes = l.total;
+    return r;
+}
+
 hipError_t launch_gemm_group(const LinearShape& s, int n, const void* const* w, float* const* y, const int* M,
-                             const float* x, void* ws, size_t ws_bytes, hipStream_t stream) {
+                             const float* x, void* ws, size_t ws_bytes, hipStream_t stream, bool x_split) {
     if (n < 1 || n > 3 || w == nullptr || y == nullptr || M == nullptr) return hipErrorInvalidValue;
     LinearShape st = s;
     st.M = 0;
@@ -1332,6 +1290,7 @@ hipError_t launch_gemm_group(const LinearShape& s, int n, const void* const* w, 
     }
     if (!use_chunk(st, x)) return hipErrorNotSupported;
     const ChunkCfg c = choose_chunk(st);
+    if (x_split && !c.xs) return hipErrorInvalidValue;  // gemm_split_x said no
     const int bm = 64 * c.rw;
     for (int g = 0; g + 1 < n; ++g)
         if (M[g] % bm != 0) return hipErrorNotSupported;  // a row tile may not straddle two weights
@@ -1342,9 +1301,9 @@ hipError_t launch_gemm_group(const LinearShape& s, int n, const void* const* w, 
     for (int g = 0; g < n; ++g) grp.w[g] = w[g], grp.y[g] = y[g], grp.M[g] = M[g];
     char* base = static_cast<char*>(ws);
     switch (st.qtype) {
-        case 1: return launch_chunk_q<1>(st, c, w[0], x, y[0], base, stream, &grp);
-        case 2: return launch_chunk_q<2>(st, c, w[0], x, y[0], base, stream, &grp);
-        default: return launch_chunk_q<3>(st, c, w[0], x, y[0], base, stream, &grp);
+        case 1: return launch_chunk_q<1>(st, c, w[0], x, y[0], base, stream, &grp, x_split);
+        case 2: return launch_chunk_q<2>(st, c, w[0], x, y[0], base, stream, &grp, x_split);
+        default: return launch_chunk_q<3>(st, c, w[0], x, y[0], base, stream, &grp, x_split);
     }
 }
 

@@ -115,8 +115,23 @@ const char* gemm_kernel_name(const LinearShape& s);
 // a weight other than the last whose M is not a multiple of the tile height):
 // then launch the linears one by one.  The workspace is sized for a LinearShape
 // whose M is the total.
+// x_split: the workspace already holds x split as the GEMM reads it (written
+// by the kernel that produced x, at the offsets gemm_split_x gives); `x` is
+// not read and no split launch is made.
 hipError_t launch_gemm_group(const LinearShape& s, int n, const void* const* w, float* const* y, const int* M,
-                             const float* x, void* ws, size_t ws_bytes, hipStream_t stream);
+                             const float* x, void* ws, size_t ws_bytes, hipStream_t stream, bool x_split = false);
+
+// Where a grouped (or, n = 1, single) GEMM of `rows` > 128 token rows reads
+// its split x inside the workspace (xsplit_device.h's layout: xs [npad][nb][64]
+// halves, bsum [npad][nb], scale [npad]; byte offsets), and the workspace size
+// the launch needs.  ok = false: the call would not read a split x (the
+// producer then writes plain x and the launch splits it).
+struct GemmSplitX {
+    bool ok;
+    int npad;
+    size_t xs, bsum, scale, ws_bytes;
+};
+GemmSplitX gemm_split_x(const LinearShape& s, int n, const int* M);
 
 // Persistent GEMV over a chain of linears (sequence.hip).  A stage is up to
 // kSeqMaxCalls GEMVs reading the same x; their rows are concatenated in call

@@ -247,6 +247,23 @@ def test_batched_prefill_head_dims(hip, orc, ref, tmp_path, dim, heads, kv_heads
     dec.close()
 
 
+@pytest.mark.parametrize("fmt", ["q4_0", "q8_0", "q4_1"])
+def test_batched_prefill_split_x_written_by_norm_and_swiglu(hip, orc, ref, tmp_path, fmt):
+    """Over 128 rows the RMSNorm and SwiGLU row kernels write the q/k/v,
+    gate/up and down GEMMs' split x themselves (every linear of one format, so
+    q/k/v and gate/up run as grouped GEMMs); then a short batch (plain x) reads
+    the cache the long one wrote."""
+    path = mf.write_model(orc, str(tmp_path / f"split_{fmt}.gguf"), dim=256, heads=2, kv_heads=1, hidden=768,
+                          ctx=320, fmts=(fmt,), lm=fmt, seed=21)
+    dec = hip.Decoder(path)
+    rd = ref.decoder(path)
+    toks = np.random.default_rng(22).integers(0, 300, 260).tolist()
+    worst = close(dec.prefill(toks[:200]), rd.batch(toks[:200]), f"{fmt} batch 0..199")
+    worst = max(worst, close(dec.prefill(toks[200:260], 200), rd.batch(toks[200:260], 200), f"{fmt} batch 200..259"))
+    say(f"  {fmt}: worst relative logit difference {worst:.2e}")
+    dec.close()
+
+
 def test_batched_prefill_longer_than_one_pass(hip, orc, ref, tmp_path):
     """A prompt of more rows than one batched pass holds (chunks of 512)."""
     path = mf.write_model(orc, str(tmp_path / "long.gguf"), ctx=640, vocab=300, layers=2, seed=9)
