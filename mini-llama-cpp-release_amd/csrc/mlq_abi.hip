@@ -1380,7 +1380,15 @@ private:
     CopyPool() : owner_(getpid()) {
         const unsigned hw = std::thread::hardware_concurrency();
         const unsigned n = std::min(7u, hw > 1 ? hw / 2 : 0u);
-        for (unsigned i = 0; i < n; ++i) workers_.emplace_back([this, i] { loop(i + 1); });
+        // A thread that cannot be started leaves the pool smaller (at worst
+        // empty: every copy then runs on the calling thread).
+        for (unsigned i = 0; i < n; ++i) {
+            try {
+                workers_.emplace_back([this, i] { loop(i + 1); });
+            } catch (const std::exception&) {
+                break;
+            }
+        }
     }
 
     // Slice i of the job, 4 KiB aligned.
