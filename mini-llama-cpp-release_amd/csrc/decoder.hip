@@ -323,6 +323,24 @@ __global__ __launch_bounds__(kFlashThreads) void attention_rope_kernel(
     a0 += has_b ? b0 : 0.0f;
     a1 += has_b ? b1 : 0.0f;
     ve += bv != nullptr ? bve : 0.0f;
+    const size_t layer_base = static_cast<size_t>(layer) * max_seq * n_kv * HD;
+    const size_t t_stride = static_cast<size_t>(n_kv) * HD;
+    const float* kbase = kc + layer_base + kvh * HD;
+    const float* vbase = vc + layer_base + kvh * HD;
+    const int lr = tid / LPR;
+    const int li = tid % LPR;
+    // The first pass's cache rows of the run that starts at position 0 (split
+    // 0), requested before the position word is back: they do not depend on
+    // it.  Rows at or past the position (this step's row, or rows of an older,
+    // longer generation) are selected away in the pass; a split that starts
+    // later requests its own rows once the position is known.
+    float4 kr[AHEAD], vr[AHEAD];
+#pragma unroll
+    for (int j = 0; j < AHEAD; ++j) {
+        const int tj = min(lr + j * ROWS, max_seq - 1);
+        kr[j] = *reinterpret_cast<const float4*>(kbase + tj * t_stride + 4 * li);
+        vr[j] = *reinterpret_cast<const float4*>(vbase + tj * t_stride + 4 * li);
+    }
 
     const int p0 = st->pos;
     const bool ok = p0 >= 0 && p0 < max_seq;
@@ -336,20 +354,13 @@ __global__ __launch_bounds__(kFlashThreads) void attention_rope_kernel(
     const int t_end = min(pos + 1, t_begin + chunk);  // this workgroup's positions: [t_begin, t_end)
     // Rows read from the cache stay below pos and inside the run.
     const int last = max(min(t_end, pos) - 1, 0);
-    const size_t layer_base = static_cast<size_t>(layer) * max_seq * n_kv * HD;
-    const size_t t_stride = static_cast<size_t>(n_kv) * HD;
-    const float* kbase = kc + layer_base + kvh * HD;
-    const float* vbase = vc + layer_base + kvh * HD;
-    const int lr = tid / LPR;
-    const int li = tid % LPR;
-    // The first pass's cache rows, requested ahead of the RoPE math (rows past
-    // the last cached one re-read it and are not used).
-    float4 kr[AHEAD], vr[AHEAD];
+    if (t_begin != 0) {  // a later split: its first pass, ahead of the RoPE math
 #pragma unroll
-    for (int j = 0; j < AHEAD; ++j) {
-        const int tj = min(t_begin + lr + j * ROWS, last);
-        kr[j] = *reinterpret_cast<const float4*>(kbase + tj * t_stride + 4 * li);
-        vr[j] = *reinterpret_cast<const float4*>(vbase + tj * t_stride + 4 * li);
+        for (int j = 0; j < AHEAD; ++j) {
+            const int tj = min(t_begin + lr + j * ROWS, last);
+            kr[j] = *reinterpret_cast<const float4*>(kbase + tj * t_stride + 4 * li);
+            vr[j] = *reinterpret_cast<const float4*>(vbase + tj * t_stride + 4 * li);
+        }
     }
     if (tid < HD) {
         const float freq = 1.0f / powf(theta, static_cast<float>(2 * r) / static_cast<float>(HD));
