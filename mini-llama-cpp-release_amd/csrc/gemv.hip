@@ -682,6 +682,9 @@ hipError_t launch_gemv_glu(const LinearShape& s, const GemvGroup& g, const float
     // 727 -> 737 tokens/s; one unit and two workgroups per CU had been best
     // before x was loaded ahead of the weights; three units: 717).  Q8_0 keeps
     // one unit (its 17-dword pairs would not fit two units in 128 VGPRs).
+    // Rows of 64 pairs: one of the two units requested with x, the other once
+    // x is staged (741 -> 752 tokens/s; both with x, as before: 741; three
+    // units with one ahead: 736; one unit, two workgroups per CU: 731).
     auto go = [&](auto kernel, int lpr, int wgs_per_cu) {
         const int groups = (s.M + (64 / lpr) - 1) / (64 / lpr);
         int grid = (groups + kWaves - 1) / kWaves;
@@ -694,9 +697,9 @@ hipError_t launch_gemv_glu(const LinearShape& s, const GemvGroup& g, const float
         case 116: return go(gemv_single_kernel<1, 16, kWaves, 1, kModeNormGlu>, 16, 2);
         case 164: return go(gemv_single_kernel<1, 64, kWaves, 1, kModeNormGlu>, 64, 2);
         case 216: return go(gemv_single_kernel<2, 16, kWaves, 2, kModeNormGlu>, 16, 1);
-        case 264: return go(gemv_single_kernel<2, 64, kWaves, 2, kModeNormGlu>, 64, 1);
+        case 264: return go(gemv_single_kernel<2, 64, kWaves, 2, kModeNormGlu, 1>, 64, 1);
         case 316: return go(gemv_single_kernel<3, 16, kWaves, 2, kModeNormGlu>, 16, 1);
-        case 364: return go(gemv_single_kernel<3, 64, kWaves, 2, kModeNormGlu>, 64, 1);
+        case 364: return go(gemv_single_kernel<3, 64, kWaves, 2, kModeNormGlu, 1>, 64, 1);
         default: return hipErrorInvalidValue;
     }
 }
