@@ -1334,9 +1334,13 @@ constexpr size_t kPinChunk = size_t(16) << 20;
 // mapping at ~15 GB/s).  One copy at a time; the workers sleep in between.
 class CopyPool {
 public:
+    // Never destroyed: a forked child holds copies of the parent's
+    // std::thread objects (their threads do not exist there), and destroying
+    // a joinable std::thread terminates the process.  At exit the workers are
+    // blocked on the condition variable and end with the process.
     static CopyPool& get() {
-        static CopyPool pool;
-        return pool;
+        static CopyPool* pool = new CopyPool;
+        return *pool;
     }
 
     void copy(void* dst, const void* src, size_t n) {
@@ -1357,15 +1361,6 @@ public:
         run_slice(job_, 0);
         std::unique_lock<std::mutex> l(mu_);
         done_.wait(l, [&] { return pending_ == 0; });
-    }
-
-    ~CopyPool() {
-        {
-            std::lock_guard<std::mutex> l(mu_);
-            stop_ = true;
-        }
-        wake_.notify_all();
-        for (std::thread& t : workers_) t.join();
     }
 
 private:
@@ -1402,8 +1397,7 @@ private:
         uint64_t seen = 0;
         std::unique_lock<std::mutex> l(mu_);
         for (;;) {
-            wake_.wait(l, [&] { return stop_ || generation_ != seen; });
-            if (stop_) return;
+            wake_.wait(l, [&] { return generation_ != seen; });
             seen = generation_;
             const Job j = job_;
             l.unlock();
@@ -1421,7 +1415,6 @@ private:
     Job job_{};
     unsigned pending_ = 0;
     uint64_t generation_ = 0;
-    bool stop_ = false;
 };
 
 // Copies `bytes` from host memory that is not pinned (a file mapping) into
