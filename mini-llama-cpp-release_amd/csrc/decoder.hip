@@ -886,10 +886,15 @@ __global__ __launch_bounds__(kPrefillAttnThreads) void attention_rows_kernel(con
 }
 
 // Causal attention of prefill rows on MFMA (head_dim HD = 64 or 128).
-// Workgroup (head h, 16 W query rows; the blocks with the most cache rows are
-// launched first), wave w: query rows 16 w .. 16 w + 15.
-// Key blocks of 32 cache rows are staged in LDS as fp16 hi + lo (K as rows,
-// V transposed), so every f32 product becomes hi*hi + hi*lo + lo*hi in
+// Workgroup (head h, 16 W / KS query rows; the blocks with the most cache
+// rows are launched first), wave w: query rows 16 (w % (W / KS)) .. + 15 and
+// key blocks ks, ks + KS, ... of them with ks = w / (W / KS).  With KS = 2
+// the two waves of a query tile each walk half of its key blocks (half the
+// serial chain of the longest tiles) and merge their softmax states through
+// LDS at the end: M = max(m0, m1), o = o0 e^(m0 - M) + o1 e^(m1 - M), the
+// same for the sums.
+// Key blocks of 32 cache rows are staged in LDS, KS at a time, as fp16 hi +
+// lo (K as rows, V transposed), so every f32 product becomes hi*hi + hi*lo + lo*hi in
 // v_mfma_f32_16x16x32_f16 (the dropped lo*lo term is 2^-22 of the product):
 //  * scores, transposed: S^T[key][query] = K . Q^T (A = K rows of the block,
 //    B = the wave's query rows, held in registers), then times 1/sqrt(HD);
@@ -916,7 +921,7 @@ __device__ __forceinline__ _Float16 f16_lo(float v, _Float16 hi) {
 // Slot of key k (0..31) in a transposed V tile (the P^T operand's order).
 __device__ __forceinline__ int attn_slot(int k) { return k < 16 ? 8 * (k >> 2) + (k & 3) : 8 * ((k - 16) >> 2) + 4 + (k & 3); }
 
-template <int HD, int W, int PF>
+template <int HD, int W, int PF, int KS>
 __global__ __launch_bounds__(64 * W) void attention_rows_mfma_kernel(const float* __restrict__ Q,
                                                                   const float* __restrict__ kc,
                                                                   const float* __restrict__ vc, int n_heads, int n_kv,
@@ -928,28 +933,41 @@ __global__ __launch_bounds__(64 * W) void attention_rows_mfma_kernel(const float
     constexpr int KROW = HD + 8;  // halves per K row in LDS (16-byte aligned, banks spread)
     constexpr int VROW = KB + 8;  // halves per V^T row
     constexpr int NT = 64 * W;
-    constexpr int TPK = NT / KB;        // threads per K row
+    constexpr int QW = W / KS;          // query tiles of 16 rows per workgroup
+    constexpr int KBS = KS * KB;        // keys staged per step
+    constexpr int TPK = NT / KBS;       // threads per K row
     constexpr int KPT = HD / TPK;       // K elements per thread
-    constexpr int VPT = KB * HD / NT;   // V elements per thread (one d, VPT consecutive keys)
-    static_assert(KPT % 8 == 0 && VPT % 4 == 0, "staging map");
+    constexpr int VPT = KBS * HD / NT;  // V elements per thread (one d, VPT consecutive keys of one block)
+    static_assert(W % KS == 0 && KPT % 8 == 0 && VPT % 4 == 0 && KB % VPT == 0, "staging map");
     static_assert(HD == 64 || HD == 128, "head_dim");
-    __shared__ __attribute__((aligned(16))) _Float16 khi[KB * KROW], klo[KB * KROW];
-    __shared__ __attribute__((aligned(16))) _Float16 vhi[HD * VROW], vlo[HD * VROW];
+    constexpr int KSZ = KB * KROW;  // halves of one K buffer
+    constexpr int VSZ = HD * VROW;  // halves of one V^T buffer
+    // [K hi: KS][K lo: KS][V^T hi: KS][V^T lo: KS]; after the last step the
+    // merge of the KS states reuses it.
+    __shared__ __attribute__((aligned(16))) _Float16 smem[KS * (2 * KSZ + 2 * VSZ)];
+    static_assert(KS == 1 || (KS - 1) * QW * 64 * (4 * (HD / 16) + 2) * 4 <= KS * (2 * KSZ + 2 * VSZ) * 2,
+                  "merge area");
+    _Float16* const khi = smem;
+    _Float16* const klo = smem + KS * KSZ;
+    _Float16* const vhi = smem + 2 * KS * KSZ;
+    _Float16* const vlo = smem + 2 * KS * KSZ + KS * VSZ;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int i16 = lane & 15;
     const int g = lane >> 4;
     const int wave = tid >> 6;
+    const int qw = wave % QW;
+    const int ks = wave / QW;
     const int h = blockIdx.x;
     const int kvh = h / (n_heads / n_kv);
     const size_t layer_base = static_cast<size_t>(layer) * max_seq * n_kv * HD;
     const size_t t_stride = static_cast<size_t>(n_kv) * HD;
     const float* kbase = kc + layer_base + kvh * HD;
     const float* vbase = vc + layer_base + kvh * HD;
-    const int qb0 = (gridDim.y - 1 - blockIdx.y) * 16 * W;
-    const int last_pos = start + min(qb0 + 16 * W, n) - 1;  // the workgroup's last query position
+    const int qb0 = (gridDim.y - 1 - blockIdx.y) * 16 * QW;
+    const int last_pos = start + min(qb0 + 16 * QW, n) - 1;  // the workgroup's last query position
     // This lane's query (rows past n repeat row n - 1; not stored).
-    const int qrow = min(qb0 + 16 * wave + i16, n - 1);
+    const int qrow = min(qb0 + 16 * qw + i16, n - 1);
     const int qpos = start + qrow;
     h8_t qh[DC], ql[DC];
     {
@@ -967,16 +985,21 @@ __global__ __launch_bounds__(64 * W) void attention_rows_mfma_kernel(const float
             }
         }
     }
-    // Staging maps: K thread -> key tid / TPK, elements (tid % TPK) * KPT ..;
-    // V thread -> d = tid % HD, keys (tid / HD) * VPT ...
+    // Staging maps (keys of a step: KS blocks of KB): K thread -> key
+    // tid / TPK, elements (tid % TPK) * KPT ..; V thread -> d = tid % HD,
+    // keys (tid / HD) * VPT ...
     const int k_key = tid / TPK;
     const int k_d0 = (tid % TPK) * KPT;
     const int v_d = tid % HD;
     const int v_k0 = (tid / HD) * VPT;
-    // PF key blocks in flight: block kb is staged from register set kb % PF.
+    _Float16* const kst_hi = khi + (k_key / KB) * KSZ + (k_key % KB) * KROW + k_d0;
+    _Float16* const kst_lo = klo + (k_key / KB) * KSZ + (k_key % KB) * KROW + k_d0;
+    _Float16* const vst_hi = vhi + (v_k0 / KB) * VSZ + v_d * VROW;
+    _Float16* const vst_lo = vlo + (v_k0 / KB) * VSZ + v_d * VROW;
+    // PF steps in flight: step sb is staged from register set sb % PF.
     float kreg[PF][KPT], vreg[PF][VPT];
-    auto load_block = [&](int kb, int u) {
-        const int t = min(kb * KB + k_key, last_pos);
+    auto load_block = [&](int sb, int u) {
+        const int t = min(sb * KBS + k_key, last_pos);
         const float* kp = kbase + static_cast<size_t>(t) * t_stride + k_d0;
 #pragma unroll
         for (int i = 0; i < KPT; i += 4) {
@@ -988,7 +1011,7 @@ __global__ __launch_bounds__(64 * W) void attention_rows_mfma_kernel(const float
         }
 #pragma unroll
         for (int i = 0; i < VPT; ++i) {
-            const int tv = min(kb * KB + v_k0 + i, last_pos);
+            const int tv = min(sb * KBS + v_k0 + i, last_pos);
             vreg[u][i] = vbase[static_cast<size_t>(tv) * t_stride + v_d];
         }
     };
@@ -1002,8 +1025,8 @@ __global__ __launch_bounds__(64 * W) void attention_rows_mfma_kernel(const float
                 hk[j] = hh;
                 lk[j] = f16_lo(kreg[u][i + j], hh);
             }
-            *reinterpret_cast<h8_t*>(khi + k_key * KROW + k_d0 + i) = hk;
-            *reinterpret_cast<h8_t*>(klo + k_key * KROW + k_d0 + i) = lk;
+            *reinterpret_cast<h8_t*>(kst_hi + i) = hk;
+            *reinterpret_cast<h8_t*>(kst_lo + i) = lk;
         }
         typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
 #pragma unroll
@@ -1015,9 +1038,9 @@ __global__ __launch_bounds__(64 * W) void attention_rows_mfma_kernel(const float
                 hv[j] = hh;
                 lv[j] = f16_lo(vreg[u][i + j], hh);
             }
-            const int slot = attn_slot(v_k0 + i);
-            *reinterpret_cast<h4_t*>(vhi + v_d * VROW + slot) = hv;
-            *reinterpret_cast<h4_t*>(vlo + v_d * VROW + slot) = lv;
+            const int slot = attn_slot(v_k0 % KB + i);
+            *reinterpret_cast<h4_t*>(vst_hi + slot) = hv;
+            *reinterpret_cast<h4_t*>(vst_lo + slot) = lv;
         }
     };
     const float scale = 1.0f / sqrtf(static_cast<float>(HD));
@@ -1026,23 +1049,29 @@ __global__ __launch_bounds__(64 * W) void attention_rows_mfma_kernel(const float
 #pragma unroll
     for (int t = 0; t < DT; ++t) o[t] = zero;
     float m = -INFINITY, l = 0.0f;
-    const int nkb = last_pos / KB + 1;
+    const int nkb = last_pos / KB + 1;   // key blocks
+    const int nsb = (nkb + KS - 1) / KS;  // steps (a step's blocks past nkb - 1 are all masked)
+    const _Float16* const kh_w = khi + ks * KSZ;
+    const _Float16* const kl_w = klo + ks * KSZ;
+    const _Float16* const vh_w = vhi + ks * VSZ;
+    const _Float16* const vl_w = vlo + ks * VSZ;
 #pragma unroll
     for (int u = 0; u < PF; ++u)
-        if (u < nkb) load_block(u, u);
-    auto step = [&](int kb, int u) {
-        __syncthreads();  // the previous block's readers are done
+        if (u < nsb) load_block(u, u);
+    auto step = [&](int sb, int u) {
+        __syncthreads();  // the previous step's readers are done
         store_block(u);
         __syncthreads();
-        if (kb + PF < nkb) load_block(kb + PF, u);
+        if (sb + PF < nsb) load_block(sb + PF, u);
+        const int kb = sb * KS + ks;  // this wave's key block
         // S^T for the two 16-key tiles: three product terms in separate
         // accumulators (independent MFMA chains), summed after.
         f4_t s[2];
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt) {
             f4_t a0 = zero, a1 = zero, a2 = zero;
-            const _Float16* kh = khi + (16 * kt + i16) * KROW + 8 * g;
-            const _Float16* kl = klo + (16 * kt + i16) * KROW + 8 * g;
+            const _Float16* kh = kh_w + (16 * kt + i16) * KROW + 8 * g;
+            const _Float16* kl = kl_w + (16 * kt + i16) * KROW + 8 * g;
 #pragma unroll
             for (int c = 0; c < DC; ++c) {
                 const h8_t ah = *reinterpret_cast<const h8_t*>(kh + 32 * c);
@@ -1087,21 +1116,54 @@ __global__ __launch_bounds__(64 * W) void attention_rows_mfma_kernel(const float
 #pragma unroll
         for (int t = 0; t < DT; ++t) {
             f4_t a0 = o[t] * c_old, a1 = zero, a2 = zero;
-            const h8_t vh = *reinterpret_cast<const h8_t*>(vhi + (16 * t + i16) * VROW + 8 * g);
-            const h8_t vl = *reinterpret_cast<const h8_t*>(vlo + (16 * t + i16) * VROW + 8 * g);
+            const h8_t vh = *reinterpret_cast<const h8_t*>(vh_w + (16 * t + i16) * VROW + 8 * g);
+            const h8_t vl = *reinterpret_cast<const h8_t*>(vl_w + (16 * t + i16) * VROW + 8 * g);
             a0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, ph, a0, 0, 0, 0);
             a1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, pl, a1, 0, 0, 0);
             a2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(vl, ph, a2, 0, 0, 0);
             o[t] = a0 + (a1 + a2);
         }
     };
-    for (int kb0 = 0; kb0 < nkb; kb0 += PF) {
+    for (int sb0 = 0; sb0 < nsb; sb0 += PF) {
 #pragma unroll
         for (int u = 0; u < PF; ++u)
-            if (kb0 + u < nkb) step(kb0 + u, u);
+            if (sb0 + u < nsb) step(sb0 + u, u);
+    }
+    if (KS > 1) {
+        // Waves ks >= 1 leave (m, l, O^T) in LDS; wave 0 of the tile folds
+        // them in, in ks order.  Wave 0 saw key 0, so its maximum is finite.
+        float* const mrg = reinterpret_cast<float*>(smem);
+        constexpr int PER = 4 * DT + 2;  // floats per lane
+        __syncthreads();  // every wave is done with the staged keys
+        if (ks > 0) {
+            float* dst = mrg + (((ks - 1) * QW + qw) * PER) * 64;
+#pragma unroll
+            for (int t = 0; t < DT; ++t)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) dst[(4 * t + q) * 64 + lane] = o[t][q];
+            dst[(4 * DT) * 64 + lane] = m;
+            dst[(4 * DT + 1) * 64 + lane] = l;
+        }
+        __syncthreads();
+        if (ks > 0) return;
+#pragma unroll
+        for (int j = 1; j < KS; ++j) {
+            const float* src = mrg + (((j - 1) * QW + qw) * PER) * 64;
+            const float m1 = src[(4 * DT) * 64 + lane];
+            const float l1 = src[(4 * DT + 1) * 64 + lane];
+            const float mx = fmaxf(m, m1);
+            const float c0 = expf(m - mx);
+            const float c1 = expf(m1 - mx);  // 0 when that wave saw no key of this query
+#pragma unroll
+            for (int t = 0; t < DT; ++t)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) o[t][q] = o[t][q] * c0 + src[(4 * t + q) * 64 + lane] * c1;
+            l = l * c0 + l1 * c1;
+            m = mx;
+        }
     }
     // O^T[d = 16 t + 4 g + q][this lane's query] / l.
-    if (qb0 + 16 * wave + i16 < n) {
+    if (qb0 + 16 * qw + i16 < n) {
         const float inv = 1.0f / l;
         float* op = out + static_cast<size_t>(qrow) * n_heads * HD + h * HD + 4 * g;
 #pragma unroll
@@ -1919,14 +1981,15 @@ void Decoder::enqueue_prefill(hipStream_t s, const int32_t* tokens, int n, int s
                            V_, L.bq, L.bk, L.bv, c.n_heads, c.n_kv_heads, c.head_dim, c.rope_theta, c.rope_neox,
                            c.max_seq_len, l, start, kcache_, vcache_, rot_wgs);
         check(hipGetLastError(), "rope_kv_rows_kernel");
-#define MLQ_ATTN_MFMA(HD, W)                                                                                      \
-    hipLaunchKernelGGL((attention_rows_mfma_kernel<HD, W, 2>), dim3(c.n_heads, (n + 16 * W - 1) / (16 * W)),        \
-                       dim3(64 * W), 0, s, Q_, kcache_, vcache_, c.n_heads, c.n_kv_heads, c.max_seq_len, l, start, n, ATT_)
+#define MLQ_ATTN_MFMA(HD, W, PF, KS)                                                                             \
+    hipLaunchKernelGGL((attention_rows_mfma_kernel<HD, W, PF, KS>),                                              \
+                       dim3(c.n_heads, (n + 16 * (W / KS) - 1) / (16 * (W / KS))), dim3(64 * W), 0, s, Q_, kcache_,  \
+                       vcache_, c.n_heads, c.n_kv_heads, c.max_seq_len, l, start, n, ATT_)
 #define MLQ_ATTN_ROWS(LPR, V4, QR, A)                                                                           \
     hipLaunchKernelGGL((attention_rows_kernel<LPR, V4, QR, A>), dim3(c.n_heads, (n + QR - 1) / QR),            \
                        dim3(kPrefillAttnThreads), 0, s, Q_, kcache_, vcache_, c.n_heads, c.n_kv_heads, c.max_seq_len, l, \
                        start, n, ATT_)
-        // (lanes per cache row, float4s per lane, query rows per workgroup,
+        // VALU kernel (other head sizes): (lanes per cache row, float4s per lane, query rows per workgroup,
         // passes in flight).  LLaMA-7B shape (32 heads x 128, 512 rows, MI355X):
         // prefill 27.7 ms with one float4 per lane (32 lanes per row, per-row
         // softmax update) -> 25.4-25.6 ms at (16, 2, 4, 2); (8, 4, 4, 1) 25.7,
@@ -1934,8 +1997,12 @@ void Decoder::enqueue_prefill(hipStream_t s, const int32_t* tokens, int n, int s
         switch (c.head_dim) {
             case 16: MLQ_ATTN_ROWS(4, 1, 4, 2); break;
             case 32: MLQ_ATTN_ROWS(8, 1, 4, 2); break;
-            case 64: MLQ_ATTN_MFMA(64, 4); break;
-            case 128: MLQ_ATTN_MFMA(128, 4); break;
+            // MFMA: (waves, key steps in flight, key splits).  LLaMA-7B shape,
+            // 512 rows, kernel µs per layer: (4, 2, 1) 43.0, (4, 2, 2) 41.0,
+            // (4, 1, 2) 37.8, (8, 2, 2) 32.4, (8, 1, 2) 31.3, (8, 1, 4) 37.1,
+            // (16, 1, 2) 43.5 (spills).
+            case 64: MLQ_ATTN_MFMA(64, 8, 1, 2); break;
+            case 128: MLQ_ATTN_MFMA(128, 8, 1, 2); break;
             default: MLQ_ATTN_ROWS(32, 2, 4, 2); break;
         }
 #undef MLQ_ATTN_ROWS
