@@ -633,8 +633,10 @@ __global__ __launch_bounds__(256) void swiglu_split_rows_kernel(const float* __r
 }
 
 // rope_kv_kernel for every row (position start + r): workgroups (0 .. R-1,
-// row) rotate the row's q and k heads and write k to the cache; workgroups
-// (R.., row) copy v (+ bias) to the cache.  Thread (hg, r) of rotating
+// row) rotate the row's q heads in place and write the rotated k heads to the
+// cache (k itself is left as it was: only the cache is read after this);
+// workgroups (R.., row), when launched, copy v (+ bias) to the cache (without
+// a v bias the q/k/v GEMM writes v into the cache itself).  Thread (hg, r) of rotating
 // workgroup b computes the angle of pair r once (the same expressions as
 // rope_kv_kernel, so the same values) and applies it to heads
 // b HG + hg, (b + R) HG + hg, ... of q and then k (HG = 256 / (hd / 2)): one
@@ -682,12 +684,10 @@ __global__ __launch_bounds__(256) void rope_kv_rows_kernel(float* __restrict__ Q
         }
         const float r0 = a0 * c - a1 * sn;
         const float r1 = a0 * sn + a1 * c;
-        t[o0] = r0;
-        t[o1] = r1;
-        if (!is_q) {
-            kc[cache_row + hh * hd + o0] = r0;
-            kc[cache_row + hh * hd + o1] = r1;
-        }
+        // rotated q in place (attention reads it); rotated k only into the cache
+        float* dst = is_q ? t : kc + cache_row + hh * hd;
+        dst[o0] = r0;
+        dst[o1] = r1;
     }
 }
 
@@ -1964,7 +1964,12 @@ void Decoder::enqueue_prefill(hipStream_t s, const int32_t* tokens, int n, int s
         // itself where the GEMM splits x (saves the split launch per GEMM).
         {
             const Linear* w[3] = {&L.wq, &L.wk, &L.wv};
-            float* y[3] = {Q_, K_, V_};
+            // Without a v bias, v goes straight into this pass's cache rows
+            // (rows start .. start + n - 1 are contiguous, kv_dim apart).
+            float* const vdst = L.bv == nullptr
+                                    ? vcache_ + (static_cast<size_t>(l) * c.max_seq_len + start) * kv_dim
+                                    : V_;
+            float* y[3] = {Q_, K_, vdst};
             SplitTarget t;
             if (split_target(3, w, n, t)) {
                 norm_into(s, &t, X_, l == 0 ? nullptr : FF_, L.attn_norm, n);
@@ -1977,7 +1982,8 @@ void Decoder::enqueue_prefill(hipStream_t s, const int32_t* tokens, int n, int s
         // Rotating workgroups: about four head steps each.
         const int rope_hg = 256 / (c.head_dim / 2);
         const int rot_wgs = std::max(1, (c.n_heads + c.n_kv_heads + 4 * rope_hg - 1) / (4 * rope_hg));
-        hipLaunchKernelGGL(rope_kv_rows_kernel, dim3(rot_wgs + (kv_dim + 255) / 256, n), dim3(256), 0, s, Q_, K_,
+        const int copy_wgs = L.bv == nullptr ? 0 : (kv_dim + 255) / 256;  // v (+ bias) into the cache
+        hipLaunchKernelGGL(rope_kv_rows_kernel, dim3(rot_wgs + copy_wgs, n), dim3(256), 0, s, Q_, K_,
                            V_, L.bq, L.bk, L.bv, c.n_heads, c.n_kv_heads, c.head_dim, c.rope_theta, c.rope_neox,
                            c.max_seq_len, l, start, kcache_, vcache_, rot_wgs);
         check(hipGetLastError(), "rope_kv_rows_kernel");
