@@ -555,18 +555,39 @@ __global__ __launch_bounds__(256) void add_rmsnorm_split_rows_kernel(float* __re
     const size_t off = static_cast<size_t>(valid ? row : 0) * dim;
     float v[C][16], wv[C][16];
     float ss = 0.0f;
-    // The norm weights are requested with the row (they do not depend on it).
+    // Every load is unconditional (half blocks past the row re-read the last
+    // one, D absent reads X again; both are selected away): a load under a
+    // branch makes the compiler wait for it at the join, one round trip per
+    // half block.  The norm weights are requested with the row.
+    const float* const Dp = D != nullptr ? D + off : X + off;
 #pragma unroll
     for (int c = 0; c < C; ++c) {
-        const int k0 = 16 * (static_cast<int>(threadIdx.x) + 256 * c);
-        const bool in = k0 < dim;
+        const int k0 = min(16 * (static_cast<int>(threadIdx.x) + 256 * c), dim - 16);
 #pragma unroll
         for (int i = 0; i < 16; i += 4) {
-            const float4 a = in ? *reinterpret_cast<const float4*>(w + k0 + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            const float4 a = *reinterpret_cast<const float4*>(w + k0 + i);
             wv[c][i] = a.x;
             wv[c][i + 1] = a.y;
             wv[c][i + 2] = a.z;
             wv[c][i + 3] = a.w;
+        }
+    }
+    float dv[C][16];
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+        const int k0 = min(16 * (static_cast<int>(threadIdx.x) + 256 * c), dim - 16);
+#pragma unroll
+        for (int i = 0; i < 16; i += 4) {
+            const float4 a = *reinterpret_cast<const float4*>(X + off + k0 + i);
+            const float4 d = *reinterpret_cast<const float4*>(Dp + k0 + i);
+            v[c][i] = a.x;
+            v[c][i + 1] = a.y;
+            v[c][i + 2] = a.z;
+            v[c][i + 3] = a.w;
+            dv[c][i] = d.x;
+            dv[c][i + 1] = d.y;
+            dv[c][i + 2] = d.z;
+            dv[c][i + 3] = d.w;
         }
     }
 #pragma unroll
@@ -574,18 +595,16 @@ __global__ __launch_bounds__(256) void add_rmsnorm_split_rows_kernel(float* __re
         const int k0 = 16 * (static_cast<int>(threadIdx.x) + 256 * c);
         const bool in = valid && k0 < dim;
 #pragma unroll
-        for (int i = 0; i < 16; i += 4) {
-            float4 a = in ? *reinterpret_cast<const float4*>(X + off + k0 + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            if (in && D != nullptr) {
-                const float4 d = *reinterpret_cast<const float4*>(D + off + k0 + i);
-                a = make_float4(a.x + d.x, a.y + d.y, a.z + d.z, a.w + d.w);
-                *reinterpret_cast<float4*>(X + off + k0 + i) = a;
-            }
-            v[c][i] = a.x;
-            v[c][i + 1] = a.y;
-            v[c][i + 2] = a.z;
-            v[c][i + 3] = a.w;
-            ss += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w;
+        for (int i = 0; i < 16; ++i) {
+            const float a = D != nullptr ? v[c][i] + dv[c][i] : v[c][i];
+            v[c][i] = in ? a : 0.0f;
+            ss += v[c][i] * v[c][i];
+        }
+        if (in && D != nullptr) {
+#pragma unroll
+            for (int i = 0; i < 16; i += 4)
+                *reinterpret_cast<float4*>(X + off + k0 + i) =
+                    make_float4(v[c][i], v[c][i + 1], v[c][i + 2], v[c][i + 3]);
         }
     }
     ss = wg_reduce<256, false>(ss, part);
@@ -612,21 +631,35 @@ __global__ __launch_bounds__(256) void swiglu_split_rows_kernel(const float* __r
     const int row = blockIdx.x;
     const bool valid = row < n;
     const size_t off = static_cast<size_t>(valid ? row : 0) * hidden;
-    float v[C][16];
+    float v[C][16], uv[C][16];
+    // Unconditional loads (half blocks past the row re-read the last one and
+    // are selected away), all issued before any is used.
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+        const int k0 = min(16 * (static_cast<int>(threadIdx.x) + 256 * c), hidden - 16);
+#pragma unroll
+        for (int i = 0; i < 16; i += 4) {
+            const float4 g = *reinterpret_cast<const float4*>(G + off + k0 + i);
+            const float4 u = *reinterpret_cast<const float4*>(U + off + k0 + i);
+            v[c][i] = g.x;
+            v[c][i + 1] = g.y;
+            v[c][i + 2] = g.z;
+            v[c][i + 3] = g.w;
+            uv[c][i] = u.x;
+            uv[c][i + 1] = u.y;
+            uv[c][i + 2] = u.z;
+            uv[c][i + 3] = u.w;
+        }
+    }
 #pragma unroll
     for (int c = 0; c < C; ++c) {
         const int k0 = 16 * (static_cast<int>(threadIdx.x) + 256 * c);
         const bool in = valid && k0 < hidden;
 #pragma unroll
-        for (int i = 0; i < 16; i += 4) {
-            const float4 g = in ? *reinterpret_cast<const float4*>(G + off + k0 + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            const float4 u = in ? *reinterpret_cast<const float4*>(U + off + k0 + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            const float gv[4] = {g.x, g.y, g.z, g.w}, uv[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float sig = 1.0f / (1.0f + expf(-gv[e]));
-                v[c][i + e] = in ? gv[e] * sig * uv[e] : 0.0f;
-            }
+        for (int i = 0; i < 16; ++i) {
+            const float gv = v[c][i];
+            const float sig = 1.0f / (1.0f + expf(-gv));
+            v[c][i] = in ? gv * sig * uv[c][i] : 0.0f;
         }
     }
     xsplit_emit_row<QT, C>(row, nb, v, xs, bsum, scale, red);
