@@ -28,8 +28,13 @@ namespace {
 
 constexpr int kNormThreads = 1024;
 constexpr int kAttnThreads = 256;
-constexpr int kFlashThreads = 512;
+// Decode attention: threads per head (>= head_dim) and cache rows in flight
+// per lane group.  LLaMA-7B shape on MI355X, decode at positions 4..131:
+// 256 threads 760.5-761.1 tokens/s, 512 threads 754.6-755.5 (4 rows ahead
+// both); 256 x 8 rows 757, 1024 x 2 rows 716.
+constexpr int kFlashThreads = 256;
 constexpr int kFlashAhead = 4;
+static_assert(kFlashThreads >= 256, "the RoPE step gives one thread per element of a head of up to 256");
 constexpr int kMaxHeadDim = 256;
 // Decode attention splits a head's positions over up to kAttnMaxSplits
 // workgroups once there are more than kAttnSplitRows of them.
@@ -260,7 +265,7 @@ __device__ __forceinline__ float lane_group_sum(float v) {
 // to 256).  Each workgroup rotates its q head and its kv head's k (as
 // rope_kv_kernel does), uses this position's k and v from LDS and writes them
 // to the cache; earlier positions come from the cache.  A cache row is read
-// as LPR float4s by LPR lanes, ROWS = 512 / LPR rows at a time, so every load
+// as LPR float4s by LPR lanes, ROWS = kFlashThreads / LPR rows at a time, so every load
 // is a coalesced row segment.  The softmax is folded into the same pass
 // (running maximum, sum and weighted v per row group, rescaled when the
 // maximum grows), and the row groups are merged once at the end:
