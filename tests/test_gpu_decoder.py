@@ -232,9 +232,9 @@ def test_batched_prefill_matches_reference(hip, orc, ref, tmp_path, name):
 
 @pytest.mark.parametrize("dim,heads,kv_heads", [(256, 4, 2), (256, 1, 1)], ids=["head_dim_64", "head_dim_256"])
 def test_batched_prefill_head_dims(hip, orc, ref, tmp_path, dim, heads, kv_heads):
-    """The prefill attention's other lane layouts (head_dim 64: 8 lanes of two
-    float4s per cache row; 256: 32 lanes of two), over many passes of cache
-    rows and a second batch at a later start."""
+    """The prefill attention at other head sizes (64: the MFMA kernel; 256:
+    the VALU kernel, 32 lanes of two float4s per cache row), over many passes
+    of cache rows and a second batch at a later start; then decode steps."""
     path = mf.write_model(orc, str(tmp_path / "hd.gguf"), dim=dim, heads=heads, kv_heads=kv_heads, hidden=352,
                           ctx=256, fmts=("q4_0",), lm="q4_0", seed=12)
     dec = hip.Decoder(path)
@@ -243,6 +243,10 @@ def test_batched_prefill_head_dims(hip, orc, ref, tmp_path, dim, heads, kv_heads
     worst = close(dec.prefill(toks[:150]), rd.batch(toks[:150]), f"head_dim {dim // heads} batch 0..149")
     worst = max(worst, close(dec.prefill(toks[150:230], 150), rd.batch(toks[150:230], 150),
                              f"head_dim {dim // heads} batch 150..229"))
+    # decode steps after the batches: the single-token attention at this head
+    # size, past 128 positions (its positions split over two workgroups)
+    for pos, t in ((230, 5), (231, 7)):
+        worst = max(worst, close(dec.forward(t, pos), rd.forward(t, pos), f"head_dim {dim // heads} step {pos}"))
     say(f"  head_dim {dim // heads}: worst relative logit difference {worst:.2e}")
     dec.close()
 
