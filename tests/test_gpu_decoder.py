@@ -15,8 +15,9 @@ oracle/_ref, on seeded model files written by tests/model_files.py.
 * the loader's and the forward's error messages.
 Variants cover llama (normal RoPE) and qwen2 (NeoX RoPE, q/k/v biases, tied
 lm_head -> F32 GEMV), every linear format including F32, a quantized
-embedding, multi-head / grouped / multi-query attention, head_dim 16 and 128,
-and hidden widths of an odd number of blocks.
+embedding, multi-head / grouped / multi-query attention, head_dim 16 and 128
+(and 64 / 256 after a batched prefill), and hidden widths of an odd number of
+blocks.
 """
 
 import os
@@ -86,8 +87,8 @@ def test_logits_match_reference(hip, orc, ref, tmp_path, name):
 
 @pytest.mark.parametrize("name,n_tok", [("head_dim_128", 160), ("mha_q4_0", 560), ("head_dim_128", 1000)])
 def test_long_context_logits_match_reference(hip, orc, ref, tmp_path, name, n_tok):
-    """Contexts of several attention passes: one pass covers 64 cache rows at
-    head_dim 128 and 256 rows at head_dim 32 (512 threads, 4 rows each), so
+    """Contexts of several attention passes: one pass covers 32 cache rows at
+    head_dim 128 and 128 rows at head_dim 32 (256 threads, 4 rows each), so
     these runs take the multi-pass path with its one-pass-ahead requests; past
     128 positions the positions are split over up to 8 workgroups per head
     (2, 5 and 8 splits for caches of 168, 568 and 1008 positions)."""
