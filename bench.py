@@ -53,6 +53,9 @@ sys.path.insert(0, REPO)
 
 import mlq_hip as hip  # noqa: E402
 
+sys.path.insert(0, os.path.join(REPO, "tests"))
+from sweep_workload import LAYER, Sweep, gemv_bytes, make_weight  # noqa: E402,F401
+
 METRIC = "quant matvec HBM GB/s (% of 8 TB/s peak) + µs per 7B-shape decode linear sweep"
 HBM_PEAK_GBS = 8000.0
 FP16_PEAK_TFLOPS = 2500.0
@@ -88,20 +91,6 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def gemv_bytes(qt, m, k):
-    return m * ((k + 31) // 32) * BB[qt] + 4 * k + 4 * m
-
-
-def make_weight(qt, m, k, seed, tmp):
-    """Generate W ~ N(0, 0.02) on the device and quantize it in place (device
-    quantizer, bit-identical to the reference quantizers)."""
-    nbytes = m * ((k + 31) // 32) * BB[qt]
-    blocks = hip.DeviceBuffer(nbytes)
-    hip.fill_normal(tmp, m * k, seed, 0.0, 0.02)
-    hip.quantize_device(qt, tmp, m, k, blocks)
-    return hip.Weight.wrap(qt, blocks, m * ((k + 31) // 32), m, k)
-
-
 def time_region(fn, steps, stream):
     start, stop = hip.Event(), hip.Event()
     hip.synchronize(stream)
@@ -111,55 +100,6 @@ def time_region(fn, steps, stream):
     stop.record(stream)
     hip.synchronize(stream)
     return start.elapsed_ms(stop)
-
-
-# ------------------------------------------------------------------ sweep
-LAYER = [("q", 4096, 4096, "x"), ("k", 4096, 4096, "x"), ("v", 4096, 4096, "x"),
-         ("o", 4096, 4096, "x"), ("gate", 11008, 4096, "x"), ("up", 11008, 4096, "x"),
-         ("down", 4096, 11008, "h")]
-
-
-class Sweep:
-    def __init__(self, layers=32, qt=hip.Q4_0, seed=7):
-        self.qt = qt
-        tmp = hip.DeviceBuffer(4 * 32000 * 4096)  # f32 scratch for the largest weight (lm_head)
-        self.weights, self.calls_desc, self.ys, self.xs = [], [], [], []
-        for l in range(layers):
-            x = hip.DeviceBuffer(4 * 4096)
-            h = hip.DeviceBuffer(4 * 11008)
-            hip.fill_normal(x, 4096, seed * 1000003 + 2 * l, 0.0, 1.0)
-            hip.fill_normal(h, 11008, seed * 1000003 + 2 * l + 1, 0.0, 1.0)
-            self.xs.append((x, h))
-            for j, (name, m, k, src) in enumerate(LAYER):
-                w = make_weight(qt, m, k, seed * 7919 + 16 * l + j, tmp)
-                y = hip.DeviceBuffer(4 * m)
-                self.weights.append(w)
-                self.ys.append(y)
-                self.calls_desc.append((f"layers.{l}.{name}", w, x if src == "x" else h, y))
-        xf = hip.DeviceBuffer(4 * 4096)
-        hip.fill_normal(xf, 4096, seed * 1000003 + 999_999, 0.0, 1.0)
-        self.x_final = xf
-        lm = make_weight(qt, 32000, 4096, seed * 7919 + 999_999, tmp)
-        ylm = hip.DeviceBuffer(4 * 32000)
-        self.weights.append(lm)
-        self.ys.append(ylm)
-        self.calls_desc.append(("lm_head", lm, xf, ylm))
-        hip.synchronize(hip.stream(0))
-        tmp.free()
-        self.calls = hip.make_calls([(w, x, y, 1) for (_, w, x, y) in self.calls_desc])
-        self.bytes = sum(gemv_bytes(qt, w.m, w.k) for (_, w, _, _) in self.calls_desc)
-
-    def n(self):
-        return len(self.calls_desc)
-
-    def stage_ids(self):
-        """Decode data flow per layer: q,k,v share x | o | gate,up share x | down;
-        lm_head last.  Every change of id is a dependency barrier."""
-        ids = []
-        for l in range(len(self.calls_desc) // len(LAYER)):
-            ids += [4 * l, 4 * l, 4 * l, 4 * l + 1, 4 * l + 2, 4 * l + 2, 4 * l + 3]
-        ids.append(ids[-1] + 1 if ids else 0)
-        return ids
 
 
 def cpu_model():
@@ -1060,7 +1000,10 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "i8 dot4 -> i32, f32 accumulate",
+        "dtype_detail": ("x as a block-scaled integer per 32 elements (Q4_0/Q4_1: 16-bit, two int8 limbs; "
+                         "Q8_0: 23-bit, three limbs), weights as stored (u4 nibbles / i8), exact int32 "
+                         "block sums from v_dot4, then f32 scaling and f32 row accumulation"),
         "data": "synthetic (device-generated N(0,0.02) weights quantized by the reference's Q4_0 rule, x~N(0,1))",
         "config": {"workload": "llama7b_q4_0_decode_linear_sweep", "layers": args.layers,
                    "calls_per_step": sw.n(), "stages_per_step": seq_info["stages"],

@@ -72,6 +72,21 @@ int mlq_hip_device_count(int* count);
  * cuda_device_summary, src/backend.cpp:43-49). */
 int mlq_hip_device_info(int device, char* buf, size_t len);
 
+/* Properties of `device` (cuda_get_device_info, include/mini_llama/cuda_runtime.h:8-16,
+ * src/cuda_runtime.cpp:63-93): name, gfx architecture, major.minor of the
+ * architecture (9.5 for gfx950), memory, CU count, driver and runtime versions. */
+typedef struct mlq_device_props {
+    char name[256];
+    char arch[64];
+    int major;
+    int minor;
+    size_t total_memory_bytes;
+    int compute_units;
+    int driver_version;
+    int runtime_version;
+} mlq_device_props;
+int mlq_hip_device_props(int device, mlq_device_props* out);
+
 /* Select `device` for the calling thread and create its stream (the
  * cudaSetDevice every CudaDeviceBuffer op does, src/cuda_runtime.cpp:187-218). */
 int mlq_hip_init(int device);
@@ -116,7 +131,10 @@ int mlq_hip_quant_linear(mlq_weight_t w, const float* x, int rows, float* y, int
  * needs more scratch is refused with MLQ_ERR_LIMIT (2048 token rows of a
  * 4096x4096 weight fit, 4096 do not).  All calls on one GPU share the scratch: calls that
  * overlap in time on one GPU (different streams, or a graph replayed while
- * another runs) race and give wrong results.  Results equal
+ * another runs) race and give wrong results, and such a race can leave a
+ * split-K arrival counter of the scratch off zero, after which every later
+ * batched call of this entry on that GPU is wrong too, until the process
+ * ends.  Serialise the calls of one GPU (one stream, or events).  Results equal
  * mlq_hip_quant_linear bit for bit.  No counterpart in the reference; for
  * callers that cannot allocate. */
 int mlq_hip_quant_linear_noalloc(mlq_weight_t w, const float* x, int rows, float* y, void* stream);
@@ -269,6 +287,43 @@ int mlq_hip_graph_capture_sequence(mlq_sequence_t seq, void* stream, mlq_graph_t
  * (splitmix64 + Box-Muller) -- synthetic weights and inputs for benchmarks. */
 int mlq_hip_fill_normal(float* device_dst, size_t n, uint64_t seed, float mean, float stddev,
                         void* stream);
+
+/* ---- Device forward ops around the linears ----
+ * The op-by-op device interfaces of the reference's forward
+ * (include/mini_llama/cuda_ops.h:9-75, cuda_attention.h:11-31,
+ * cuda_matmul.h:8-38; kernels src/cuda_ops.cu:30-170, src/cuda_attention.cu,
+ * cuBLAS in src/cuda_matmul.cpp) on device pointers of `device`,
+ * asynchronous on `stream` (NULL: the library's stream for the device).  The
+ * arithmetic is the reference's CPU ops' in f32 (src/ops.cpp:19-79, 109-176,
+ * src/forward.cpp:580-600).  Every pointer must lie inside a device allocation
+ * of at least the size the shape implies (else MLQ_ERR_LIMIT /
+ * MLQ_ERR_DEVICE, and nothing is launched). */
+/* y = x / sqrt(mean(x^2) + eps) * weight over n elements (cuda_rmsnorm*). */
+int mlq_hip_rmsnorm(int device, const float* x, const float* weight, int n, float eps, float* y, void* stream);
+/* y = x / (1 + exp(-x)) (cuda_silu*); y = a * b (cuda_elementwise_mul*);
+ * y = a + b (cuda_elementwise_add*). */
+int mlq_hip_silu(int device, const float* x, size_t n, float* y, void* stream);
+int mlq_hip_mul(int device, const float* a, const float* b, size_t n, float* y, void* stream);
+int mlq_hip_add(int device, const float* a, const float* b, size_t n, float* y, void* stream);
+/* Softmax of one vector of n elements (cuda_softmax). */
+int mlq_hip_softmax(int device, const float* x, int n, float* y, void* stream);
+/* y[dim] = row `token` of the [vocab][dim] table (cuda_embedding_lookup_device_weight). */
+int mlq_hip_embedding(int device, const float* table, int vocab, int dim, int token, float* y, void* stream);
+/* RoPE in place on x [n_heads][head_dim] at position pos (cuda_rope*): pairs
+ * (2i, 2i+1) or, with neox != 0, (i, i + head_dim/2) (RopeType::NeoX). */
+int mlq_hip_rope(int device, float* x, int n_heads, int head_dim, int pos, float theta, int neox, void* stream);
+/* Single-token attention (cuda_attention_decode*): out [n_heads][head_dim] from
+ * q [n_heads][head_dim] over positions 0..pos of `layer` of a KV cache laid out
+ * [n_layers][max_seq_len][n_kv_heads][head_dim] (CudaKVCache); scores scaled
+ * by 1/sqrt(head_dim); query head h reads kv head h / (n_heads / n_kv_heads).
+ * head_dim up to 512. */
+int mlq_hip_attention_decode(int device, const float* q, const float* keys, const float* values, int n_layers,
+                             int layer, int max_seq_len, int n_heads, int n_kv_heads, int head_dim, int pos,
+                             float* out, void* stream);
+/* C[m][n] = A[m][k] * B in f32 with B [k][n], or, with b_transposed != 0, B
+ * stored as [n][k] (a linear's W: C = x W^T) (cuda_matmul, cuda_linear*). */
+int mlq_hip_matmul_f32(int device, const float* a, const float* b, int m, int k, int n, int b_transposed, float* c,
+                       void* stream);
 
 /* Kernel selection introspection: name of the kernel the next call with this
  * shape would launch (for profiles and tests). */

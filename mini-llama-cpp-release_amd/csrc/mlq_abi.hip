@@ -17,6 +17,7 @@
 #include <algorithm>
 #include <condition_variable>
 #include <cstdio>
+#include <cmath>
 #include <cstring>
 #include <memory>
 #include <mutex>
@@ -411,6 +412,24 @@ int mlq_hip_device_info(int device, char* buf, size_t len) {
                       static_cast<double>(p.totalGlobalMem) / (1024.0 * 1024.0 * 1024.0),
                       static_cast<size_t>(p.maxSharedMemoryPerMultiProcessor) / 1024);
     }
+    return MLQ_OK;
+}
+
+int mlq_hip_device_props(int device, mlq_device_props* out) {
+    if (out == nullptr) return fail(MLQ_ERR_INVALID, "mlq_hip_device_props: null output");
+    int rc = ensure_device(device);
+    if (rc != MLQ_OK) return rc;
+    hipDeviceProp_t p;
+    MLQ_HIP_CHECK(hipGetDeviceProperties(&p, device));
+    std::memset(out, 0, sizeof *out);
+    std::snprintf(out->name, sizeof out->name, "%s", p.name[0] != 0 ? p.name : p.gcnArchName);
+    std::snprintf(out->arch, sizeof out->arch, "%s", p.gcnArchName);
+    out->major = p.major;
+    out->minor = p.minor;
+    out->total_memory_bytes = p.totalGlobalMem;
+    out->compute_units = p.multiProcessorCount;
+    MLQ_HIP_CHECK(hipDriverGetVersion(&out->driver_version));
+    MLQ_HIP_CHECK(hipRuntimeGetVersion(&out->runtime_version));
     return MLQ_OK;
 }
 
@@ -1031,6 +1050,135 @@ int mlq_hip_fill_normal(float* device_dst, size_t n, uint64_t seed, float mean, 
     hipError_t e = mlq::launch_fill_normal(device_dst, n, seed, mean, stddev, resolve_stream(dev, stream));
     if (e != hipSuccess) return hip_fail(e, "fill_normal_kernel");
     return MLQ_OK;
+}
+
+// ---- device forward ops (include/mini_llama/cuda_ops.h, cuda_attention.h,
+// cuda_matmul.h).  Every pointer is checked to lie inside a device allocation
+// on `device` of at least the size the shape implies before the launch.
+
+int mlq_hip_rmsnorm(int device, const float* x, const float* weight, int n, float eps, float* y, void* stream) {
+    const char* caller = "mlq_hip_rmsnorm";
+    if (n <= 0) return fail(MLQ_ERR_SHAPE, std::string(caller) + ": empty tensor");
+    if (!std::isfinite(eps) || eps <= 0.0f) return fail(MLQ_ERR_INVALID, std::string(caller) + ": eps must be finite and positive");
+    int rc = ensure_device(device);
+    const size_t b = static_cast<size_t>(n) * sizeof(float);
+    if (rc == MLQ_OK) rc = check_device_ptr(x, device, caller, "input", b);
+    if (rc == MLQ_OK) rc = check_device_ptr(weight, device, caller, "weight", b);
+    if (rc == MLQ_OK) rc = check_device_ptr(y, device, caller, "output", b);
+    if (rc != MLQ_OK) return rc;
+    hipError_t e = mlq::launch_op_rmsnorm(x, weight, n, eps, y, resolve_stream(device, stream));
+    return e == hipSuccess ? MLQ_OK : hip_fail(e, "op_rmsnorm_kernel");
+}
+
+static int elementwise_entry(int op, const char* caller, int device, const float* a, const float* b, size_t n, float* y,
+                void* stream) {
+    if (n == 0) return MLQ_OK;
+    int rc = ensure_device(device);
+    const size_t bytes = n * sizeof(float);
+    if (rc == MLQ_OK) rc = check_device_ptr(a, device, caller, "input", bytes);
+    if (rc == MLQ_OK && op != mlq::kOpSilu) rc = check_device_ptr(b, device, caller, "second input", bytes);
+    if (rc == MLQ_OK) rc = check_device_ptr(y, device, caller, "output", bytes);
+    if (rc != MLQ_OK) return rc;
+    hipError_t e = mlq::launch_op_elementwise(op, a, b, n, y, resolve_stream(device, stream));
+    return e == hipSuccess ? MLQ_OK : hip_fail(e, "op_elementwise_kernel");
+}
+
+int mlq_hip_silu(int device, const float* x, size_t n, float* y, void* stream) {
+    return elementwise_entry(mlq::kOpSilu, "mlq_hip_silu", device, x, nullptr, n, y, stream);
+}
+
+int mlq_hip_mul(int device, const float* a, const float* b, size_t n, float* y, void* stream) {
+    return elementwise_entry(mlq::kOpMul, "mlq_hip_mul", device, a, b, n, y, stream);
+}
+
+int mlq_hip_add(int device, const float* a, const float* b, size_t n, float* y, void* stream) {
+    return elementwise_entry(mlq::kOpAdd, "mlq_hip_add", device, a, b, n, y, stream);
+}
+
+int mlq_hip_softmax(int device, const float* x, int n, float* y, void* stream) {
+    const char* caller = "mlq_hip_softmax";
+    if (n <= 0) return fail(MLQ_ERR_SHAPE, std::string(caller) + ": empty tensor");
+    int rc = ensure_device(device);
+    const size_t b = static_cast<size_t>(n) * sizeof(float);
+    if (rc == MLQ_OK) rc = check_device_ptr(x, device, caller, "input", b);
+    if (rc == MLQ_OK) rc = check_device_ptr(y, device, caller, "output", b);
+    if (rc != MLQ_OK) return rc;
+    hipError_t e = mlq::launch_op_softmax(x, n, y, resolve_stream(device, stream));
+    return e == hipSuccess ? MLQ_OK : hip_fail(e, "op_softmax_kernel");
+}
+
+int mlq_hip_embedding(int device, const float* table, int vocab, int dim, int token, float* y, void* stream) {
+    const char* caller = "mlq_hip_embedding";
+    if (vocab <= 0 || dim <= 0) return fail(MLQ_ERR_SHAPE, std::string(caller) + ": embedding shape must be positive");
+    if (token < 0 || token >= vocab) return fail(MLQ_ERR_LIMIT, std::string(caller) + ": token id out of range");
+    int rc = ensure_device(device);
+    if (rc == MLQ_OK) {
+        rc = check_device_ptr(table, device, caller, "embedding", static_cast<size_t>(vocab) * dim * sizeof(float));
+    }
+    if (rc == MLQ_OK) rc = check_device_ptr(y, device, caller, "output", static_cast<size_t>(dim) * sizeof(float));
+    if (rc != MLQ_OK) return rc;
+    hipError_t e = mlq::launch_op_embedding(table, dim, token, y, resolve_stream(device, stream));
+    return e == hipSuccess ? MLQ_OK : hip_fail(e, "op_embedding_kernel");
+}
+
+int mlq_hip_rope(int device, float* x, int n_heads, int head_dim, int pos, float theta, int neox, void* stream) {
+    const char* caller = "mlq_hip_rope";
+    if (n_heads <= 0 || head_dim <= 0 || head_dim % 2 != 0) {
+        return fail(MLQ_ERR_SHAPE, std::string(caller) + ": invalid head shape");
+    }
+    if (pos < 0) return fail(MLQ_ERR_LIMIT, std::string(caller) + ": position must be non-negative");
+    if (!std::isfinite(theta) || theta <= 0.0f) {
+        return fail(MLQ_ERR_INVALID, std::string(caller) + ": theta must be finite and positive");
+    }
+    int rc = ensure_device(device);
+    if (rc == MLQ_OK) {
+        rc = check_device_ptr(x, device, caller, "input", static_cast<size_t>(n_heads) * head_dim * sizeof(float));
+    }
+    if (rc != MLQ_OK) return rc;
+    hipError_t e = mlq::launch_op_rope(x, n_heads, head_dim, pos, theta, neox != 0, resolve_stream(device, stream));
+    return e == hipSuccess ? MLQ_OK : hip_fail(e, "op_rope_kernel");
+}
+
+int mlq_hip_attention_decode(int device, const float* q, const float* keys, const float* values, int n_layers,
+                             int layer, int max_seq_len, int n_heads, int n_kv_heads, int head_dim, int pos,
+                             float* out, void* stream) {
+    const char* caller = "mlq_hip_attention_decode";
+    if (n_heads <= 0 || n_kv_heads <= 0 || head_dim <= 0 || n_layers <= 0 || max_seq_len <= 0) {
+        return fail(MLQ_ERR_SHAPE, std::string(caller) + ": head counts, head_dim and cache extents must be positive");
+    }
+    if (n_heads % n_kv_heads != 0) {
+        return fail(MLQ_ERR_SHAPE, std::string(caller) + ": n_heads must be divisible by n_kv_heads");
+    }
+    if (head_dim > mlq::kOpAttnMaxHeadDim) {
+        return fail(MLQ_ERR_LIMIT, std::string(caller) + ": head_dim above " +
+                                       std::to_string(mlq::kOpAttnMaxHeadDim) + " is not supported");
+    }
+    if (layer < 0 || layer >= n_layers) return fail(MLQ_ERR_LIMIT, std::string(caller) + ": layer out of range");
+    if (pos < 0 || pos >= max_seq_len) return fail(MLQ_ERR_LIMIT, std::string(caller) + ": position out of range");
+    int rc = ensure_device(device);
+    const size_t cache = static_cast<size_t>(n_layers) * max_seq_len * n_kv_heads * head_dim * sizeof(float);
+    const size_t qb = static_cast<size_t>(n_heads) * head_dim * sizeof(float);
+    if (rc == MLQ_OK) rc = check_device_ptr(q, device, caller, "query", qb);
+    if (rc == MLQ_OK) rc = check_device_ptr(keys, device, caller, "key cache", cache);
+    if (rc == MLQ_OK) rc = check_device_ptr(values, device, caller, "value cache", cache);
+    if (rc == MLQ_OK) rc = check_device_ptr(out, device, caller, "output", qb);
+    if (rc != MLQ_OK) return rc;
+    hipError_t e = mlq::launch_op_attention_decode(q, keys, values, layer, max_seq_len, n_heads, n_kv_heads, head_dim,
+                                                   pos, out, resolve_stream(device, stream));
+    return e == hipSuccess ? MLQ_OK : hip_fail(e, "op_attention_decode_kernel");
+}
+
+int mlq_hip_matmul_f32(int device, const float* a, const float* b, int m, int k, int n, int b_transposed, float* c,
+                       void* stream) {
+    const char* caller = "mlq_hip_matmul_f32";
+    if (m <= 0 || k <= 0 || n <= 0) return fail(MLQ_ERR_SHAPE, std::string(caller) + ": empty tensors are not supported");
+    int rc = ensure_device(device);
+    if (rc == MLQ_OK) rc = check_device_ptr(a, device, caller, "A", static_cast<size_t>(m) * k * sizeof(float));
+    if (rc == MLQ_OK) rc = check_device_ptr(b, device, caller, "B", static_cast<size_t>(k) * n * sizeof(float));
+    if (rc == MLQ_OK) rc = check_device_ptr(c, device, caller, "C", static_cast<size_t>(m) * n * sizeof(float));
+    if (rc != MLQ_OK) return rc;
+    hipError_t e = mlq::launch_op_matmul_f32(a, b, m, k, n, b_transposed != 0, c, resolve_stream(device, stream));
+    return e == hipSuccess ? MLQ_OK : hip_fail(e, "op_matmul_f32_kernel");
 }
 
 int mlq_hip_kernel_name(int qtype, int rows, int out_features, int in_features, char* buf,

@@ -181,6 +181,23 @@ hipError_t launch_sequence(int qtype, int lpr, const SeqStageDesc* stages, int n
                            int grid, int lds_bytes, unsigned spin_limit, hipStream_t stream);
 const char* sequence_kernel_name(int qtype, int lpr);
 
+// Device forward ops (ops.hip) behind the op-by-op device interfaces of the
+// reference (include/mini_llama/cuda_ops.h, cuda_attention.h, cuda_matmul.h).
+constexpr int kOpSilu = 0;
+constexpr int kOpMul = 1;
+constexpr int kOpAdd = 2;
+constexpr int kOpAttnMaxHeadDim = 512;
+hipError_t launch_op_rmsnorm(const float* x, const float* w, int n, float eps, float* y, hipStream_t s);
+hipError_t launch_op_elementwise(int op, const float* a, const float* b, size_t n, float* y, hipStream_t s);
+hipError_t launch_op_softmax(const float* x, int n, float* y, hipStream_t s);
+hipError_t launch_op_embedding(const float* table, int dim, int token, float* y, hipStream_t s);
+hipError_t launch_op_rope(float* x, int n_heads, int head_dim, int pos, float theta, bool neox, hipStream_t s);
+hipError_t launch_op_attention_decode(const float* q, const float* keys, const float* values, int layer,
+                                      int max_seq, int n_heads, int n_kv_heads, int head_dim, int pos,
+                                      float* out, hipStream_t s);
+hipError_t launch_op_matmul_f32(const float* a, const float* b, int m, int k, int n, bool b_transposed, float* c,
+                                hipStream_t s);
+
 // Device quantizer and synthetic-data generator.
 hipError_t launch_quantize(int qtype, const float* src, int rows, int row_len, void* dst,
                            hipStream_t stream);

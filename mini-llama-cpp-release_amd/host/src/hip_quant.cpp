@@ -1,9 +1,10 @@
 // HIP quantized linear, host-side C++ layer over the C ABI (see mlq/hip_quant.h).
 //
-// The shape validation restates src/cuda_quant.cu:150-243 (same order, same
-// messages with "hip" for "cuda"); the bias is added on the host after the
-// download as in src/cuda_quant.cu:139-148, 283-285.
+// The shape validation and the host bias add are mlq/linear_checks.h, shared
+// with the drop-in of the reference's device interface (dropin/hip_quant.cpp):
+// src/cuda_quant.cu:150-243 and 139-148, 283-285, with "hip" callers.
 #include "mlq/hip_quant.h"
+#include "mlq/linear_checks.h"
 
 #include "mlq_hip.h"
 
@@ -30,41 +31,13 @@ const char* caller_of(QuantType t) {
     throw std::runtime_error(std::string(caller) + ": " + msg);
 }
 
-int in_features_of(const std::vector<int>& xs, const std::string& xstr, const char* caller) {
-    if (xs.size() == 1) return xs[0];
-    if (xs.size() == 2) return xs[1];
-    throw std::runtime_error(std::string(caller) +
-                             ": expected x shape [in_features] or [batch, in_features], got " + xstr);
-}
-
 void validate_shape(const std::vector<int>& xs, const std::string& xstr, const std::vector<int>& ws,
                     size_t block_count, const char* caller) {
-    if (ws.size() != 2) {
-        throw std::runtime_error(std::string(caller) + ": expected W shape [out_features, in_features]");
-    }
-    const int in = in_features_of(xs, xstr, caller);
-    if (in <= 0 || ws[0] <= 0 || ws[1] <= 0) {
-        throw std::runtime_error(std::string(caller) + ": empty tensors are not supported");
-    }
-    if (ws[1] != in) {
-        throw std::runtime_error(std::string(caller) + ": dimension mismatch x=" + xstr + " W=[" +
-                                 std::to_string(ws[0]) + ", " + std::to_string(ws[1]) + "]");
-    }
-    const int nb = (in + kBlockElems - 1) / kBlockElems;
-    const size_t expected = static_cast<size_t>(ws[0]) * nb;
-    if (block_count != expected) {
-        throw std::runtime_error(std::string(caller) + ": block count mismatch: expected " +
-                                 std::to_string(expected) + ", got " + std::to_string(block_count));
-    }
+    checks::linear_shape(xs, xstr, ws, block_count, caller);
 }
 
 void add_bias(Tensor& y, const Tensor& bias, int rows, int cols, const char* caller) {
-    if (bias.ndim() != 1 || bias.shape[0] != cols) {
-        throw std::runtime_error(std::string(caller) + ": expected bias shape [out_features]");
-    }
-    for (int r = 0; r < rows; ++r) {
-        for (int c = 0; c < cols; ++c) y.data[static_cast<size_t>(r) * cols + c] += bias.data[c];
-    }
+    checks::add_bias(y.data.data(), bias.shape, bias.data.data(), rows, cols, caller);
 }
 
 Tensor device_weight_linear(QuantType t, const Tensor& x, const void* w, size_t count,

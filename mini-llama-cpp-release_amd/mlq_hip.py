@@ -45,6 +45,12 @@ class DecoderConfig(ctypes.Structure):
                [("rope_theta", ctypes.c_float), ("rms_norm_eps", ctypes.c_float), ("rope_neox", ctypes.c_int)]
 
 
+class DeviceProps(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char * 256), ("arch", ctypes.c_char * 64), ("major", ctypes.c_int),
+                ("minor", ctypes.c_int), ("total_memory_bytes", ctypes.c_size_t), ("compute_units", ctypes.c_int),
+                ("driver_version", ctypes.c_int), ("runtime_version", ctypes.c_int)]
+
+
 _LIB = None
 
 _SIGS = {
@@ -52,6 +58,7 @@ _SIGS = {
     "mlq_hip_built": (ctypes.c_int, []),
     "mlq_hip_device_count": (ctypes.c_int, [ctypes.POINTER(ctypes.c_int)]),
     "mlq_hip_device_info": (ctypes.c_int, [ctypes.c_int, ctypes.c_char_p, ctypes.c_size_t]),
+    "mlq_hip_device_props": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(DeviceProps)]),
     "mlq_hip_init": (ctypes.c_int, [ctypes.c_int]),
     "mlq_hip_upload_weight": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, _vp, ctypes.c_size_t,
                                               ctypes.c_int, ctypes.c_int, ctypes.POINTER(_vp)]),
@@ -122,6 +129,17 @@ _SIGS = {
     "mlq_hip_graph_capture_sequence": (ctypes.c_int, [_vp, _vp, ctypes.POINTER(_vp)]),
     "mlq_hip_fill_normal": (ctypes.c_int, [_vp, ctypes.c_size_t, ctypes.c_uint64, ctypes.c_float,
                                             ctypes.c_float, _vp]),
+    "mlq_hip_rmsnorm": (ctypes.c_int, [ctypes.c_int, _vp, _vp, ctypes.c_int, ctypes.c_float, _vp, _vp]),
+    "mlq_hip_silu": (ctypes.c_int, [ctypes.c_int, _vp, ctypes.c_size_t, _vp, _vp]),
+    "mlq_hip_mul": (ctypes.c_int, [ctypes.c_int, _vp, _vp, ctypes.c_size_t, _vp, _vp]),
+    "mlq_hip_add": (ctypes.c_int, [ctypes.c_int, _vp, _vp, ctypes.c_size_t, _vp, _vp]),
+    "mlq_hip_softmax": (ctypes.c_int, [ctypes.c_int, _vp, ctypes.c_int, _vp, _vp]),
+    "mlq_hip_embedding": (ctypes.c_int, [ctypes.c_int, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, _vp, _vp]),
+    "mlq_hip_rope": (ctypes.c_int, [ctypes.c_int, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_float,
+                                     ctypes.c_int, _vp]),
+    "mlq_hip_attention_decode": (ctypes.c_int, [ctypes.c_int, _vp, _vp, _vp] + [ctypes.c_int] * 7 + [_vp, _vp]),
+    "mlq_hip_matmul_f32": (ctypes.c_int, [ctypes.c_int, _vp, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                           ctypes.c_int, _vp, _vp]),
     "mlq_hip_kernel_name": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                             ctypes.c_char_p, ctypes.c_size_t]),
 }
@@ -166,6 +184,14 @@ def device_info(device: int = 0) -> str:
     buf = ctypes.create_string_buffer(256)
     _check(load().mlq_hip_device_info(device, buf, 256))
     return buf.value.decode()
+
+
+def device_props(device: int = 0) -> dict:
+    p = DeviceProps()
+    _check(load().mlq_hip_device_props(device, ctypes.byref(p)))
+    return {"name": p.name.decode(), "arch": p.arch.decode(), "major": p.major, "minor": p.minor,
+            "total_memory_bytes": p.total_memory_bytes, "compute_units": p.compute_units,
+            "driver_version": p.driver_version, "runtime_version": p.runtime_version}
 
 
 def init(device: int = 0) -> None:

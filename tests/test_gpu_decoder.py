@@ -252,20 +252,37 @@ def test_batched_prefill_head_dims(hip, orc, ref, tmp_path, dim, heads, kv_heads
     dec.close()
 
 
+# Row widths of the producers that write a GEMM's split x: the RMSNorm row
+# kernel covers `dim`, the SwiGLU row kernel `hidden`, each with C = 1..4
+# halves of 16 elements per thread (C = ceil(width / 4096)).
+SPLIT_SHAPES = {
+    "c1": dict(dim=256, heads=2, kv_heads=1, hidden=768, layers=2),
+    "swiglu_c2": dict(dim=256, heads=2, kv_heads=1, hidden=4608, layers=2),
+    "swiglu_c3": dict(dim=256, heads=2, kv_heads=1, hidden=11008, layers=2),
+    "swiglu_c4": dict(dim=256, heads=2, kv_heads=1, hidden=13824, layers=1),
+    "norm_c2": dict(dim=4608, heads=36, kv_heads=4, hidden=352, layers=1),
+}
+
+
+@pytest.mark.parametrize("shape", list(SPLIT_SHAPES))
 @pytest.mark.parametrize("fmt", ["q4_0", "q8_0", "q4_1"])
-def test_batched_prefill_split_x_written_by_norm_and_swiglu(hip, orc, ref, tmp_path, fmt):
+def test_batched_prefill_split_x_written_by_norm_and_swiglu(hip, orc, ref, tmp_path, fmt, shape):
     """Over 128 rows the RMSNorm and SwiGLU row kernels write the q/k/v,
     gate/up and down GEMMs' split x themselves (every linear of one format, so
-    q/k/v and gate/up run as grouped GEMMs); then a short batch (plain x) reads
-    the cache the long one wrote."""
-    path = mf.write_model(orc, str(tmp_path / f"split_{fmt}.gguf"), dim=256, heads=2, kv_heads=1, hidden=768,
-                          ctx=320, fmts=(fmt,), lm=fmt, seed=21)
+    q/k/v and gate/up run as grouped GEMMs), at every producer width C = 1..4
+    (hidden 768 / 4608 / 11008 / 13824, dim 256 / 4608); then a short batch
+    (plain x) reads the cache the long one wrote."""
+    kw = SPLIT_SHAPES[shape]
+    path = mf.write_model(orc, str(tmp_path / f"split_{fmt}_{shape}.gguf"), ctx=320, fmts=(fmt,), lm=fmt,
+                          seed=21, **kw)
     dec = hip.Decoder(path)
     rd = ref.decoder(path)
     toks = np.random.default_rng(22).integers(0, 300, 260).tolist()
-    worst = close(dec.prefill(toks[:200]), rd.batch(toks[:200]), f"{fmt} batch 0..199")
-    worst = max(worst, close(dec.prefill(toks[200:260], 200), rd.batch(toks[200:260], 200), f"{fmt} batch 200..259"))
-    say(f"  {fmt}: worst relative logit difference {worst:.2e}")
+    say(f"split-x producers {shape} {fmt}: batch of 200 rows, then 60")
+    worst = close(dec.prefill(toks[:200]), rd.batch(toks[:200]), f"{fmt} {shape} batch 0..199")
+    worst = max(worst, close(dec.prefill(toks[200:260], 200), rd.batch(toks[200:260], 200),
+                             f"{fmt} {shape} batch 200..259"))
+    say(f"  {fmt} {shape}: worst relative logit difference {worst:.2e}")
     dec.close()
 
 
