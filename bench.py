@@ -71,6 +71,8 @@ KERNEL_BY_LAUNCH = {
     "per_stage": "Q4_0 GEMV family (gemv_single / gemv_multi), one fused launch per stage (q,k,v | o | gate,up | down)",
     "sequence": "gemv_sequence (persistent, grid barriers between stages)",
     "independent": "gemv_sequence (persistent, no barriers)",
+    "pipelined": "gemv_chain (persistent, grid barriers between stages; weight ring across barriers, control wave "
+                 "per workgroup for stores, arrival and x)",
 }
 
 
@@ -788,7 +790,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--launch", choices=["graph", "plain", "sequence", "per_stage", "independent"],
+    ap.add_argument("--launch", choices=["graph", "plain", "sequence", "per_stage", "independent", "pipelined"],
                     default="per_stage")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline / parity leg")
     ap.add_argument("--no-shapes", action="store_true", help="skip the per-shape GEMV / GEMM tables")
@@ -878,7 +880,7 @@ def main():
     #              all fresh, so nothing depends on anything; reported, not headline).
     seqs = {m: hip.Sequence(sw.calls, sw.stage_ids(), mode)
             for m, mode in (("sequence", hip.SEQ_PERSISTENT), ("per_stage", hip.SEQ_PER_STAGE),
-                            ("independent", hip.SEQ_INDEPENDENT))}
+                            ("independent", hip.SEQ_INDEPENDENT), ("pipelined", hip.SEQ_PIPELINED))}
     graph = hip.Graph(sw.calls, stream)
     stage_graph = hip.Graph(sequence=seqs["per_stage"])
     steps_by_mode = {
@@ -887,6 +889,7 @@ def main():
         "sequence": lambda: seqs["sequence"].launch(stream),
         "per_stage": lambda: stage_graph.launch(stream),
         "independent": lambda: seqs["independent"].launch(stream),
+        "pipelined": lambda: seqs["pipelined"].launch(stream),
     }
     variants = {}
     for name, fn in steps_by_mode.items():
@@ -918,7 +921,8 @@ def main():
             f"{floor['gbs']:8.1f} GB/s")
     seq_info = seqs["sequence"].info()
     launches = {"graph": sw.n(), "plain": sw.n(), "per_stage": seqs["per_stage"].info()["launches"],
-                "sequence": seq_info["launches"], "independent": seqs["independent"].info()["launches"]}[args.launch]
+                "sequence": seq_info["launches"], "independent": seqs["independent"].info()["launches"],
+                "pipelined": seqs["pipelined"].info()["launches"]}[args.launch]
     log(f"sweep: {ms_step * 1e3:.1f} us/step, {gbs:.1f} GB/s ({args.launch}); sequence {seq_info}")
 
     shapes = []

@@ -264,13 +264,21 @@ int mlq_hip_graph_end(int device, void* stream, mlq_graph_t* out);
  *   MLQ_SEQ_PER_STAGE    one launch per stage, ordered by the stream (same
  *                        semantics, no device-wide barrier);
  *   MLQ_SEQ_INDEPENDENT  one launch without barriers: no call may read any
- *                        call's output (checked when the sequence is created).
+ *                        call's output (checked when the sequence is created);
+ *   MLQ_SEQ_PIPELINED    the semantics of MLQ_SEQ_PERSISTENT (device-wide
+ *                        barrier before every stage) in one launch whose
+ *                        weight requests run ahead across the barriers: per
+ *                        workgroup a control wave stores a stage's last rows,
+ *                        synchronizes the grid and loads the next x while the
+ *                        compute waves' next-stage weights are in flight.
+ *                        Every call needs in_features % 32 == 0.
  * The sequence keeps the pointers (buffers must outlive it and any graph
  * captured from it); launches of one sequence must not overlap in time. */
 typedef struct mlq_sequence_s* mlq_sequence_t;
 #define MLQ_SEQ_PERSISTENT 0
 #define MLQ_SEQ_PER_STAGE 1
 #define MLQ_SEQ_INDEPENDENT 2
+#define MLQ_SEQ_PIPELINED 3
 int mlq_hip_sequence_create(const mlq_linear_call* calls, int n, const int* stage, int mode,
                             mlq_sequence_t* out);
 int mlq_hip_sequence_launch(mlq_sequence_t seq, void* stream);

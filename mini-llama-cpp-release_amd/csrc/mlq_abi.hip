@@ -63,6 +63,7 @@ struct mlq_sequence_s {
         int nstages;
         int lds_bytes;
         int grid;
+        int kmax;  // largest in_features of the segment (pipelined mode)
     };
     int device;
     int mode;
@@ -78,6 +79,7 @@ struct mlq_sequence_s {
     std::vector<HostStage> host_stages;
     void* mem;               // [stage descriptors][SeqSync per segment]
     size_t sync_offset;      // byte offset of the first SeqSync
+    size_t sink_offset;      // pipelined mode: byte offset of the chain kernel's sink words
 };
 
 namespace {
@@ -1221,7 +1223,8 @@ int mlq_hip_sequence_create(const mlq_linear_call* calls, int n, const int* stag
     if (out == nullptr) return fail(MLQ_ERR_INVALID, std::string(caller) + ": null output");
     *out = nullptr;
     if (calls == nullptr || n <= 0) return fail(MLQ_ERR_INVALID, std::string(caller) + ": no calls");
-    if (mode != MLQ_SEQ_PERSISTENT && mode != MLQ_SEQ_PER_STAGE && mode != MLQ_SEQ_INDEPENDENT) {
+    if (mode != MLQ_SEQ_PERSISTENT && mode != MLQ_SEQ_PER_STAGE && mode != MLQ_SEQ_INDEPENDENT &&
+        mode != MLQ_SEQ_PIPELINED) {
         return fail(MLQ_ERR_INVALID, std::string(caller) + ": unknown mode " + std::to_string(mode));
     }
     if (calls[0].w == nullptr) return fail(MLQ_ERR_INVALID, std::string(caller) + ": null weight handle");
@@ -1243,6 +1246,10 @@ int mlq_hip_sequence_create(const mlq_linear_call* calls, int n, const int* stag
         if (!mlq::sequence_supported(c.w->qtype, c.w->K)) {
             return fail(MLQ_ERR_LIMIT, at + ": in_features=" + std::to_string(c.w->K) +
                                            " needs an even block count and at most 15360 elements");
+        }
+        if (mode == MLQ_SEQ_PIPELINED && c.w->K % mlq::kQK != 0) {
+            return fail(MLQ_ERR_LIMIT, at + ": in_features=" + std::to_string(c.w->K) +
+                                           "; MLQ_SEQ_PIPELINED needs in_features % 32 == 0");
         }
         const char* lin = caller_for(c.w->qtype);
         const size_t xb = static_cast<size_t>(c.w->K) * sizeof(float);
@@ -1359,14 +1366,17 @@ int mlq_hip_sequence_create(const mlq_linear_call* calls, int n, const int* stag
             auto& last = seq->segs.back();
             last.nstages += 1;
             last.lds_bytes = std::max(last.lds_bytes, lds);
-            descs[s].barrier = mode == MLQ_SEQ_PERSISTENT ? 1 : 0;
+            last.kmax = std::max(last.kmax, w0->K);
+            descs[s].barrier = mode == MLQ_SEQ_PERSISTENT || mode == MLQ_SEQ_PIPELINED ? 1 : 0;
         } else {
-            seq->segs.push_back(mlq_sequence_s::Segment{w0->qtype, lpr, s, 1, lds, 0});
+            seq->segs.push_back(mlq_sequence_s::Segment{w0->qtype, lpr, s, 1, lds, 0, w0->K});
             descs[s].barrier = 0;
         }
     }
     for (auto& g : seq->segs) {
-        hipError_t e = mlq::sequence_grid(g.qtype, g.lpr, g.lds_bytes, device, &g.grid);
+        if (mode == MLQ_SEQ_PIPELINED) g.lds_bytes = mlq::chain_lds_bytes(g.qtype, g.kmax);
+        hipError_t e = mode == MLQ_SEQ_PIPELINED ? mlq::chain_grid(g.qtype, g.lpr, g.lds_bytes, device, &g.grid)
+                                                 : mlq::sequence_grid(g.qtype, g.lpr, g.lds_bytes, device, &g.grid);
         if (e != hipSuccess) {
             delete seq;
             return hip_fail(e, "sequence occupancy");
@@ -1375,7 +1385,7 @@ int mlq_hip_sequence_create(const mlq_linear_call* calls, int n, const int* stag
             // A stage reads x coherently when an earlier stage of the same
             // launch writes where it reads.
             descs[k].coherent = 0;
-            if (mode == MLQ_SEQ_PERSISTENT) {
+            if (mode == MLQ_SEQ_PERSISTENT || mode == MLQ_SEQ_PIPELINED) {
                 for (int e2 = g.stage_begin; e2 < k; ++e2)
                     for (int c = stage_first[e2]; c < stage_first[e2] + descs[e2].ncalls; ++c)
                         if (overlaps(yr[c], xr[stage_first[k]])) descs[k].coherent = 1;
@@ -1384,7 +1394,9 @@ int mlq_hip_sequence_create(const mlq_linear_call* calls, int n, const int* stag
     }
     const size_t table_bytes = descs.size() * sizeof(mlq::SeqStageDesc);
     seq->sync_offset = (table_bytes + 255) & ~static_cast<size_t>(255);
-    const size_t total = seq->sync_offset + seq->segs.size() * sizeof(mlq::SeqSync);
+    const size_t sync_end = seq->sync_offset + seq->segs.size() * sizeof(mlq::SeqSync);
+    seq->sink_offset = (sync_end + 255) & ~static_cast<size_t>(255);
+    const size_t total = seq->sink_offset + (mode == MLQ_SEQ_PIPELINED ? mlq::chain_sink_bytes() : 0);
     hipError_t e = hipMalloc(&seq->mem, total);
     if (e == hipSuccess) e = hipMemset(seq->mem, 0, total);
     if (e == hipSuccess) e = hipMemcpy(seq->mem, descs.data(), table_bytes, hipMemcpyHostToDevice);
@@ -1414,6 +1426,13 @@ int mlq_hip_sequence_launch(mlq_sequence_t seq, void* stream) {
     auto* syncs = reinterpret_cast<mlq::SeqSync*>(static_cast<char*>(seq->mem) + seq->sync_offset);
     for (size_t i = 0; i < seq->segs.size(); ++i) {
         const auto& g = seq->segs[i];
+        if (seq->mode == MLQ_SEQ_PIPELINED) {
+            float* sink = reinterpret_cast<float*>(static_cast<char*>(seq->mem) + seq->sink_offset);
+            hipError_t e = mlq::launch_chain(g.qtype, g.lpr, table + g.stage_begin, g.nstages, syncs + i, g.grid,
+                                             g.lds_bytes, seq->spin_limit, g.kmax, sink, s);
+            if (e != hipSuccess) return hip_fail(e, mlq::chain_kernel_name(g.qtype, g.lpr));
+            continue;
+        }
         hipError_t e = mlq::launch_sequence(g.qtype, g.lpr, table + g.stage_begin, g.nstages, syncs + i, g.grid,
                                             g.lds_bytes, seq->spin_limit, s);
         if (e != hipSuccess) return hip_fail(e, mlq::sequence_kernel_name(g.qtype, g.lpr));

@@ -181,6 +181,15 @@ hipError_t launch_sequence(int qtype, int lpr, const SeqStageDesc* stages, int n
                            int grid, int lds_bytes, unsigned spin_limit, hipStream_t stream);
 const char* sequence_kernel_name(int qtype, int lpr);
 
+// Pipelined chain kernel (chain.hip): the same stage descriptors, stages of
+// K % 32 == 0; kmax = largest K of the launch.
+int chain_lds_bytes(int qtype, int kmax);
+hipError_t chain_grid(int qtype, int lpr, int lds_bytes, int device, int* grid);
+hipError_t launch_chain(int qtype, int lpr, const SeqStageDesc* stages, int nstages, SeqSync* sync, int grid,
+                        int lds_bytes, unsigned spin_limit, int kmax, float* sink, hipStream_t stream);
+size_t chain_sink_bytes();  // device words a launch's compute lanes store dropped values to
+const char* chain_kernel_name(int qtype, int lpr);
+
 // Device forward ops (ops.hip) behind the op-by-op device interfaces of the
 // reference (include/mini_llama/cuda_ops.h, cuda_attention.h, cuda_matmul.h).
 constexpr int kOpSilu = 0;

@@ -97,7 +97,7 @@ def test_chain_matches_per_call_launches(hip, fmt):
     want = snapshot(outs)
     for b in outs:
         b.fill(0)
-    for mode in (hip.SEQ_PERSISTENT, hip.SEQ_PER_STAGE):
+    for mode in (hip.SEQ_PERSISTENT, hip.SEQ_PER_STAGE, hip.SEQ_PIPELINED):
         say(f"sequence chain {fmt} mode={mode}")
         seq = run_sequence(hip, calls, stages, mode)
         got = snapshot(outs)
@@ -141,7 +141,7 @@ def test_independent_shapes_all_modes(hip, shape):
         calls = [(lins[i], x, outs[i]) for i in range(4)]
         per_call(hip, calls)
         want = snapshot(outs)
-        for mode in (hip.SEQ_PERSISTENT, hip.SEQ_PER_STAGE, hip.SEQ_INDEPENDENT):
+        for mode in (hip.SEQ_PERSISTENT, hip.SEQ_PER_STAGE, hip.SEQ_INDEPENDENT, hip.SEQ_PIPELINED):
             for stages in ([0, 0, 0, 0], [0, 1, 1, 2], None):
                 for b in outs:
                     b.fill(0)
@@ -171,13 +171,14 @@ def test_mixed_formats_split_launches(hip):
         assert np.array_equal(g.view(np.uint32), w.view(np.uint32)), f"call {i}"
 
 
-def test_graph_replays(hip):
+@pytest.mark.parametrize("mode", ["persistent", "pipelined"])
+def test_graph_replays(hip, mode):
     """A captured sequence replayed with new x contents and eager work between
     replays: every replay equals per-call launches on the same x."""
     calls, stages, outs, keep = llama_layer(hip, oracle.Q4_0, seed=21)
     x = keep[-1]
     arr = hip.make_calls([(w.w, xx, y, 1) for w, xx, y in calls])
-    seq = hip.Sequence(arr, stages, hip.SEQ_PERSISTENT)
+    seq = hip.Sequence(arr, stages, hip.SEQ_PERSISTENT if mode == "persistent" else hip.SEQ_PIPELINED)
     g = hip.Graph(sequence=seq)
     scratch = hip.DeviceBuffer(4 * 4096)
     for rep in range(4):
@@ -228,11 +229,16 @@ def test_validation_messages(hip):
         create([(l1.w, x, ys[i], 1) for i in range(5)], [0] * 5)
     with pytest.raises(hip.MlqError, match="unknown mode"):
         create([(l1.w, x, y, 1)], None, 7)
+    k40 = Lin(hip, oracle.Q4_0, 64, 40, 6)  # two blocks per row, the second partial
+    with pytest.raises(hip.MlqError, match="MLQ_SEQ_PIPELINED needs in_features % 32 == 0"):
+        create([(k40.w, x, y, 1)], None, hip.SEQ_PIPELINED)
+    create([(k40.w, x, y, 1)], None, hip.SEQ_PERSISTENT).destroy()
     # a dependent chain is fine in the barrier modes
     create([(l1.w, x, y, 1), (l64.w, y, y2, 1)]).destroy()
 
 
-def test_barrier_wait_bound_recovers(hip):
+@pytest.mark.parametrize("mode", ["persistent", "pipelined"])
+def test_barrier_wait_bound_recovers(hip, mode):
     """With a one-poll bound the barrier waits give up instead of spinning; the
     launch still ends, the status reports it, and the next launch with the
     default bound is correct again (the barrier words reset themselves)."""
@@ -240,7 +246,7 @@ def test_barrier_wait_bound_recovers(hip):
     per_call(hip, calls)
     want = snapshot(outs)
     arr = hip.make_calls([(w.w, x, y, 1) for w, x, y in calls])
-    seq = hip.Sequence(arr, stages, hip.SEQ_PERSISTENT)
+    seq = hip.Sequence(arr, stages, hip.SEQ_PERSISTENT if mode == "persistent" else hip.SEQ_PIPELINED)
     seq.set_spin_limit(1)
     say("sequence with a one-poll barrier bound")
     seq.launch()

@@ -2,7 +2,8 @@
 sweep (3.727 GB) in the launch structure the bench times as its headline --
 one fused launch per decode stage (q/k/v | o | gate/up | down, then lm_head),
 129 dependent launches recorded as one graph -- and in the persistent
-sequence kernel with grid barriers between the same stages.
+sequence kernels with grid barriers between the same stages (plain and
+pipelined).
 
 Every one of the 225 outputs is checked against the CPU linear of the oracle
 (the reference's linear_quantized_impl, src/quant.cpp:367-433) on the same
@@ -50,11 +51,11 @@ def cpu_outputs(sweep, orc):
     return out
 
 
-@pytest.mark.parametrize("launch", ["per_stage", "sequence"])
+@pytest.mark.parametrize("launch", ["per_stage", "sequence", "pipelined"])
 def test_config5_sweep_matches_cpu(hip, sweep, cpu_outputs, orc, launch):
     say(f"config 5 sweep, launch {launch}: 225 calls, every output against the CPU linear")
     stream = hip.stream(0)
-    mode = hip.SEQ_PER_STAGE if launch == "per_stage" else hip.SEQ_PERSISTENT
+    mode = {"per_stage": hip.SEQ_PER_STAGE, "sequence": hip.SEQ_PERSISTENT, "pipelined": hip.SEQ_PIPELINED}[launch]
     seq = hip.Sequence(sweep.calls, sweep.stage_ids(), mode)
     graph = hip.Graph(sequence=seq) if launch == "per_stage" else None
     for y in sweep.ys:
