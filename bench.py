@@ -105,15 +105,24 @@ def time_region(fn, steps, stream):
 
 
 def cpu_model():
-    """The host CPU's model name (from /proc/cpuinfo), for the baseline line."""
+    """The host CPU (from /proc/cpuinfo: model name, family / model / stepping
+    numbers, logical CPUs), for the baseline line; some hosts report only a
+    generic model name, which the numbers then identify."""
+    fields, cpus = {}, 0
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
+                key, _, val = line.partition(":")
+                key = key.strip()
+                if key == "processor":
+                    cpus += 1
+                elif key in ("model name", "cpu family", "model", "stepping") and key not in fields:
+                    fields[key] = val.strip()
     except OSError:
-        pass
-    return "unknown"
+        return "unknown"
+    name = fields.get("model name", "unknown")
+    ids = ", ".join(f"{k} {fields[k]}" for k in ("cpu family", "model", "stepping") if k in fields)
+    return f"{name} ({ids}; {cpus} logical CPUs)" if ids else name
 
 
 def cpu_sweep_check(sw: Sweep, threads: int, runs: int = 3):
@@ -166,11 +175,15 @@ def cpu_sweep_check(sw: Sweep, threads: int, runs: int = 3):
     }
 
 
-def floor_bench(sw: Sweep, stream, steps: int, warmup: int):
+def floor_bench(sw: Sweep, stream, steps: int, warmup: int, probe=None):
     """The sweep's 129 stages as weight-stream-only launches (mlq_hip_stream_floor:
     the GEMV kernels' grid, work units and request ring, no arithmetic),
     recorded as one graph like the headline: the floor that one launch per
-    stage pays for launching and streaming the weights."""
+    stage pays for launching and streaming the weights.  probe: the floor's
+    parts instead (mlq_hip_stream_probe): PROBE_EMPTY, the same grid launched
+    with no work (the dependent-launch cost), or PROBE_LOAD, the same bytes
+    read with plain coalesced 16-byte loads (launch plus stream, without the
+    GEMV's work units)."""
     ids = sw.stage_ids()
     groups, i = [], 0
     while i < len(ids):
@@ -180,18 +193,29 @@ def floor_bench(sw: Sweep, stream, steps: int, warmup: int):
         groups.append(hip.make_calls([(w, x, y, 1) for (_, w, x, y) in sw.calls_desc[i:j]]))
         i = j
     sink = hip.DeviceBuffer(4 * 65536)
-    graph = hip.Graph.record(lambda: [hip.stream_floor(g, sink, stream) for g in groups], stream,
-                             keep=(groups, sink))
+    if probe is None:
+        graph = hip.Graph.record(lambda: [hip.stream_floor(g, sink, stream) for g in groups], stream,
+                                 keep=(groups, sink))
+    else:
+        graph = hip.Graph.record(lambda: [hip.stream_probe(g, probe, sink, stream) for g in groups], stream,
+                                 keep=(groups, sink))
     for _ in range(warmup):
         graph.launch(stream)
     ms = time_region(lambda: graph.launch(stream), steps, stream) / steps
     graph.destroy()
     sink.free()
-    return {"launches": len(groups), "us_per_step": round(ms * 1e3, 1),
-            "gbs": round(sw.bytes / (ms * 1e-3) / 1e9, 1),
-            "us_per_launch": round(ms * 1e3 / len(groups), 3),
-            "note": "mlq_hip_stream_floor per stage (weights streamed with the GEMV grid and ring, no "
-                    "arithmetic), one graph of the same 129 dependent launches as per_stage"}
+    note = {None: "mlq_hip_stream_floor per stage (weights streamed with the GEMV grid and ring, no "
+                  "arithmetic), one graph of the same 129 dependent launches as per_stage",
+            hip.PROBE_EMPTY: "mlq_hip_stream_probe(MLQ_PROBE_EMPTY) per stage: the floor's grid launched with "
+                             "no work, one graph of 129 dependent launches (the launch cost alone)",
+            hip.PROBE_LOAD: "mlq_hip_stream_probe(MLQ_PROBE_LOAD) per stage: the stage's weight bytes read with "
+                            "plain coalesced 16-byte loads on the floor's grid, one graph of 129 dependent "
+                            "launches (launch plus stream, no GEMV work units)"}[probe]
+    res = {"launches": len(groups), "us_per_step": round(ms * 1e3, 1),
+           "us_per_launch": round(ms * 1e3 / len(groups), 3), "note": note}
+    if probe != hip.PROBE_EMPTY:
+        res["gbs"] = round(sw.bytes / (ms * 1e-3) / 1e9, 1)
+    return res
 
 
 # ------------------------------------------------------------------ per-shape GEMV
@@ -811,7 +835,8 @@ def main():
     ap.add_argument("--gemm-only", action="store_true",
                     help="run only the prefill GEMM table (config 4) and print it as one JSON line")
     ap.add_argument("--gemm-filter", default="",
-                    help="with --gemm-only: keep the configs named fmt:M:N (comma-separated, e.g. q4_0:4096:64)")
+                    help="with --gemm-only: keep the configs named fmt:M:N (comma-separated, e.g. q4_0:4096:64); "
+                         "fmt:M:N:K adds a shape with K other than 4096")
     ap.add_argument("--profile-summary", default="",
                     help="print per-stage tables of this rocprofv3 CSV output directory (of a --launch "
                          "per_stage --no-variants run with the same --steps) and exit; no GPU use")
@@ -833,9 +858,16 @@ def main():
         if args.calibration_copy_mb > 0:
             calibration_copy(args.calibration_copy_mb, stream)
         rows = []
-        for cfg in GEMM_CONFIGS:
-            qt, m, _, n = cfg
-            if keep and f"{FMT_NAME[qt]}:{m}:{n}" not in keep:
+        configs = list(GEMM_CONFIGS)
+        by_name = {v: k for k, v in FMT_NAME.items()}
+        for f in sorted(keep):
+            parts = f.split(":")
+            if len(parts) == 4:  # fmt:M:N:K, a shape outside the config-4 list
+                configs.append((by_name[parts[0]], int(parts[1]), int(parts[3]), int(parts[2])))
+        for cfg in configs:
+            qt, m, k, n = cfg
+            name = f"{FMT_NAME[qt]}:{m}:{n}" + ("" if k == 4096 else f":{k}")
+            if keep and name not in keep:
                 continue
             r = gemm_shape_bench(*cfg, stream)
             log(f"  gemm {r['fmt']} {r['M']:>6}x{r['K']:<5} N={r['N']:<4} {r['us_per_call']:9.2f} us "
@@ -916,9 +948,13 @@ def main():
     ms_step = ms / args.steps
     gbs = sw.bytes / (ms_step * 1e-3) / 1e9
     floor = floor_bench(sw, stream, args.steps, args.warmup)
-    if floor:
-        log(f"sweep floor (weights only, one launch per stage): {floor['us_per_step']:8.1f} us/step, "
-            f"{floor['gbs']:8.1f} GB/s")
+    log(f"sweep floor (weights only, one launch per stage): {floor['us_per_step']:8.1f} us/step, "
+        f"{floor['gbs']:8.1f} GB/s")
+    empty = floor_bench(sw, stream, args.steps, args.warmup, hip.PROBE_EMPTY)
+    load_only = floor_bench(sw, stream, args.steps, args.warmup, hip.PROBE_LOAD)
+    log(f"sweep launch cost (129 empty dependent launches): {empty['us_per_step']:8.1f} us/step, "
+        f"{empty['us_per_launch']:.3f} us/launch; load-only chain: {load_only['us_per_step']:8.1f} us/step, "
+        f"{load_only['gbs']:8.1f} GB/s")
     seq_info = seqs["sequence"].info()
     launches = {"graph": sw.n(), "plain": sw.n(), "per_stage": seqs["per_stage"].info()["launches"],
                 "sequence": seq_info["launches"], "independent": seqs["independent"].info()["launches"],
@@ -1014,7 +1050,8 @@ def main():
                    "bytes_per_step": sw.bytes, "launch": args.launch,
                    "sweep_us": round(ms_step * 1e3, 1),
                    "sweep_us_by_launch": {k: round(v * 1e3, 1) for k, v in variants.items()},
-                   "per_stage_floor": floor},
+                   "per_stage_floor": floor, "per_stage_empty_launches": empty,
+                   "per_stage_load_only": load_only},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(args.launch),
                      "algorithmic_bytes_per_launch": round(sw.bytes / launches),

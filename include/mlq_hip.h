@@ -177,6 +177,17 @@ int mlq_hip_quant_linear_fused(const mlq_linear_call* calls, int n, void* stream
  * stream).  Asynchronous on `stream`. */
 int mlq_hip_stream_floor(const mlq_linear_call* calls, int n, void* sink, void* stream);
 
+/* Measurement, not a linear: the floor's two parts, for the same `calls` and
+ * `sink`.  MLQ_PROBE_EMPTY launches the floor's grid and does nothing (the
+ * cost of a launch); MLQ_PROBE_LOAD streams the same weight bytes with plain
+ * coalesced 16-byte loads, each thread reading every T-th unit of the calls'
+ * weights taken back to back (the cost of the bytes without the GEMV's work
+ * units; a tail under 16 bytes per weight is not read).  Asynchronous on
+ * `stream`. */
+#define MLQ_PROBE_EMPTY 1
+#define MLQ_PROBE_LOAD 2
+int mlq_hip_stream_probe(const mlq_linear_call* calls, int n, int mode, void* sink, void* stream);
+
 /* Greedy pick fused into the decode GEMV of an output projection (lm_head):
  * y = W x as mlq_hip_quant_linear (bit for bit; y may be NULL when the logits
  * are not needed) and *token = the first index of the largest y, or -1 when

@@ -1279,6 +1279,21 @@ GemmSplitX gemm_split_x(const LinearShape& s, int n, const int* M) {
     return r;
 }
 
+bool gemm_group_supported(const LinearShape& s, int n, const int* M, const float* x) {
+    if (n < 1 || n > 3 || M == nullptr) return false;
+    LinearShape st = s;
+    st.M = 0;
+    for (int g = 0; g < n; ++g) {
+        if (M[g] <= 0) return false;
+        st.M += M[g];
+    }
+    if (!use_chunk(st, x)) return false;
+    const int bm = 64 * choose_chunk(st).rw;
+    for (int g = 0; g + 1 < n; ++g)
+        if (M[g] % bm != 0) return false;  // a row tile may not straddle two weights
+    return true;
+}
+
 hipError_t launch_gemm_group(const LinearShape& s, int n, const void* const* w, float* const* y, const int* M,
                              const float* x, void* ws, size_t ws_bytes, hipStream_t stream, bool x_split) {
     if (n < 1 || n > 3 || w == nullptr || y == nullptr || M == nullptr) return hipErrorInvalidValue;
@@ -1288,12 +1303,9 @@ hipError_t launch_gemm_group(const LinearShape& s, int n, const void* const* w, 
         if (M[g] <= 0) return hipErrorInvalidValue;
         st.M += M[g];
     }
-    if (!use_chunk(st, x)) return hipErrorNotSupported;
+    if (!gemm_group_supported(s, n, M, x)) return hipErrorNotSupported;
     const ChunkCfg c = choose_chunk(st);
     if (x_split && !c.xs) return hipErrorInvalidValue;  // gemm_split_x said no
-    const int bm = 64 * c.rw;
-    for (int g = 0; g + 1 < n; ++g)
-        if (M[g] % bm != 0) return hipErrorNotSupported;  // a row tile may not straddle two weights
     if (ws == nullptr) return hipErrorInvalidValue;
     if (ws_bytes < chunk_workspace_bytes(st)) return hipErrorInvalidValue;
     ChunkGroup grp{};

@@ -665,6 +665,39 @@ __global__ __launch_bounds__(kWaves * 64, 2) void stream_floor_kernel(const Gemv
     sink[(static_cast<size_t>(gw) * 64 + lane) & (kFloorSinkWords - 1)] = acc;
 }
 
+// Measurement kernels (not GEMVs) that take a GEMV launch's floor apart:
+// probe_empty_kernel is the launch alone (the floor's grid, no work);
+// probe_load_kernel streams the same weights with the plainest pattern: each
+// call's weight bytes as 16-byte units, thread t of T reading units t, t + T,
+// ... eight at a time, folded into one XOR (a tail of under 16 bytes per call
+// is not read).
+__global__ __launch_bounds__(kWaves * 64) void probe_empty_kernel(uint32_t* __restrict__ sink) {
+    (void)sink;
+}
+
+typedef uint32_t probe_u4 __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(kWaves * 64) void probe_load_kernel(const GemvGroup g, int M, size_t row_bytes,
+                                                                 uint32_t* __restrict__ sink) {
+    const size_t T = static_cast<size_t>(gridDim.x) * blockDim.x;
+    const size_t t = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    probe_u4 acc{0u, 0u, 0u, 0u};
+    for (int j = 0; j < g.ncalls; ++j) {
+        const int r0 = g.row_begin[j];
+        const int r1 = j + 1 < g.ncalls ? g.row_begin[j + 1] : M;
+        const size_t units = static_cast<size_t>(r1 - r0) * row_bytes / 16;
+        const probe_u4* w = static_cast<const probe_u4*>(g.W[j]);
+        for (size_t u = t; u < units; u += 8 * T) {
+            probe_u4 v[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) v[k] = u + k * T < units ? w[u + k * T] : probe_u4{0u, 0u, 0u, 0u};
+#pragma unroll
+            for (int k = 0; k < 8; ++k) acc ^= v[k];
+        }
+    }
+    sink[t & (kFloorSinkWords - 1)] = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
+}
+
 }  // namespace
 
 hipError_t launch_gemv_group(const LinearShape& s, const GemvGroup& g, const float* x, hipStream_t stream) {
@@ -784,6 +817,26 @@ hipError_t launch_stream_floor(const LinearShape& s, const GemvGroup& g, uint32_
         case 364: return go(stream_floor_kernel<3, 64, 3>);
         default: return hipErrorInvalidValue;
     }
+}
+
+hipError_t launch_stream_probe(const LinearShape& s, const GemvGroup& g, int mode, uint32_t* sink,
+                               hipStream_t stream) {
+    if (g.ncalls < 1 || g.ncalls > kGroupMaxCalls || sink == nullptr) return hipErrorInvalidValue;
+    // The floor's grid: one persistent workgroup of kWaves waves per CU at most.
+    const int np = s.nb / 2;
+    const int rows_per_item = np > 16 ? 1 : 4;
+    const int items = (s.M + rows_per_item - 1) / rows_per_item;
+    int grid = (items + kWaves - 1) / kWaves;
+    if (grid > kPersistentWgs) grid = kPersistentWgs;
+    if (mode == kProbeEmpty) {
+        hipLaunchKernelGGL(probe_empty_kernel, dim3(grid), dim3(kWaves * 64), 0, stream, sink);
+    } else if (mode == kProbeLoad) {
+        const size_t row_bytes = static_cast<size_t>(s.nb) * block_bytes(s.qtype);
+        hipLaunchKernelGGL(probe_load_kernel, dim3(grid), dim3(kWaves * 64), 0, stream, g, s.M, row_bytes, sink);
+    } else {
+        return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
 }
 
 const char* gemv_kernel_name(const LinearShape& s) {

@@ -697,11 +697,13 @@ int mlq_hip_quant_linear_fused(const mlq_linear_call* calls, int n, void* stream
         // most three weights, each but the last a whole number of row tiles),
         // else one GEMM (or GEMV batch) per call.
         mlq::LinearShape total{w0->qtype, static_cast<int>(rows), w0->K, w0->nb, nrows};
-        if (n <= 3 && mlq::gemm_supported(total)) {
+        int M[3] = {0, 0, 0};
+        for (int i = 0; i < n && i < 3; ++i) M[i] = calls[i].w->M;
+        // The workspace is sized (and grown) only for a group that will launch.
+        if (n <= 3 && mlq::gemm_supported(total) && mlq::gemm_group_supported(total, n, M, calls[0].x)) {
             const void* wd[3];
             float* yd[3];
-            int M[3];
-            for (int i = 0; i < n; ++i) wd[i] = calls[i].w->ptr, yd[i] = calls[i].y, M[i] = calls[i].w->M;
+            for (int i = 0; i < n; ++i) wd[i] = calls[i].w->ptr, yd[i] = calls[i].y;
             const size_t need = mlq::gemm_workspace_bytes(total);
             void* ws = nullptr;
             if ((rc = stream_workspace(device, s, need, &ws)) != MLQ_OK) return rc;
@@ -725,8 +727,12 @@ int mlq_hip_quant_linear_fused(const mlq_linear_call* calls, int n, void* stream
     return MLQ_OK;
 }
 
-int mlq_hip_stream_floor(const mlq_linear_call* calls, int n, void* sink, void* stream) {
-    static const char* caller = "mlq_hip_stream_floor";
+namespace {
+
+// The group of a measurement launch (mlq_hip_stream_floor / _probe): calls
+// validated as for a fused launch, weights only.
+int floor_group(const mlq_linear_call* calls, int n, void* sink, const char* caller, mlq::GemvGroup& g,
+                mlq::LinearShape& shape, int& device) {
     if (calls == nullptr || n <= 0) return fail(MLQ_ERR_INVALID, std::string(caller) + ": no calls");
     if (n > mlq::kGroupMaxCalls) {
         return fail(MLQ_ERR_LIMIT, std::string(caller) + ": " + std::to_string(n) + " calls (at most " +
@@ -734,12 +740,12 @@ int mlq_hip_stream_floor(const mlq_linear_call* calls, int n, void* sink, void* 
     }
     if (calls[0].w == nullptr) return fail(MLQ_ERR_INVALID, std::string(caller) + ": null weight handle");
     const mlq_weight_s* w0 = calls[0].w;
-    const int device = w0->device;
+    device = w0->device;
     int rc = ensure_device(device);
     if (rc != MLQ_OK) return rc;
     if ((rc = check_device_ptr(sink, device, caller, "sink", size_t(mlq::kFloorSinkWords) * 4)) != MLQ_OK) return rc;
     if (w0->nb % 2 != 0) return fail(MLQ_ERR_INVALID, std::string(caller) + ": needs an even block count");
-    mlq::GemvGroup g{};
+    g = mlq::GemvGroup{};
     long long rows = 0;
     for (int i = 0; i < n; ++i) {
         const mlq_linear_call& c = calls[i];
@@ -755,8 +761,36 @@ int mlq_hip_stream_floor(const mlq_linear_call* calls, int n, void* sink, void* 
     }
     if (rows > (1ll << 30)) return fail(MLQ_ERR_LIMIT, std::string(caller) + ": too many rows");
     g.ncalls = n;
-    mlq::LinearShape shape{w0->qtype, static_cast<int>(rows), w0->K, w0->nb, 1};
+    shape = mlq::LinearShape{w0->qtype, static_cast<int>(rows), w0->K, w0->nb, 1};
+    return MLQ_OK;
+}
+
+}  // namespace
+
+int mlq_hip_stream_floor(const mlq_linear_call* calls, int n, void* sink, void* stream) {
+    static const char* caller = "mlq_hip_stream_floor";
+    mlq::GemvGroup g;
+    mlq::LinearShape shape;
+    int device = 0;
+    const int rc = floor_group(calls, n, sink, caller, g, shape, device);
+    if (rc != MLQ_OK) return rc;
     hipError_t e = mlq::launch_stream_floor(shape, g, static_cast<uint32_t*>(sink), resolve_stream(device, stream));
+    if (e != hipSuccess) return hip_fail(e, caller);
+    return MLQ_OK;
+}
+
+int mlq_hip_stream_probe(const mlq_linear_call* calls, int n, int mode, void* sink, void* stream) {
+    static const char* caller = "mlq_hip_stream_probe";
+    if (mode != MLQ_PROBE_EMPTY && mode != MLQ_PROBE_LOAD) {
+        return fail(MLQ_ERR_INVALID, std::string(caller) + ": unknown mode " + std::to_string(mode));
+    }
+    mlq::GemvGroup g;
+    mlq::LinearShape shape;
+    int device = 0;
+    const int rc = floor_group(calls, n, sink, caller, g, shape, device);
+    if (rc != MLQ_OK) return rc;
+    const int m = mode == MLQ_PROBE_EMPTY ? mlq::kProbeEmpty : mlq::kProbeLoad;
+    hipError_t e = mlq::launch_stream_probe(shape, g, m, static_cast<uint32_t*>(sink), resolve_stream(device, stream));
     if (e != hipSuccess) return hip_fail(e, caller);
     return MLQ_OK;
 }

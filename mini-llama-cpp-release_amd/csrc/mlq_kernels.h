@@ -96,6 +96,12 @@ hipError_t launch_gemv_pick_norm(const LinearShape& s, const void* w, const floa
 // kFloorSinkWords words the kernel overwrites.
 constexpr int kFloorSinkWords = 1 << 16;
 hipError_t launch_stream_floor(const LinearShape& s, const GemvGroup& g, uint32_t* sink, hipStream_t stream);
+// The floor's two parts: kProbeEmpty launches the floor's grid with no work;
+// kProbeLoad streams the same weight bytes with plain coalesced 16-byte loads.
+constexpr int kProbeEmpty = 1;
+constexpr int kProbeLoad = 2;
+hipError_t launch_stream_probe(const LinearShape& s, const GemvGroup& g, int mode, uint32_t* sink,
+                               hipStream_t stream);
 
 // Batched prefill GEMM for rows > 1 (MFMA).  Needs a device workspace of
 // gemm_workspace_bytes(s) bytes (split x, scales, split-K partials) that no
@@ -120,6 +126,9 @@ const char* gemm_kernel_name(const LinearShape& s);
 // not read and no split launch is made.
 hipError_t launch_gemm_group(const LinearShape& s, int n, const void* const* w, float* const* y, const int* M,
                              const float* x, void* ws, size_t ws_bytes, hipStream_t stream, bool x_split = false);
+// Whether launch_gemm_group would launch that group (rather than return
+// hipErrorNotSupported), so a caller sizes a workspace only when it will.
+bool gemm_group_supported(const LinearShape& s, int n, const int* M, const float* x);
 
 // Where a grouped (or, n = 1, single) GEMM of `rows` > 128 token rows reads
 // its split x inside the workspace (xsplit_device.h's layout: xs [npad][nb][64]

@@ -71,6 +71,7 @@ _SIGS = {
     "mlq_hip_quant_linear": (ctypes.c_int, [_vp, _vp, ctypes.c_int, _vp, ctypes.c_int, _vp]),
     "mlq_hip_quant_linear_noalloc": (ctypes.c_int, [_vp, _vp, ctypes.c_int, _vp, _vp]),
     "mlq_hip_stream_floor": (ctypes.c_int, [ctypes.POINTER(LinearCall), ctypes.c_int, _vp, _vp]),
+    "mlq_hip_stream_probe": (ctypes.c_int, [ctypes.POINTER(LinearCall), ctypes.c_int, ctypes.c_int, _vp, _vp]),
     "mlq_hip_quant_linear_device": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, _vp, ctypes.c_size_t,
                                                     ctypes.c_int, ctypes.c_int, _vp, ctypes.c_int, _vp, _vp]),
     "mlq_hip_quant_linear_many": (ctypes.c_int, [ctypes.POINTER(LinearCall), ctypes.c_int, _vp]),
@@ -356,6 +357,15 @@ def stream_floor(arr: ctypes.Array, sink: "DeviceBuffer", stream=None) -> None:
     """mlq_hip_stream_floor: the weight stream of a fused launch of `arr`,
     without the arithmetic (a measurement of the per-launch floor)."""
     _check(load().mlq_hip_stream_floor(arr, len(arr), sink.ptr, stream))
+
+
+PROBE_EMPTY, PROBE_LOAD = 1, 2
+
+
+def stream_probe(arr: ctypes.Array, mode: int, sink: "DeviceBuffer", stream=None) -> None:
+    """mlq_hip_stream_probe: the floor's grid with no work (PROBE_EMPTY) or
+    the same weight bytes read with plain coalesced loads (PROBE_LOAD)."""
+    _check(load().mlq_hip_stream_probe(arr, len(arr), mode, sink.ptr, stream))
 
 
 def linear_fused(arr: ctypes.Array, stream=None) -> None:

@@ -326,3 +326,22 @@ def test_stream_floor_runs_and_validates(hip):
         hip.stream_floor(hip.make_calls([(qkv[0].w, x, y, 1)]), small)
     with pytest.raises(hip.MlqError, match="differs from call 0"):
         hip.stream_floor(hip.make_calls([(qkv[0].w, x, y, 1), (down.w, x, y, 1)]), sink)
+
+
+def test_stream_probe_runs_and_validates(hip):
+    """mlq_hip_stream_probe (the floor's launch alone, and its bytes read with
+    plain coalesced loads; measurements) runs on the fused group shapes and
+    refuses an unknown mode and a small sink."""
+    qkv = [Lin(hip, oracle.Q4_0, 4096, 4096, 70 + i) for i in range(3)]
+    down = Lin(hip, oracle.Q4_0, 4096, 11008, 73)
+    x = vec(hip, 4096, 74)
+    y = hip.DeviceBuffer(4 * 4096)
+    sink = hip.DeviceBuffer(4 * 65536)
+    for mode in (hip.PROBE_EMPTY, hip.PROBE_LOAD):
+        for calls in ([(l.w, x, y, 1) for l in qkv], [(down.w, x, y, 1)]):
+            hip.stream_probe(hip.make_calls(calls), mode, sink)
+    hip.synchronize()
+    with pytest.raises(hip.MlqError, match="unknown mode"):
+        hip.stream_probe(hip.make_calls([(qkv[0].w, x, y, 1)]), 3, sink)
+    with pytest.raises(hip.MlqError, match="sink"):
+        hip.stream_probe(hip.make_calls([(qkv[0].w, x, y, 1)]), hip.PROBE_LOAD, hip.DeviceBuffer(1024))
