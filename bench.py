@@ -125,13 +125,15 @@ def cpu_model():
     return f"{name} ({ids}; {cpus} logical CPUs)" if ids else name
 
 
-def cpu_sweep_check(sw: Sweep, threads: int, runs: int = 3):
+def cpu_sweep_check(sw: Sweep, threads: int, runs: int = 3, alt=None):
     """Run the reference CPU linear over the whole sweep on the same blocks and
     compare every output with the GPU's.  Timing follows the reference's own
     benchmark pattern (src/main.cpp:1226-1238): one untimed warm-up sweep, then
     `runs` timed sweeps, median reported; each sweep calls the threaded
     linear() once per weight (parallel_for over all host cores,
-    src/thread_pool.cpp:23-73)."""
+    src/thread_pool.cpp:23-73).  alt: a callable that recomputes the sweep's
+    outputs with another GPU path; its outputs are checked against the same
+    CPU results (worst_err_over_bound_alt)."""
     import oracle
 
     sys.path.insert(0, os.path.join(REPO, "tests"))
@@ -167,8 +169,15 @@ def cpu_sweep_check(sw: Sweep, threads: int, runs: int = 3):
         if name == "lm_head":
             arg_gpu, arg_cpu = int(np.argmax(yg)), orc.argmax(yc)
             top2 = np.sort(yc)[-2:]
+    worst_alt = None
+    if alt is not None:
+        alt()
+        worst_alt = 0.0
+        for (name, w, blocks, _, xv, _, yc), (_, _, _, y) in zip(prepared, sw.calls_desc):
+            worst_alt = max(worst_alt, check_close(y.download(np.float32), yc, xv, w.qtype, blocks, name))
     del prepared
     return {
+        "worst_err_over_bound_alt": worst_alt,
         "kind": kind, "cpu_s": float(np.median(times)), "cpu_s_runs": [round(t, 4) for t in times],
         "cpu_s_warmup": round(warm, 4), "cpu_bytes": cpu_bytes, "worst_err_over_bound": worst,
         "argmax_gpu": arg_gpu, "argmax_cpu": arg_cpu, "argmax_top2_gap": float(top2[1] - top2[0]),
@@ -216,6 +225,39 @@ def floor_bench(sw: Sweep, stream, steps: int, warmup: int, probe=None):
     if probe != hip.PROBE_EMPTY:
         res["gbs"] = round(sw.bytes / (ms * 1e-3) / 1e9, 1)
     return res
+
+
+def f32_sweep_bench(sw: Sweep, stream, steps: int, warmup: int):
+    """The sweep's 129 stages on the f32 GEMV (mlq_hip_quant_linear_fused_f32:
+    each weight dequantized to f32 and multiplied into an f32 sum of x, the
+    reference's arithmetic, src/quant.cpp:413-429), recorded as one graph like
+    the headline: what the integer path's speed is bought against.  Returns
+    the timing and a function that reruns the sweep once (for the margin
+    check against the CPU results)."""
+    ids = sw.stage_ids()
+    groups, i = [], 0
+    while i < len(ids):
+        j = i + 1
+        while j < len(ids) and ids[j] == ids[i]:
+            j += 1
+        groups.append(hip.make_calls([(w, x, y, 1) for (_, w, x, y) in sw.calls_desc[i:j]]))
+        i = j
+    graph = hip.Graph.record(lambda: [hip.linear_fused_f32(g, stream) for g in groups], stream, keep=groups)
+    for _ in range(warmup):
+        graph.launch(stream)
+    ms = time_region(lambda: graph.launch(stream), steps, stream) / steps
+
+    def rerun():
+        graph.launch(stream)
+        hip.synchronize(stream)
+
+    res = {"launches": len(groups), "us_per_step": round(ms * 1e3, 1),
+           "gbs": round(sw.bytes / (ms * 1e-3) / 1e9, 1),
+           "frac_of_peak": round(sw.bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+           "note": "mlq_hip_quant_linear_fused_f32 per stage (weights dequantized to f32, f32 multiply-adds "
+                   "with f32 x, as src/quant.cpp:413-429), one graph of the same 129 dependent launches as "
+                   "per_stage"}
+    return res, rerun, graph
 
 
 # ------------------------------------------------------------------ per-shape GEMV
@@ -950,6 +992,12 @@ def main():
     floor = floor_bench(sw, stream, args.steps, args.warmup)
     log(f"sweep floor (weights only, one launch per stage): {floor['us_per_step']:8.1f} us/step, "
         f"{floor['gbs']:8.1f} GB/s")
+    f32_line, f32_rerun, f32_graph = f32_sweep_bench(sw, stream, args.steps, args.warmup)
+    log(f"sweep f32 GEMV (the reference's arithmetic, one launch per stage): {f32_line['us_per_step']:8.1f} "
+        f"us/step, {f32_line['gbs']:8.1f} GB/s")
+    # The headline's outputs again for the CPU check below (the f32 sweep wrote them).
+    step()
+    hip.synchronize(stream)
     empty = floor_bench(sw, stream, args.steps, args.warmup, hip.PROBE_EMPTY)
     load_only = floor_bench(sw, stream, args.steps, args.warmup, hip.PROBE_LOAD)
     log(f"sweep launch cost (129 empty dependent launches): {empty['us_per_step']:8.1f} us/step, "
@@ -1012,7 +1060,8 @@ def main():
         import oracle
 
         threads = os.cpu_count() or 1
-        chk = cpu_sweep_check(sw, threads)
+        chk = cpu_sweep_check(sw, threads, alt=f32_rerun)
+        f32_line["worst_err_over_bound"] = round(chk["worst_err_over_bound_alt"], 6)
         cpu = {"value": round(chk["cpu_bytes"] / chk["cpu_s"] / 1e9, 3), "unit": "GB/s",
                "cores": threads, "cpu_model": cpu_model(), "kind": chk["kind"],
                "sample": f"whole sweep ({sw.n()} calls, {chk['cpu_bytes'] / 1e9:.3f} GB): one warm-up sweep "
@@ -1029,6 +1078,7 @@ def main():
         if not parity["argmax_match"]:
             raise SystemExit("argmax mismatch between GPU and CPU sweep")
 
+    f32_graph.destroy()
     out = {
         "metric": METRIC,
         "value": round(gbs, 1),
@@ -1050,6 +1100,7 @@ def main():
                    "bytes_per_step": sw.bytes, "launch": args.launch,
                    "sweep_us": round(ms_step * 1e3, 1),
                    "sweep_us_by_launch": {k: round(v * 1e3, 1) for k, v in variants.items()},
+                   "per_stage_f32_gemv": f32_line,
                    "per_stage_floor": floor, "per_stage_empty_launches": empty,
                    "per_stage_load_only": load_only},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",

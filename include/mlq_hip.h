@@ -169,6 +169,18 @@ int mlq_hip_quant_linear_many(const mlq_linear_call* calls, int n, void* stream)
  * linear per projection, src/forward.cpp:172-227).  Asynchronous on `stream`. */
 int mlq_hip_quant_linear_fused(const mlq_linear_call* calls, int n, void* stream);
 
+/* The same fused launch (one token row, an even block count) with the
+ * reference's f32 arithmetic instead of the integer block sums: each weight
+ * dequantized to f32 as quantized_linear's dequant functions do
+ * (src/quant.cpp:413-429, 435-460: d * (q - 8), d * q, d * q + m) and
+ * multiplied into an f32 sum of x; each lane sums its elements in k order
+ * with fused multiply-adds and the lanes' sums meet in a butterfly.  Slower
+ * than mlq_hip_quant_linear_fused (about three VALU operations and an LDS
+ * read of x per weight against about one), closer to the CPU's f32 sums;
+ * there for callers that want that and to price the integer path.
+ * Asynchronous on `stream`. */
+int mlq_hip_quant_linear_fused_f32(const mlq_linear_call* calls, int n, void* stream);
+
 /* Measurement, not a linear: streams exactly the weights a fused launch of
  * `calls` (as mlq_hip_quant_linear_fused; x and y are ignored) would read,
  * with the GEMV kernels' grid, work units and request ring, and no

@@ -698,7 +698,157 @@ __global__ __launch_bounds__(kWaves * 64) void probe_load_kernel(const GemvGroup
     sink[t & (kFloorSinkWords - 1)] = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
 }
 
+// f32 GEMV: the reference's arithmetic (src/quant.cpp:413-429: each weight
+// dequantized to f32, w = d * (q - 8), d * q or d * q + m, then an f32
+// multiply-add with x), for pricing the integer path against it.  Work units
+// as in the multi kernel: a wave takes row r and chunk c of 64 pairs, lane l
+// pair 64 c + l, and rows w, w + W, ...; D units' weights are requested ahead.
+// x is staged in LDS as f32 with its 16-byte slots XOR-swizzled by pair, so
+// that the 64 lanes, each reading its own pair's 64 elements, spread over the
+// banks.  Each lane sums its elements in k order with fused multiply-adds; the
+// row sum is the lanes' sums added by a butterfly.
+typedef float gf32x4 __attribute__((ext_vector_type(4)));
+
+template <int QT, int D>
+__global__ __launch_bounds__(512) void gemv_f32_kernel(const GemvGroup g, const float* __restrict__ x, int M, int K,
+                                                       int nb) {
+    constexpr int DW = Fmt<QT>::DW;
+    extern __shared__ gf32x4 xs4[];  // [np][16] slots
+    const int np = nb >> 1;
+    for (int v = threadIdx.x; v < np * 16; v += blockDim.x) {
+        const int p = v >> 4, sl = v & 15;
+        const int k0 = 64 * p + 4 * sl;
+        gf32x4 f;
+        for (int i = 0; i < 4; ++i) f[i] = k0 + i < K ? x[k0 + i] : 0.0f;
+        xs4[16 * p + (sl ^ (p & 15))] = f;
+    }
+    __syncthreads();
+    const int lane = threadIdx.x & 63;
+    const int W = gridDim.x * 8;
+    const int gw = blockIdx.x * 8 + (threadIdx.x >> 6);
+    const int nch = (np + 63) >> 6;
+    const int rows_w = gw < M ? (M - gw + W - 1) / W : 0;
+    const int nu = rows_w * nch;
+    if (nu == 0) return;
+    const size_t row_dw = static_cast<size_t>(np) * DW;
+    int pr = 0, pc = 0;  // the next unit to request (past the end: the last one again)
+    auto request = [&](uint32_t (&w)[DW]) {
+        const int row = gw + W * min(pr, rows_w - 1);
+        const int p = min(min(pc, nch - 1) * 64 + lane, np - 1);
+        const uint32_t* src = group_row(g, row, row_dw) + static_cast<size_t>(p) * DW;
+#pragma unroll
+        for (int i = 0; i < DW; ++i) w[i] = src[i];
+        if (++pc == nch) {
+            pc = 0;
+            ++pr;
+        }
+    };
+    uint32_t ring[D][DW];
+#pragma unroll
+    for (int k = 0; k < D; ++k) request(ring[k]);
+    float acc = 0.0f;
+    int cr = 0, cc = 0;  // the unit being computed
+    // One block: the 32 codes (nibbles or bytes) of qs[0..7] (dwords) with
+    // scale d (and offset m), against x slots 8h .. 8h + 7 of pair p.
+    auto block = [&](const uint32_t (&q)[8], float d, float m, int p, int h) {
+        float xv[32];
+#pragma unroll
+        for (int sl = 0; sl < 8; ++sl) {
+            const gf32x4 f = xs4[16 * p + ((8 * h + sl) ^ (p & 15))];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) xv[4 * sl + i] = f[i];
+        }
+        if (QT == 1) {
+#pragma unroll
+            for (int k = 0; k < 32; ++k) {
+                const int8_t b = static_cast<int8_t>(q[k >> 2] >> (8 * (k & 3)));
+                acc = __builtin_fmaf(d * static_cast<float>(b), xv[k], acc);
+            }
+        } else {
+            const float off = QT == 2 ? -8.0f * d : m;
+#pragma unroll
+            for (int k = 0; k < 32; ++k) {
+                const uint32_t byte = q[(k & 15) >> 2] >> (8 * (k & 3));
+                const uint32_t nib = k < 16 ? (byte & 15u) : ((byte >> 4) & 15u);
+                acc = __builtin_fmaf(__builtin_fmaf(static_cast<float>(nib), d, off), xv[k], acc);
+            }
+        }
+    };
+    auto step = [&](uint32_t (&w)[DW]) {
+        const int p = cc * 64 + lane;
+        if (p < np) {
+            uint32_t q0[8], q1[8];
+            float d0, d1, m0 = 0.0f, m1 = 0.0f;
+            if (QT == 2) {  // 9 dwords: d0 | qs0 (bytes 2..17) | d1 (bytes 18..19) | qs1 (dwords 5..8)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) q0[i] = __builtin_amdgcn_alignbit(w[i + 1], w[i], 16);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) q1[i] = w[5 + i];
+                d0 = h_lo(w[0]);
+                d1 = h_hi(w[4]);
+            } else if (QT == 1) {  // 17 dwords: d0 | qs0 (bytes 2..33) | d1 (bytes 34..35) | qs1 (dwords 9..16)
+#pragma unroll
+                for (int i = 0; i < 8; ++i) q0[i] = __builtin_amdgcn_alignbit(w[i + 1], w[i], 16);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) q1[i] = w[9 + i];
+                d0 = h_lo(w[0]);
+                d1 = h_hi(w[8]);
+            } else {  // 10 dwords: d0 m0 | qs0 (dwords 1..4) | d1 m1 | qs1 (dwords 6..9)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) q0[i] = w[1 + i], q1[i] = w[6 + i];
+                d0 = h_lo(w[0]);
+                m0 = h_hi(w[0]);
+                d1 = h_lo(w[5]);
+                m1 = h_hi(w[5]);
+            }
+            block(q0, d0, m0, p, 0);
+            block(q1, d1, m1, p, 1);
+        }
+        request(w);
+        if (++cc == nch) {
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+            if (lane == 0) {
+                const int row = gw + W * cr;
+                *group_y(g, row, M, 0) = acc;
+            }
+            acc = 0.0f;
+            cc = 0;
+            ++cr;
+        }
+    };
+    int u = 0;
+    for (; u + D <= nu; u += D) {
+#pragma unroll
+        for (int k = 0; k < D; ++k) step(ring[k]);
+    }
+#pragma unroll
+    for (int k = 0; k < D; ++k)
+        if (u + k < nu) step(ring[k]);
+}
+
 }  // namespace
+
+hipError_t launch_gemv_f32(const LinearShape& s, const GemvGroup& g, const float* x, hipStream_t stream) {
+    if (g.ncalls < 1 || g.ncalls > kGroupMaxCalls || s.rows != 1 || s.nb % 2 != 0) return hipErrorInvalidValue;
+    const size_t lds = static_cast<size_t>(s.nb / 2) * 16 * sizeof(float) * 4;
+    if (lds > 160 * 1024) return hipErrorNotSupported;
+    int grid = (s.M + 7) / 8;
+    if (grid > 2 * kPersistentWgs) grid = 2 * kPersistentWgs;
+    auto go = [&](auto kernel) {
+        if (lds > 64 * 1024 &&
+            hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                static_cast<int>(lds)) != hipSuccess)
+            return hipErrorInvalidConfiguration;
+        hipLaunchKernelGGL(kernel, dim3(grid), dim3(512), lds, stream, g, x, s.M, s.K, s.nb);
+        return hipGetLastError();
+    };
+    switch (s.qtype) {
+        case 1: return go(gemv_f32_kernel<1, 2>);
+        case 2: return go(gemv_f32_kernel<2, 3>);
+        default: return go(gemv_f32_kernel<3, 3>);
+    }
+}
 
 hipError_t launch_gemv_group(const LinearShape& s, const GemvGroup& g, const float* x, hipStream_t stream) {
     if (g.ncalls < 1 || g.ncalls > kGroupMaxCalls) return hipErrorInvalidValue;

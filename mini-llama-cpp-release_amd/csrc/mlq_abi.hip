@@ -646,8 +646,12 @@ int mlq_hip_quant_linear_many(const mlq_linear_call* calls, int n, void* stream)
     return MLQ_OK;
 }
 
-int mlq_hip_quant_linear_fused(const mlq_linear_call* calls, int n, void* stream) {
-    static const char* caller = "mlq_hip_quant_linear_fused";
+namespace {
+
+// Validates a fused call list (same x, rows, in_features and quant type;
+// outputs disjoint from x and from each other) into its GEMV group.
+int fused_group(const mlq_linear_call* calls, int n, const char* caller, mlq::GemvGroup& g, long long& rows,
+                int& device) {
     if (calls == nullptr || n <= 0) return fail(MLQ_ERR_INVALID, std::string(caller) + ": no calls");
     if (n > mlq::kGroupMaxCalls) {
         return fail(MLQ_ERR_LIMIT, std::string(caller) + ": " + std::to_string(n) + " calls (at most " +
@@ -655,11 +659,11 @@ int mlq_hip_quant_linear_fused(const mlq_linear_call* calls, int n, void* stream
     }
     if (calls[0].w == nullptr) return fail(MLQ_ERR_INVALID, std::string(caller) + ": null weight handle");
     const mlq_weight_s* w0 = calls[0].w;
-    const int device = w0->device;
+    device = w0->device;
     int rc = ensure_device(device);
     if (rc != MLQ_OK) return rc;
-    mlq::GemvGroup g{};
-    long long rows = 0;
+    g = mlq::GemvGroup{};
+    rows = 0;
     const int nrows = calls[0].rows;
     for (int i = 0; i < n; ++i) {
         const mlq_linear_call& c = calls[i];
@@ -691,6 +695,38 @@ int mlq_hip_quant_linear_fused(const mlq_linear_call* calls, int n, void* stream
         rows += c.w->M;
     }
     if (rows > (1ll << 30)) return fail(MLQ_ERR_LIMIT, std::string(caller) + ": too many rows");
+    g.ncalls = n;
+    return MLQ_OK;
+}
+
+}  // namespace
+
+int mlq_hip_quant_linear_fused_f32(const mlq_linear_call* calls, int n, void* stream) {
+    static const char* caller = "mlq_hip_quant_linear_fused_f32";
+    mlq::GemvGroup g;
+    long long rows = 0;
+    int device = 0;
+    int rc = fused_group(calls, n, caller, g, rows, device);
+    if (rc != MLQ_OK) return rc;
+    const mlq_weight_s* w0 = calls[0].w;
+    if (calls[0].rows != 1) return fail(MLQ_ERR_INVALID, std::string(caller) + ": one token row only");
+    if (w0->nb % 2 != 0) return fail(MLQ_ERR_INVALID, std::string(caller) + ": needs an even block count");
+    mlq::LinearShape shape{w0->qtype, static_cast<int>(rows), w0->K, w0->nb, 1};
+    const hipError_t e = mlq::launch_gemv_f32(shape, g, static_cast<const float*>(calls[0].x),
+                                              resolve_stream(device, stream));
+    if (e != hipSuccess) return hip_fail(e, caller);
+    return MLQ_OK;
+}
+
+int mlq_hip_quant_linear_fused(const mlq_linear_call* calls, int n, void* stream) {
+    static const char* caller = "mlq_hip_quant_linear_fused";
+    mlq::GemvGroup g;
+    long long rows = 0;
+    int device = 0;
+    int rc = fused_group(calls, n, caller, g, rows, device);
+    if (rc != MLQ_OK) return rc;
+    const mlq_weight_s* w0 = calls[0].w;
+    const int nrows = calls[0].rows;
     hipStream_t s = resolve_stream(device, stream);
     if (nrows > 1) {
         // Batched rows: one grouped GEMM launch where the shapes allow it (at

@@ -55,6 +55,9 @@ struct GemvGroup {
 };
 
 hipError_t launch_gemv_group(const LinearShape& s, const GemvGroup& g, const float* x, hipStream_t stream);
+// The same group with the reference's f32 arithmetic (each weight dequantized
+// to f32, f32 multiply-adds with x); one token row, an even block count.
+hipError_t launch_gemv_f32(const LinearShape& s, const GemvGroup& g, const float* x, hipStream_t stream);
 
 // Greedy pick fused into the GEMV (one call, rows == 1): besides y (skipped
 // when y is null) the launch writes *token = the first index of the largest

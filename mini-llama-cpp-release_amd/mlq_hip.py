@@ -71,6 +71,7 @@ _SIGS = {
     "mlq_hip_quant_linear": (ctypes.c_int, [_vp, _vp, ctypes.c_int, _vp, ctypes.c_int, _vp]),
     "mlq_hip_quant_linear_noalloc": (ctypes.c_int, [_vp, _vp, ctypes.c_int, _vp, _vp]),
     "mlq_hip_stream_floor": (ctypes.c_int, [ctypes.POINTER(LinearCall), ctypes.c_int, _vp, _vp]),
+    "mlq_hip_quant_linear_fused_f32": (ctypes.c_int, [ctypes.POINTER(LinearCall), ctypes.c_int, _vp]),
     "mlq_hip_stream_probe": (ctypes.c_int, [ctypes.POINTER(LinearCall), ctypes.c_int, ctypes.c_int, _vp, _vp]),
     "mlq_hip_quant_linear_device": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, _vp, ctypes.c_size_t,
                                                     ctypes.c_int, ctypes.c_int, _vp, ctypes.c_int, _vp, _vp]),
@@ -366,6 +367,12 @@ def stream_probe(arr: ctypes.Array, mode: int, sink: "DeviceBuffer", stream=None
     """mlq_hip_stream_probe: the floor's grid with no work (PROBE_EMPTY) or
     the same weight bytes read with plain coalesced loads (PROBE_LOAD)."""
     _check(load().mlq_hip_stream_probe(arr, len(arr), mode, sink.ptr, stream))
+
+
+def linear_fused_f32(arr: ctypes.Array, stream=None) -> None:
+    """mlq_hip_quant_linear_fused_f32: the fused decode launch with the
+    reference's f32 arithmetic (dequantized weights, f32 multiply-adds)."""
+    _check(load().mlq_hip_quant_linear_fused_f32(arr, len(arr), stream))
 
 
 def linear_fused(arr: ctypes.Array, stream=None) -> None:
