@@ -703,10 +703,13 @@ STAGE_NAMES = ("q/k/v fused 12288x4096", "o 4096x4096", "gate/up fused 22016x409
 def profile_summary(path: str, steps: int, stages: int = 129) -> None:
     """Per-stage table of a rocprofv3 CSV output directory (`-f csv`) of a
     `--no-shapes --no-cpu --no-variants --launch per_stage` run: the last
-    `steps` x `stages` dispatches of the GEMV kernels and of the stream floor
-    kernel, i.e. the timed steps of each leg (each leg runs its warm-up steps
-    before its timed ones).  A kernel trace gives durations; a counter
-    collection gives each counter's mean per dispatch.  Returns the text."""
+    `steps` x `stages` dispatches of the GEMV kernels, of the f32 GEMV, of the
+    stream floor kernel and of the two probes (empty launch, load only), i.e.
+    the timed steps of each leg (each leg runs its warm-up steps before its
+    timed ones).  A kernel trace gives durations (per step from the per-stage
+    medians, which the tracer's occasional stretched dispatch does not move,
+    and from the means); a counter collection gives each counter's mean per
+    dispatch.  Returns the text."""
     import csv
     import glob
     import statistics
@@ -717,7 +720,13 @@ def profile_summary(path: str, steps: int, stages: int = 129) -> None:
     def family(name):
         if "gemv_single" in name or "gemv_multi" in name:
             return "gemv"
-        return "floor" if "stream_floor" in name else None
+        for key, fam in (("gemv_f32", "f32"), ("stream_floor", "floor"), ("probe_empty", "empty"),
+                         ("probe_load", "load")):
+            if key in name:
+                return fam
+        return None
+
+    families = ("gemv", "f32", "floor", "load", "empty")
 
     def short(name):
         return name.replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0]
@@ -730,7 +739,7 @@ def profile_summary(path: str, steps: int, stages: int = 129) -> None:
     counters = glob.glob(os.path.join(path, "**", "*counter_collection.csv"), recursive=True)
     if trace:
         rows = sorted(csv.DictReader(open(trace[0])), key=lambda r: int(r["Start_Timestamp"]))
-        for fam in ("gemv", "floor"):
+        for fam in families:
             sel = [r for r in rows if family(r["Kernel_Name"]) == fam][-last:]
             if len(sel) < last:
                 continue
@@ -742,17 +751,20 @@ def profile_summary(path: str, steps: int, stages: int = 129) -> None:
                 key = (short(r["Kernel_Name"]), stage(i))
                 by.setdefault(key, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
             total = 0.0
+            total_med = 0.0
             for (k, st), v in by.items():
                 total += sum(v)
+                total_med += statistics.median(v) * len(v) / steps
                 out(f"| {k} | {st} | {len(v)} | {statistics.mean(v):.3f} | {statistics.median(v):.3f} | "
                       f"{min(v):.3f} | {max(v):.3f} |")
-            out(f"\nkernel time per step {total / steps:.1f} us, {total / len(sel):.3f} us per launch")
+            out(f"\nkernel time per step {total_med:.1f} us from the per-stage medians "
+                f"({total_med * steps / len(sel):.3f} us per launch); {total / steps:.1f} us from the means")
     if counters:
         per = {}
         for r in csv.DictReader(open(counters[0])):
             per.setdefault(int(r["Dispatch_Id"]), [r["Kernel_Name"], {}])[1][r["Counter_Name"]] = float(r["Counter_Value"])
         ids = sorted(per)
-        for fam in ("gemv", "floor"):
+        for fam in families:
             sel = [i for i in ids if family(per[i][0]) == fam][-last:]
             if len(sel) < last:
                 continue
@@ -861,6 +873,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline / parity leg")
     ap.add_argument("--no-shapes", action="store_true", help="skip the per-shape GEMV / GEMM tables")
     ap.add_argument("--layers", type=int, default=32)
+    ap.add_argument("--no-probes", action="store_true",
+                    help="skip the f32 GEMV, empty-launch and load-only legs (profiled runs: one of those "
+                         "graph launches ended in a host SIGSEGV under rocprofv3's kernel trace)")
     ap.add_argument("--no-variants", action="store_true",
                     help="time only the --launch mode (for profiling one mode's kernels)")
     ap.add_argument("--calibration-copy-mb", type=int, default=0,
@@ -992,17 +1007,19 @@ def main():
     floor = floor_bench(sw, stream, args.steps, args.warmup)
     log(f"sweep floor (weights only, one launch per stage): {floor['us_per_step']:8.1f} us/step, "
         f"{floor['gbs']:8.1f} GB/s")
-    f32_line, f32_rerun, f32_graph = f32_sweep_bench(sw, stream, args.steps, args.warmup)
-    log(f"sweep f32 GEMV (the reference's arithmetic, one launch per stage): {f32_line['us_per_step']:8.1f} "
-        f"us/step, {f32_line['gbs']:8.1f} GB/s")
-    # The headline's outputs again for the CPU check below (the f32 sweep wrote them).
-    step()
-    hip.synchronize(stream)
-    empty = floor_bench(sw, stream, args.steps, args.warmup, hip.PROBE_EMPTY)
-    load_only = floor_bench(sw, stream, args.steps, args.warmup, hip.PROBE_LOAD)
-    log(f"sweep launch cost (129 empty dependent launches): {empty['us_per_step']:8.1f} us/step, "
-        f"{empty['us_per_launch']:.3f} us/launch; load-only chain: {load_only['us_per_step']:8.1f} us/step, "
-        f"{load_only['gbs']:8.1f} GB/s")
+    f32_line = f32_rerun = f32_graph = empty = load_only = None
+    if not args.no_probes:
+        f32_line, f32_rerun, f32_graph = f32_sweep_bench(sw, stream, args.steps, args.warmup)
+        log(f"sweep f32 GEMV (the reference's arithmetic, one launch per stage): {f32_line['us_per_step']:8.1f} "
+            f"us/step, {f32_line['gbs']:8.1f} GB/s")
+        # The headline's outputs again for the CPU check below (the f32 sweep wrote them).
+        step()
+        hip.synchronize(stream)
+        empty = floor_bench(sw, stream, args.steps, args.warmup, hip.PROBE_EMPTY)
+        load_only = floor_bench(sw, stream, args.steps, args.warmup, hip.PROBE_LOAD)
+        log(f"sweep launch cost (129 empty dependent launches): {empty['us_per_step']:8.1f} us/step, "
+            f"{empty['us_per_launch']:.3f} us/launch; load-only chain: {load_only['us_per_step']:8.1f} us/step, "
+            f"{load_only['gbs']:8.1f} GB/s")
     seq_info = seqs["sequence"].info()
     launches = {"graph": sw.n(), "plain": sw.n(), "per_stage": seqs["per_stage"].info()["launches"],
                 "sequence": seq_info["launches"], "independent": seqs["independent"].info()["launches"],
@@ -1061,7 +1078,8 @@ def main():
 
         threads = os.cpu_count() or 1
         chk = cpu_sweep_check(sw, threads, alt=f32_rerun)
-        f32_line["worst_err_over_bound"] = round(chk["worst_err_over_bound_alt"], 6)
+        if f32_line is not None:
+            f32_line["worst_err_over_bound"] = round(chk["worst_err_over_bound_alt"], 6)
         cpu = {"value": round(chk["cpu_bytes"] / chk["cpu_s"] / 1e9, 3), "unit": "GB/s",
                "cores": threads, "cpu_model": cpu_model(), "kind": chk["kind"],
                "sample": f"whole sweep ({sw.n()} calls, {chk['cpu_bytes'] / 1e9:.3f} GB): one warm-up sweep "
@@ -1078,7 +1096,8 @@ def main():
         if not parity["argmax_match"]:
             raise SystemExit("argmax mismatch between GPU and CPU sweep")
 
-    f32_graph.destroy()
+    if f32_graph is not None:
+        f32_graph.destroy()
     out = {
         "metric": METRIC,
         "value": round(gbs, 1),
