@@ -566,6 +566,12 @@ struct ChunkArgs {
     float* y1;
     float* y2;
     int M1, M2, tile1, tile2;
+    // XCD-blocked tile order (one K split, grid a multiple of 8; xcd_br = 0: off):
+    // workgroup i runs on XCD i % 8, which owns the block of xcd_br-th of the row
+    // tiles x (8 / xcd_br)-th of the token tiles; inside it the row tiles vary
+    // fastest (token tiles if xcd_row_outer), so the block's x (or its weights)
+    // stays in that XCD's L2 while the other operand streams.
+    int xcd_br, xcd_row_outer;
 };
 
 template <int QT, int RW, int TT, int P, bool XS>
@@ -588,7 +594,16 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_chunk_kernel(const ChunkArg
     const int g = lane >> 4;
     const int wg = blockIdx.x;
     const int split = wg % a.splits;
-    const int tile = wg / a.splits;
+    int tile = wg / a.splits;
+    if (a.xcd_br > 0) {
+        const int tok_tiles = a.npad / BN;
+        const int bt_n = 8 / a.xcd_br;
+        const int rows_b = a.row_tiles / a.xcd_br, toks_b = tok_tiles / bt_n;
+        const int xcd = wg % 8, j = wg / 8;
+        const int rl = a.xcd_row_outer ? j / toks_b : j % rows_b;
+        const int tl = a.xcd_row_outer ? j % toks_b : j / rows_b;
+        tile = ((xcd % bt_n) * toks_b + tl) * a.row_tiles + (xcd / bt_n) * rows_b + rl;
+    }
     const int rt = tile % a.row_tiles;
     const int gi = (rt >= a.tile1 ? 1 : 0) + (rt >= a.tile2 ? 1 : 0);  // this tile's weight of the group
     const uint8_t* const Wg = gi == 0 ? a.W : gi == 1 ? a.W1 : a.W2;
@@ -1177,6 +1192,24 @@ hipError_t launch_chunk_t(const LinearShape& s, const ChunkCfg& c, const void* w
     a.y1 = a.y2 = nullptr;
     a.M1 = a.M2 = 0;
     a.tile1 = a.tile2 = c.row_tiles;
+    a.xcd_br = 0;
+    a.xcd_row_outer = 0;
+    // One K split: block the tiles by XCD (4096 x 4096 Q4_0 at 512 tokens: fabric reads
+    // 76.8 -> 52.7 MB per call, the time unchanged within 1 %).
+    if (c.splits == 1 && (c.row_tiles * c.tok_tiles) % 8 == 0) {
+        for (int br : {4, 2, 8, 1}) {
+            const int bt = 8 / br;
+            if (c.row_tiles % br == 0 && c.tok_tiles % bt == 0) {
+                a.xcd_br = br;
+                // Keep the smaller operand of the block resident: its weights (rows x K)
+                // or its x (tokens x K, split: 4 bytes per element).
+                const double wb = static_cast<double>(c.row_tiles / br) * 64 * RW * s.nb * block_bytes(s.qtype);
+                const double xb = static_cast<double>(c.tok_tiles / bt) * 16 * TT * s.K * 4.0;
+                a.xcd_row_outer = wb > xb ? 1 : 0;
+                break;
+            }
+        }
+    }
     if (grp != nullptr) {
         const int bm = 64 * RW;
         a.W = static_cast<const uint8_t*>(grp->w[0]);
