@@ -73,6 +73,8 @@ KERNEL_BY_LAUNCH = {
     "independent": "gemv_sequence (persistent, no barriers)",
     "pipelined": "gemv_chain (persistent, grid barriers between stages; weight ring across barriers, control wave "
                  "per workgroup for stores, arrival and x)",
+    "lds_ring": "gemv_ring (persistent, grid barriers between stages; loader waves stream every stage's weights "
+                "into an LDS ring per CU, compute waves stage x and take the weights from the ring)",
 }
 
 
@@ -868,7 +870,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--launch", choices=["graph", "plain", "sequence", "per_stage", "independent", "pipelined"],
+    ap.add_argument("--launch", choices=["graph", "plain", "sequence", "per_stage", "independent", "pipelined", "lds_ring"],
                     default="per_stage")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline / parity leg")
     ap.add_argument("--no-shapes", action="store_true", help="skip the per-shape GEMV / GEMM tables")
@@ -969,7 +971,8 @@ def main():
     #              all fresh, so nothing depends on anything; reported, not headline).
     seqs = {m: hip.Sequence(sw.calls, sw.stage_ids(), mode)
             for m, mode in (("sequence", hip.SEQ_PERSISTENT), ("per_stage", hip.SEQ_PER_STAGE),
-                            ("independent", hip.SEQ_INDEPENDENT), ("pipelined", hip.SEQ_PIPELINED))}
+                            ("independent", hip.SEQ_INDEPENDENT), ("pipelined", hip.SEQ_PIPELINED),
+                            ("lds_ring", hip.SEQ_LDS_RING))}
     graph = hip.Graph(sw.calls, stream)
     stage_graph = hip.Graph(sequence=seqs["per_stage"])
     steps_by_mode = {
@@ -979,6 +982,7 @@ def main():
         "per_stage": lambda: stage_graph.launch(stream),
         "independent": lambda: seqs["independent"].launch(stream),
         "pipelined": lambda: seqs["pipelined"].launch(stream),
+        "lds_ring": lambda: seqs["lds_ring"].launch(stream),
     }
     variants = {}
     for name, fn in steps_by_mode.items():
@@ -1023,7 +1027,8 @@ def main():
     seq_info = seqs["sequence"].info()
     launches = {"graph": sw.n(), "plain": sw.n(), "per_stage": seqs["per_stage"].info()["launches"],
                 "sequence": seq_info["launches"], "independent": seqs["independent"].info()["launches"],
-                "pipelined": seqs["pipelined"].info()["launches"]}[args.launch]
+                "pipelined": seqs["pipelined"].info()["launches"],
+                "lds_ring": seqs["lds_ring"].info()["launches"]}[args.launch]
     log(f"sweep: {ms_step * 1e3:.1f} us/step, {gbs:.1f} GB/s ({args.launch}); sequence {seq_info}")
 
     shapes = []

@@ -295,6 +295,15 @@ int mlq_hip_graph_end(int device, void* stream, mlq_graph_t* out);
  *                        synchronizes the grid and loads the next x while the
  *                        compute waves' next-stage weights are in flight.
  *                        Every call needs in_features % 32 == 0.
+ *   MLQ_SEQ_LDS_RING     the semantics of MLQ_SEQ_PERSISTENT in one launch
+ *                        whose weight stream does not wait for x: per CU,
+ *                        loader waves copy the weights of every stage, in
+ *                        order, into a ring in LDS as far ahead as the ring
+ *                        holds, and compute waves take them from there once
+ *                        the stage's x is staged.  Every call needs rows
+ *                        that a single launch sums in 64-lane groups (e.g.
+ *                        in_features 4096 and 11008; not 896 or 1024) and a
+ *                        weight under 2 GiB.
  * The sequence keeps the pointers (buffers must outlive it and any graph
  * captured from it); launches of one sequence must not overlap in time. */
 typedef struct mlq_sequence_s* mlq_sequence_t;
@@ -302,6 +311,7 @@ typedef struct mlq_sequence_s* mlq_sequence_t;
 #define MLQ_SEQ_PER_STAGE 1
 #define MLQ_SEQ_INDEPENDENT 2
 #define MLQ_SEQ_PIPELINED 3
+#define MLQ_SEQ_LDS_RING 4
 int mlq_hip_sequence_create(const mlq_linear_call* calls, int n, const int* stage, int mode,
                             mlq_sequence_t* out);
 int mlq_hip_sequence_launch(mlq_sequence_t seq, void* stream);

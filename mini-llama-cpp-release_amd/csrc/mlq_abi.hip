@@ -1294,7 +1294,7 @@ int mlq_hip_sequence_create(const mlq_linear_call* calls, int n, const int* stag
     *out = nullptr;
     if (calls == nullptr || n <= 0) return fail(MLQ_ERR_INVALID, std::string(caller) + ": no calls");
     if (mode != MLQ_SEQ_PERSISTENT && mode != MLQ_SEQ_PER_STAGE && mode != MLQ_SEQ_INDEPENDENT &&
-        mode != MLQ_SEQ_PIPELINED) {
+        mode != MLQ_SEQ_PIPELINED && mode != MLQ_SEQ_LDS_RING) {
         return fail(MLQ_ERR_INVALID, std::string(caller) + ": unknown mode " + std::to_string(mode));
     }
     if (calls[0].w == nullptr) return fail(MLQ_ERR_INVALID, std::string(caller) + ": null weight handle");
@@ -1320,6 +1320,16 @@ int mlq_hip_sequence_create(const mlq_linear_call* calls, int n, const int* stag
         if (mode == MLQ_SEQ_PIPELINED && c.w->K % mlq::kQK != 0) {
             return fail(MLQ_ERR_LIMIT, at + ": in_features=" + std::to_string(c.w->K) +
                                            "; MLQ_SEQ_PIPELINED needs in_features % 32 == 0");
+        }
+        if (mode == MLQ_SEQ_LDS_RING) {
+            if (mlq::sequence_lpr(c.w->K) != 64) {
+                return fail(MLQ_ERR_LIMIT, at + ": in_features=" + std::to_string(c.w->K) +
+                                               "; MLQ_SEQ_LDS_RING needs rows summed in 64-lane groups");
+            }
+            if (c.w->n_blocks * static_cast<size_t>(mlq::block_bytes(c.w->qtype)) >= (static_cast<size_t>(1) << 31)) {
+                return fail(MLQ_ERR_LIMIT, at + ": weight of 2 GiB or more; MLQ_SEQ_LDS_RING addresses a weight "
+                                               "with 31-bit offsets");
+            }
         }
         const char* lin = caller_for(c.w->qtype);
         const size_t xb = static_cast<size_t>(c.w->K) * sizeof(float);
@@ -1437,16 +1447,19 @@ int mlq_hip_sequence_create(const mlq_linear_call* calls, int n, const int* stag
             last.nstages += 1;
             last.lds_bytes = std::max(last.lds_bytes, lds);
             last.kmax = std::max(last.kmax, w0->K);
-            descs[s].barrier = mode == MLQ_SEQ_PERSISTENT || mode == MLQ_SEQ_PIPELINED ? 1 : 0;
+            descs[s].barrier = mode == MLQ_SEQ_PERSISTENT || mode == MLQ_SEQ_PIPELINED || mode == MLQ_SEQ_LDS_RING ? 1 : 0;
         } else {
             seq->segs.push_back(mlq_sequence_s::Segment{w0->qtype, lpr, s, 1, lds, 0, w0->K});
             descs[s].barrier = 0;
         }
     }
     for (auto& g : seq->segs) {
+        int nslots = 0;
         if (mode == MLQ_SEQ_PIPELINED) g.lds_bytes = mlq::chain_lds_bytes(g.qtype, g.kmax);
-        hipError_t e = mode == MLQ_SEQ_PIPELINED ? mlq::chain_grid(g.qtype, g.lpr, g.lds_bytes, device, &g.grid)
-                                                 : mlq::sequence_grid(g.qtype, g.lpr, g.lds_bytes, device, &g.grid);
+        if (mode == MLQ_SEQ_LDS_RING) g.lds_bytes = mlq::ring_lds_bytes(g.qtype, g.kmax, &nslots);
+        hipError_t e = mode == MLQ_SEQ_PIPELINED  ? mlq::chain_grid(g.qtype, g.lpr, g.lds_bytes, device, &g.grid)
+                       : mode == MLQ_SEQ_LDS_RING ? mlq::ring_grid(g.qtype, g.lds_bytes, device, &g.grid)
+                                                  : mlq::sequence_grid(g.qtype, g.lpr, g.lds_bytes, device, &g.grid);
         if (e != hipSuccess) {
             delete seq;
             return hip_fail(e, "sequence occupancy");
@@ -1455,7 +1468,7 @@ int mlq_hip_sequence_create(const mlq_linear_call* calls, int n, const int* stag
             // A stage reads x coherently when an earlier stage of the same
             // launch writes where it reads.
             descs[k].coherent = 0;
-            if (mode == MLQ_SEQ_PERSISTENT || mode == MLQ_SEQ_PIPELINED) {
+            if (mode == MLQ_SEQ_PERSISTENT || mode == MLQ_SEQ_PIPELINED || mode == MLQ_SEQ_LDS_RING) {
                 for (int e2 = g.stage_begin; e2 < k; ++e2)
                     for (int c = stage_first[e2]; c < stage_first[e2] + descs[e2].ncalls; ++c)
                         if (overlaps(yr[c], xr[stage_first[k]])) descs[k].coherent = 1;
@@ -1501,6 +1514,12 @@ int mlq_hip_sequence_launch(mlq_sequence_t seq, void* stream) {
             hipError_t e = mlq::launch_chain(g.qtype, g.lpr, table + g.stage_begin, g.nstages, syncs + i, g.grid,
                                              g.lds_bytes, seq->spin_limit, g.kmax, sink, s);
             if (e != hipSuccess) return hip_fail(e, mlq::chain_kernel_name(g.qtype, g.lpr));
+            continue;
+        }
+        if (seq->mode == MLQ_SEQ_LDS_RING) {
+            hipError_t e = mlq::launch_ring(g.qtype, table + g.stage_begin, g.nstages, syncs + i, g.grid, g.lds_bytes,
+                                            seq->spin_limit, g.kmax, s);
+            if (e != hipSuccess) return hip_fail(e, mlq::ring_kernel_name(g.qtype));
             continue;
         }
         hipError_t e = mlq::launch_sequence(g.qtype, g.lpr, table + g.stage_begin, g.nstages, syncs + i, g.grid,

@@ -202,6 +202,15 @@ hipError_t launch_chain(int qtype, int lpr, const SeqStageDesc* stages, int nsta
 size_t chain_sink_bytes();  // device words a launch's compute lanes store dropped values to
 const char* chain_kernel_name(int qtype, int lpr);
 
+// LDS-ring chain kernel (ring.hip): the same stage descriptors, stages whose
+// lane-group width is 64; kmax = largest K of the launch.  ring_lds_bytes
+// gives the launch's LDS and its ring slots.
+int ring_lds_bytes(int qtype, int kmax, int* nslots);
+hipError_t ring_grid(int qtype, int lds_bytes, int device, int* grid);
+hipError_t launch_ring(int qtype, const SeqStageDesc* stages, int nstages, SeqSync* sync, int grid, int lds_bytes,
+                       unsigned spin_limit, int kmax, hipStream_t stream);
+const char* ring_kernel_name(int qtype);
+
 // Device forward ops (ops.hip) behind the op-by-op device interfaces of the
 // reference (include/mini_llama/cuda_ops.h, cuda_attention.h, cuda_matmul.h).
 constexpr int kOpSilu = 0;

@@ -23,7 +23,7 @@ F32, Q8_0, Q4_0, Q4_1 = 0, 1, 2, 3
 BLOCK_BYTES = {Q8_0: 34, Q4_0: 18, Q4_1: 20}
 QK = 32
 X_ON_DEVICE, Y_ON_DEVICE, ASYNC = 1, 2, 4
-SEQ_PERSISTENT, SEQ_PER_STAGE, SEQ_INDEPENDENT, SEQ_PIPELINED = 0, 1, 2, 3
+SEQ_PERSISTENT, SEQ_PER_STAGE, SEQ_INDEPENDENT, SEQ_PIPELINED, SEQ_LDS_RING = 0, 1, 2, 3, 4
 
 _vp = ctypes.c_void_p
 

@@ -3,9 +3,10 @@
 A sequence runs a chain of GEMVs in one launch with device-wide barriers
 between stages.  Per call its outputs must equal one mlq_hip_quant_linear
 launch per call bit for bit (same lane-group width, same summation order), in
-all three modes, for chained calls whose x is an earlier call's y (what the
-barriers are for), for fused stages (q/k/v, gate/up) and across graph replays
-with eager work in between.  One chain is also checked against the CPU oracle
+every mode (persistent, per-stage, independent, pipelined, LDS ring), for
+chained calls whose x is an earlier call's y (what the barriers are for), for
+fused stages (q/k/v, gate/up) and across graph replays with eager work in
+between.  One chain is also checked against the CPU oracle
 to the parity bound, and the host-side validation and the bounded barrier wait
 are exercised.
 """
@@ -97,7 +98,7 @@ def test_chain_matches_per_call_launches(hip, fmt):
     want = snapshot(outs)
     for b in outs:
         b.fill(0)
-    for mode in (hip.SEQ_PERSISTENT, hip.SEQ_PER_STAGE, hip.SEQ_PIPELINED):
+    for mode in (hip.SEQ_PERSISTENT, hip.SEQ_PER_STAGE, hip.SEQ_PIPELINED, hip.SEQ_LDS_RING):
         say(f"sequence chain {fmt} mode={mode}")
         seq = run_sequence(hip, calls, stages, mode)
         got = snapshot(outs)
@@ -110,7 +111,8 @@ def test_chain_matches_per_call_launches(hip, fmt):
             b.fill(0)
 
 
-def test_chain_against_oracle(hip, orc):
+@pytest.mark.parametrize("mode", ["persistent", "lds_ring"])
+def test_chain_against_oracle(hip, orc, mode):
     """A dependent Q4_0 chain 4096 -> 11008 -> 4096 checked call by call against
     the CPU oracle on the inputs each call actually saw."""
     qt = oracle.Q4_0
@@ -118,8 +120,8 @@ def test_chain_against_oracle(hip, orc):
     x = vec(hip, 4096, 8)
     y1, y2, y3 = hip.DeviceBuffer(4 * 11008), hip.DeviceBuffer(4 * 4096), hip.DeviceBuffer(4 * 4096)
     calls = [(l1, x, y1), (l2, y1, y2), (l3, y2, y3)]
-    say("sequence chain vs oracle")
-    run_sequence(hip, calls, None, hip.SEQ_PERSISTENT)
+    say(f"sequence chain vs oracle ({mode})")
+    run_sequence(hip, calls, None, hip.SEQ_PERSISTENT if mode == "persistent" else hip.SEQ_LDS_RING)
     ins = [x.download(np.float32), y1.download(np.float32), y2.download(np.float32)]
     for (lin, _, yb), xin in zip(calls, ins):
         blocks = lin.blocks()
@@ -132,7 +134,8 @@ def test_chain_against_oracle(hip, orc):
                          ids=lambda s: f"{s[0]}x{s[1]}")
 def test_independent_shapes_all_modes(hip, shape):
     """Every lane-group width (16 / 32 / 64), ragged row counts, a 4-call stage
-    and the largest supported K, in all three modes, against per-call launches."""
+    and the largest supported K, in every mode (the LDS-ring mode where the
+    rows are summed in 64-lane groups), against per-call launches."""
     m, k = shape
     for fmt, qt in FMTS.items():
         lins = [Lin(hip, qt, m + 3 * i, k, 40 + i) for i in range(4)]
@@ -141,7 +144,10 @@ def test_independent_shapes_all_modes(hip, shape):
         calls = [(lins[i], x, outs[i]) for i in range(4)]
         per_call(hip, calls)
         want = snapshot(outs)
-        for mode in (hip.SEQ_PERSISTENT, hip.SEQ_PER_STAGE, hip.SEQ_INDEPENDENT, hip.SEQ_PIPELINED):
+        modes = [hip.SEQ_PERSISTENT, hip.SEQ_PER_STAGE, hip.SEQ_INDEPENDENT, hip.SEQ_PIPELINED]
+        if k in (2048, 3072, 15360):
+            modes.append(hip.SEQ_LDS_RING)
+        for mode in modes:
             for stages in ([0, 0, 0, 0], [0, 1, 1, 2], None):
                 for b in outs:
                     b.fill(0)
@@ -171,14 +177,17 @@ def test_mixed_formats_split_launches(hip):
         assert np.array_equal(g.view(np.uint32), w.view(np.uint32)), f"call {i}"
 
 
-@pytest.mark.parametrize("mode", ["persistent", "pipelined"])
+SEQ_MODES = {"persistent": "SEQ_PERSISTENT", "pipelined": "SEQ_PIPELINED", "lds_ring": "SEQ_LDS_RING"}
+
+
+@pytest.mark.parametrize("mode", list(SEQ_MODES))
 def test_graph_replays(hip, mode):
     """A captured sequence replayed with new x contents and eager work between
     replays: every replay equals per-call launches on the same x."""
     calls, stages, outs, keep = llama_layer(hip, oracle.Q4_0, seed=21)
     x = keep[-1]
     arr = hip.make_calls([(w.w, xx, y, 1) for w, xx, y in calls])
-    seq = hip.Sequence(arr, stages, hip.SEQ_PERSISTENT if mode == "persistent" else hip.SEQ_PIPELINED)
+    seq = hip.Sequence(arr, stages, getattr(hip, SEQ_MODES[mode]))
     g = hip.Graph(sequence=seq)
     scratch = hip.DeviceBuffer(4 * 4096)
     for rep in range(4):
@@ -233,11 +242,13 @@ def test_validation_messages(hip):
     with pytest.raises(hip.MlqError, match="MLQ_SEQ_PIPELINED needs in_features % 32 == 0"):
         create([(k40.w, x, y, 1)], None, hip.SEQ_PIPELINED)
     create([(k40.w, x, y, 1)], None, hip.SEQ_PERSISTENT).destroy()
+    with pytest.raises(hip.MlqError, match="MLQ_SEQ_LDS_RING needs rows summed in 64-lane groups"):
+        create([(l2.w, x, y, 1)], None, hip.SEQ_LDS_RING)
     # a dependent chain is fine in the barrier modes
     create([(l1.w, x, y, 1), (l64.w, y, y2, 1)]).destroy()
 
 
-@pytest.mark.parametrize("mode", ["persistent", "pipelined"])
+@pytest.mark.parametrize("mode", list(SEQ_MODES))
 def test_barrier_wait_bound_recovers(hip, mode):
     """With a one-poll bound the barrier waits give up instead of spinning; the
     launch still ends, the status reports it, and the next launch with the
@@ -246,7 +257,7 @@ def test_barrier_wait_bound_recovers(hip, mode):
     per_call(hip, calls)
     want = snapshot(outs)
     arr = hip.make_calls([(w.w, x, y, 1) for w, x, y in calls])
-    seq = hip.Sequence(arr, stages, hip.SEQ_PERSISTENT if mode == "persistent" else hip.SEQ_PIPELINED)
+    seq = hip.Sequence(arr, stages, getattr(hip, SEQ_MODES[mode]))
     seq.set_spin_limit(1)
     say("sequence with a one-poll barrier bound")
     seq.launch()
