@@ -853,6 +853,57 @@ def calibration_copy(mb: int, stream) -> None:
     dst.free()
 
 
+def ring_stamps_report(layers: int, steps: int, warmup: int, stream) -> str:
+    """Per-stage boundary timestamps of the LDS-ring persistent chain on the
+    sweep (the measurement build's s_memrealtime stamps, 100 MHz), as markdown:
+    per stage kind, the median over the timed launches and layers 1 .. L-1 of
+    each interval, for the three stamped workgroups."""
+    sw = Sweep(layers=layers)
+    seq = hip.Sequence(sw.calls, sw.stage_ids(), hip.SEQ_LDS_RING)
+    for _ in range(warmup):
+        seq.launch(stream)
+    hip.synchronize(stream)
+    runs, walls = [], []
+    for _ in range(steps):
+        seq.launch(stream)
+        hip.synchronize(stream)
+        runs.append(hip.ring_stamps().astype(np.int64))
+    if seq.status() != 0:
+        raise SystemExit("ring stamps: a barrier or ring wait timed out")
+    nst = len(set(sw.stage_ids()))
+    kinds = ["q/k/v", "o", "gate/up", "down"]
+    cols = [("y stores complete", 0, 1), ("all compute waves done", 1, 2), ("grid barrier", 2, 3),
+            ("x staged", 3, 4), ("all x staged", 4, 5), ("to first unit", 5, 6), ("first unit's wait", 6, 7)]
+    out = [f"LDS-ring persistent chain on the sweep ({layers} layers, {nst} stages): {steps} timed launches after "
+           f"{warmup} warm-up; µs, medians over launches and layers 1..{layers - 1}; loader times relative to "
+           "the stage's entry (negative: before it)\n"]
+    for wi, wname in enumerate(["0", "G/2 + 1", "G - 1"]):
+        per = {k: {} for k in kinds}
+        for st in runs:
+            a = st[wi]
+            walls.append((a[nst - 1, 8:20].max() - a[0, 0]) / 100.0)
+            for s in range(4, min(nst - 1, 4 * layers)):
+                d = per[kinds[s % 4]]
+                e = a[s]
+                for name, i0, i1 in cols:
+                    d.setdefault(name, []).append((e[i1] - e[i0]) / 100.0)
+                d.setdefault("rows (first unit to last wave done)", []).append((e[8:20].max() - e[7]) / 100.0)
+                d.setdefault("stage (entry to next entry)", []).append((a[s + 1, 0] - e[0]) / 100.0)
+                d.setdefault("loader: first unit requested", []).append((e[22] - e[0]) / 100.0)
+                d.setdefault("loader: first unit in LDS", []).append((e[20] - e[0]) / 100.0)
+                d.setdefault("loader: last unit in LDS", []).append((e[21] - e[0]) / 100.0)
+        names = list(per[kinds[0]].keys())
+        out.append(f"\nworkgroup {wname}: stage 0 entry to the last stage's end "
+                   f"{np.median(walls[-len(runs):]):.1f} µs (median over launches)\n")
+        out.append("| interval | " + " | ".join(kinds) + " |")
+        out.append("|---|" + "---|" * len(kinds))
+        for n in names:
+            out.append(f"| {n} | " + " | ".join(f"{np.median(per[k][n]):.2f}" for k in kinds) + " |")
+    seq.destroy()
+    sw.free()
+    return "\n".join(out) + "\n"
+
+
 def emit(obj):
     """Writes the one JSON line to the process's original stdout.  main()
     points fd 1 at stderr first: C code loaded here (the reference's GGUF
@@ -899,6 +950,10 @@ def main():
     ap.add_argument("--profile-summary", default="",
                     help="print per-stage tables of this rocprofv3 CSV output directory (of a --launch "
                          "per_stage --no-variants run with the same --steps) and exit; no GPU use")
+    ap.add_argument("--ring-stamps", action="store_true",
+                    help="load the measurement build (libmlq_hip_stamps.so: make -C mini-llama-cpp-release_amd "
+                         "stamps), run the sweep in the lds_ring mode --steps times after --warmup and print "
+                         "its per-stage boundary timestamps as tables")
     ap.add_argument("--kernel-summary", default="",
                     help="print per-kernel tables (GEMM and x split) of this rocprofv3 CSV output "
                          "directory (of a --gemm-only run) and exit; no GPU use")
@@ -908,6 +963,11 @@ def main():
         return
     if args.kernel_summary:
         os.write(_JSON_FD, kernel_summary(args.kernel_summary).encode())
+        return
+    if args.ring_stamps:
+        hip.load(hip.STAMPS_LIB_PATH)
+        hip.init(0)
+        os.write(_JSON_FD, ring_stamps_report(args.layers, args.steps, args.warmup, hip.stream(0)).encode())
         return
     if args.gemm_only:
         hip.load()

@@ -314,6 +314,20 @@ typedef struct mlq_sequence_s* mlq_sequence_t;
 #define MLQ_SEQ_LDS_RING 4
 int mlq_hip_sequence_create(const mlq_linear_call* calls, int n, const int* stage, int mode,
                             mlq_sequence_t* out);
+/* Measurement, not part of the linear: the last MLQ_SEQ_LDS_RING launch's
+ * boundary timestamps, from a library built with `make stamps`
+ * (libmlq_hip_stamps.so; MLQ_ERR_NOT_BUILT from the normal build).  `host`
+ * receives 3 x 256 x 24 uint64 s_memrealtime values (100 MHz): for
+ * workgroups 0, G/2 + 1 and G - 1 (G = the launch's grid), per stage (the
+ * first 256), slots 0 stage entered by the first compute wave, 1 its y stores
+ * complete, 2 every compute wave done, 3 grid barrier passed (barrier stages),
+ * 4 x staged, 5 every compute wave's x staged, 6/7 before / after the wait for
+ * its first unit, 8 + w compute wave w done with the stage's rows (w < 12),
+ * 20 / 21 / 22 loader 0's first unit of the stage in LDS / its last unit in
+ * LDS / its first unit of the stage requested.  No counterpart in the
+ * reference. */
+#define MLQ_RING_STAMP_WORDS (3 * 256 * 24)
+int mlq_hip_ring_stamps(uint64_t* host, size_t words);
 int mlq_hip_sequence_launch(mlq_sequence_t seq, void* stream);
 /* After the launch's stream has been synchronized: the number of launches
  * whose device-wide barrier wait gave up (outputs void), then cleared. */

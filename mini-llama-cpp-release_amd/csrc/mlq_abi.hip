@@ -1493,6 +1493,24 @@ int mlq_hip_sequence_create(const mlq_linear_call* calls, int n, const int* stag
     return MLQ_OK;
 }
 
+int mlq_hip_ring_stamps(uint64_t* host, size_t words) {
+    static const char* caller = "mlq_hip_ring_stamps";
+    if (host == nullptr) return fail(MLQ_ERR_INVALID, std::string(caller) + ": null output");
+    if (words != MLQ_RING_STAMP_WORDS) {
+        return fail(MLQ_ERR_INVALID, std::string(caller) + ": words=" + std::to_string(words) + ", expected " +
+                                         std::to_string(MLQ_RING_STAMP_WORDS));
+    }
+    static_assert(MLQ_RING_STAMP_WORDS == mlq::kRingStampWgs * mlq::kRingStampStages * mlq::kRingStampSlots,
+                  "stamp layout");
+    hipError_t e = mlq::ring_stamps_copy(host, words * sizeof(uint64_t));
+    if (e == hipErrorNotSupported) {
+        return fail(MLQ_ERR_NOT_BUILT, std::string(caller) + ": the library was built without the timestamps "
+                                                             "(make stamps builds libmlq_hip_stamps.so)");
+    }
+    if (e != hipSuccess) return hip_fail(e, caller);
+    return MLQ_OK;
+}
+
 int mlq_hip_sequence_launch(mlq_sequence_t seq, void* stream) {
     if (seq == nullptr) return fail(MLQ_ERR_INVALID, "mlq_hip_sequence_launch: null sequence");
     int rc = ensure_device(seq->device);

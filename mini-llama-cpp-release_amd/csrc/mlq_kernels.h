@@ -210,6 +210,14 @@ hipError_t ring_grid(int qtype, int lds_bytes, int device, int* grid);
 hipError_t launch_ring(int qtype, const SeqStageDesc* stages, int nstages, SeqSync* sync, int grid, int lds_bytes,
                        unsigned spin_limit, int kmax, hipStream_t stream);
 const char* ring_kernel_name(int qtype);
+// Boundary timestamps of the measurement build (MLQ_RING_STAMPS): per
+// workgroup 0, G/2 + 1 and G - 1, per stage, kRingStampSlots s_memrealtime
+// values (slot meanings in include/mlq_hip.h).  hipErrorNotSupported in a
+// normal build.
+constexpr int kRingStampWgs = 3;
+constexpr int kRingStampStages = 256;
+constexpr int kRingStampSlots = 24;
+hipError_t ring_stamps_copy(void* host, size_t bytes);
 
 // Device forward ops (ops.hip) behind the op-by-op device interfaces of the
 // reference (include/mini_llama/cuda_ops.h, cuda_attention.h, cuda_matmul.h).

@@ -75,6 +75,23 @@ struct RingCtl {
 };
 static_assert(sizeof(RingCtl) <= kRingCtlBytes, "control words fit their LDS");
 
+#ifdef MLQ_RING_STAMPS
+// Measurement build (`make stamps`): s_memrealtime stamps (100 MHz) of three
+// workgroups at the points of each stage boundary, read back with
+// mlq_hip_ring_stamps.  The stamps add stores and change no work.
+__device__ unsigned long long g_ring_stamps[kRingStampWgs * kRingStampStages * kRingStampSlots];
+#define RING_STAMP(stage, j)                                                                                    \
+    do {                                                                                                        \
+        if (stamp_wg >= 0 && (stage) < kRingStampStages && lane == 0)                                          \
+            g_ring_stamps[(stamp_wg * kRingStampStages + (stage)) * kRingStampSlots + (j)] =                  \
+                __builtin_amdgcn_s_memrealtime();                                                               \
+    } while (0)
+#else
+#define RING_STAMP(stage, j) \
+    do {                     \
+    } while (0)
+#endif
+
 // Stage descriptors through the constant address space: scalar loads.
 typedef __attribute__((address_space(4))) const SeqStageDesc RDesc;
 typedef uint32_t ru4 __attribute__((ext_vector_type(4)));
@@ -224,6 +241,9 @@ __global__ __launch_bounds__(kRingThreads, 1) void gemv_ring_kernel(const SeqSta
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int lane = threadIdx.x & 63;
     const int b = blockIdx.x, G = gridDim.x;
+#ifdef MLQ_RING_STAMPS
+    const int stamp_wg = b == 0 ? 0 : b == G / 2 + 1 ? 1 : b == G - 1 ? 2 : -1;
+#endif
 
     for (int k = threadIdx.x; k < kRingMaxSlots; k += kRingThreads) {
         ctl.ready[k] = 0;
@@ -249,8 +269,22 @@ __global__ __launch_bounds__(kRingThreads, 1) void gemv_ring_kernel(const SeqSta
         cur.enter(st, nstages, b, G, lw);
         ru4 reg[R][F::KL];
         int nbytes[R];
+#ifdef MLQ_RING_STAMPS
+        int nstg[R];  // stage of each register set's unit
+        int last_issued = -1, last_written = -1;
+        auto stamp_issue = [&](int r) {
+            nstg[r] = cur.s;
+            if (lw == 0 && cur.s != last_issued) {
+                RING_STAMP(cur.s, 22);  // first unit of the stage requested
+                last_issued = cur.s;
+            }
+        };
+#else
+        auto stamp_issue = [](int) {};
+#endif
 #pragma unroll
         for (int r = 0; r < R; ++r) {
+            stamp_issue(r);
             nbytes[r] = cur.issue(nstages, lane, reg[r]);
             cur.next(st, nstages, b, G, lw);
         }
@@ -278,6 +312,14 @@ __global__ __launch_bounds__(kRingThreads, 1) void gemv_ring_kernel(const SeqSta
                     if (1024 * j + 16 * lane < nbytes[r]) *reinterpret_cast<ru4*>(dst + 1024 * j + 16 * lane) = reg[r][j];
                 lds_release();
                 if (lane == 0) lds_store(&ctl.ready[slot], k + 1);
+#ifdef MLQ_RING_STAMPS
+                if (lw == 0) {
+                    if (nstg[r] != last_written) RING_STAMP(nstg[r], 20);  // first unit of the stage in LDS
+                    last_written = nstg[r];
+                    RING_STAMP(nstg[r], 21);  // last unit so far
+                }
+#endif
+                stamp_issue(r);
                 nbytes[r] = cur.issue(nstages, lane, reg[r]);
                 cur.next(st, nstages, b, G, lw);
                 ++k;
@@ -314,9 +356,12 @@ __global__ __launch_bounds__(kRingThreads, 1) void gemv_ring_kernel(const SeqSta
     for (int s = 0; s < nstages; ++s) {
         RDesc& S = st[s];
         const int n = ring_rows(S, b, G), nch = S.nch, np = S.np;
+        if (cw == 0) RING_STAMP(s, 0);  // stage entered
         if (s > 0) {
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's y stores have completed
+            if (cw == 0) RING_STAMP(s, 1);
             meet();  // every compute wave is done with the old limbs and its stores
+            if (cw == 0) RING_STAMP(s, 2);
             if (S.barrier) {
                 ++barriers;
                 if (cw == 0 && lane == 0) {
@@ -337,6 +382,7 @@ __global__ __launch_bounds__(kRingThreads, 1) void gemv_ring_kernel(const SeqSta
                     }
                 }
                 meet();  // the grid has passed the barrier
+                if (cw == 0) RING_STAMP(s, 3);
             }
         }
         float4* xc = reinterpret_cast<float4*>(xl + np * XLimbs<QT>::PAIR_DW);
@@ -345,7 +391,10 @@ __global__ __launch_bounds__(kRingThreads, 1) void gemv_ring_kernel(const SeqSta
         } else {
             ring_stage_x<QT, false>(S, xl, xc, t);
         }
+        if (cw == 0) RING_STAMP(s, 4);
         meet();  // limbs of stage s in LDS
+        if (cw == 0) RING_STAMP(s, 5);
+        bool first_unit = cw == 0;
 
         uint32_t xq[XLimbs<QT>::PAIR_DW];
         float4 c0, c1;
@@ -365,10 +414,13 @@ __global__ __launch_bounds__(kRingThreads, 1) void gemv_ring_kernel(const SeqSta
             float acc = 0.0f;
             for (int c = 0; c < nch; ++c) {
                 const int slot = lw * SL + q;
+                if (first_unit) RING_STAMP(s, 6);
                 if (ok && !lds_wait_geq(&ctl.ready[slot], k + 1, spin_limit)) {
                     dev_store(&sync->error[0], 1u);
                     ok = false;
                 }
+                if (first_unit) RING_STAMP(s, 7);
+                first_unit = false;
                 lds_acquire();
                 const int p = c * 64 + lane;
                 if (nch > 1) load_xq<QT>(xl, xc, min(p, np - 1), xq, c0, c1);
@@ -398,6 +450,7 @@ __global__ __launch_bounds__(kRingThreads, 1) void gemv_ring_kernel(const SeqSta
                                    __HIP_MEMORY_SCOPE_AGENT);
             }
         }
+        RING_STAMP(s, 8 + cw);  // this compute wave's rows of the stage done
 #pragma unroll
         for (int l = 0; l < kRingLoaders; ++l)
             kb[l] += static_cast<unsigned>(n > l ? ((n - l - 1) / kRingLoaders + 1) * nch : 0);
@@ -468,6 +521,17 @@ hipError_t launch_ring(int qtype, const SeqStageDesc* stages, int nstages, SeqSy
     int x_bytes = (pair_lds_bytes(qtype, (kmax + kQK - 1) / kQK) + 15) & ~15;
     void* args[] = {&stages, &nstages, &sync, &spin_limit, &x_bytes, &nslots};
     return hipLaunchKernel(k, dim3(grid), dim3(kRingThreads), args, static_cast<size_t>(lds_bytes), stream);
+}
+
+hipError_t ring_stamps_copy(void* host, size_t bytes) {
+#ifdef MLQ_RING_STAMPS
+    if (bytes != sizeof(g_ring_stamps)) return hipErrorInvalidValue;
+    return hipMemcpyFromSymbol(host, HIP_SYMBOL(g_ring_stamps), bytes);
+#else
+    (void)host;
+    (void)bytes;
+    return hipErrorNotSupported;
+#endif
 }
 
 const char* ring_kernel_name(int qtype) {

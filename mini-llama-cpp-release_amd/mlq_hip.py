@@ -73,6 +73,7 @@ _SIGS = {
     "mlq_hip_stream_floor": (ctypes.c_int, [ctypes.POINTER(LinearCall), ctypes.c_int, _vp, _vp]),
     "mlq_hip_quant_linear_fused_f32": (ctypes.c_int, [ctypes.POINTER(LinearCall), ctypes.c_int, _vp]),
     "mlq_hip_stream_probe": (ctypes.c_int, [ctypes.POINTER(LinearCall), ctypes.c_int, ctypes.c_int, _vp, _vp]),
+    "mlq_hip_ring_stamps": (ctypes.c_int, [_vp, ctypes.c_size_t]),
     "mlq_hip_quant_linear_device": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, _vp, ctypes.c_size_t,
                                                     ctypes.c_int, ctypes.c_int, _vp, ctypes.c_int, _vp, _vp]),
     "mlq_hip_quant_linear_many": (ctypes.c_int, [ctypes.POINTER(LinearCall), ctypes.c_int, _vp]),
@@ -367,6 +368,20 @@ def stream_probe(arr: ctypes.Array, mode: int, sink: "DeviceBuffer", stream=None
     """mlq_hip_stream_probe: the floor's grid with no work (PROBE_EMPTY) or
     the same weight bytes read with plain coalesced loads (PROBE_LOAD)."""
     _check(load().mlq_hip_stream_probe(arr, len(arr), mode, sink.ptr, stream))
+
+
+STAMPS_LIB_PATH = os.path.join(HERE, "libmlq_hip_stamps.so")
+RING_STAMP_SHAPE = (3, 256, 24)  # workgroups, stages, slots (include/mlq_hip.h)
+
+
+def ring_stamps():
+    """mlq_hip_ring_stamps: the last LDS-ring launch's boundary timestamps
+    (s_memrealtime, 100 MHz) as a uint64 array of RING_STAMP_SHAPE; needs the
+    measurement build (STAMPS_LIB_PATH, `make stamps`) loaded."""
+    import numpy as np
+    out = np.zeros(RING_STAMP_SHAPE, np.uint64)
+    _check(load().mlq_hip_ring_stamps(out.ctypes.data, out.size))
+    return out
 
 
 def linear_fused_f32(arr: ctypes.Array, stream=None) -> None:

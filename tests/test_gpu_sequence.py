@@ -207,6 +207,17 @@ def test_graph_replays(hip, mode):
     seq.destroy()
 
 
+def test_ring_stamps_need_the_measurement_build(hip):
+    """mlq_hip_ring_stamps answers only from the measurement build (make
+    stamps); the product library refuses with MLQ_ERR_NOT_BUILT and says how
+    to build it, and checks its size argument first."""
+    buf = np.zeros(hip.RING_STAMP_SHAPE, np.uint64)
+    with pytest.raises(hip.MlqError, match="expected 18432"):
+        hip._check(hip.load().mlq_hip_ring_stamps(buf.ctypes.data, 5))
+    with pytest.raises(hip.MlqError, match="make stamps"):
+        hip.ring_stamps()
+
+
 def test_validation_messages(hip):
     l1 = Lin(hip, oracle.Q4_0, 64, 128, 1)
     l2 = Lin(hip, oracle.Q4_0, 64, 256, 2)
