@@ -155,6 +155,10 @@ private:
     void* ws_ = nullptr;
     size_t ws_bytes_ = 0;
     hipGraphExec_t graph_ = nullptr;
+    // generate() keeps at most kGenerateInflight recorded steps queued: the
+    // event after step i is waited for before step i + kGenerateInflight.
+    static constexpr int kGenerateInflight = 8;
+    hipEvent_t inflight_[kGenerateInflight] = {};
 };
 
 }  // namespace mlq

@@ -1597,6 +1597,8 @@ Decoder::~Decoder() {
     if (device_ >= 0) (void)hipSetDevice(device_);
     if (stream_) (void)hipStreamSynchronize(stream_);
     if (graph_) (void)hipGraphExecDestroy(graph_);
+    for (hipEvent_t ev : inflight_)
+        if (ev) (void)hipEventDestroy(ev);
     for (void* p : allocs_) (void)hipFree(p);
     if (stream_) (void)hipStreamDestroy(stream_);
 }
@@ -2215,7 +2217,16 @@ void Decoder::generate(const int* prompt, int n_prompt, int n_new, int* out) {
     } else {
         for (int i = 0; i + 1 < n_prompt; ++i) enqueue_step(stream_, false, true);
     }
-    for (int i = 0; i < n_new; ++i) check(hipGraphLaunch(graph_, stream_), "hipGraphLaunch");
+    // The host runs at most kGenerateInflight steps ahead of the device, so a
+    // long generation never has thousands of dispatches queued at once.
+    for (hipEvent_t& ev : inflight_)
+        if (ev == nullptr) check(hipEventCreateWithFlags(&ev, hipEventDisableTiming), "hipEventCreateWithFlags");
+    for (int i = 0; i < n_new; ++i) {
+        hipEvent_t& ev = inflight_[i % kGenerateInflight];
+        if (i >= kGenerateInflight) check(hipEventSynchronize(ev), "hipEventSynchronize");
+        check(hipGraphLaunch(graph_, stream_), "hipGraphLaunch");
+        check(hipEventRecord(ev, stream_), "hipEventRecord");
+    }
     check(hipMemcpyAsync(out, io_ + n_prompt, static_cast<size_t>(n_new) * 4, hipMemcpyDeviceToHost, stream_),
           "hipMemcpyAsync");
     check(hipMemcpyAsync(&st, state_, sizeof st, hipMemcpyDeviceToHost, stream_), "hipMemcpyAsync");
