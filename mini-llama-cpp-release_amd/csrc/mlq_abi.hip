@@ -1456,7 +1456,14 @@ int mlq_hip_sequence_create(const mlq_linear_call* calls, int n, const int* stag
     for (auto& g : seq->segs) {
         int nslots = 0;
         if (mode == MLQ_SEQ_PIPELINED) g.lds_bytes = mlq::chain_lds_bytes(g.qtype, g.kmax);
-        if (mode == MLQ_SEQ_LDS_RING) g.lds_bytes = mlq::ring_lds_bytes(g.qtype, g.kmax, &nslots);
+        if (mode == MLQ_SEQ_LDS_RING) {
+            g.lds_bytes = mlq::ring_lds_bytes(g.qtype, g.kmax, &nslots);
+            if (nslots < 8) {  // two slots per loader wave at least
+                delete seq;
+                return fail(MLQ_ERR_LIMIT, std::string(caller) + ": in_features=" + std::to_string(g.kmax) +
+                                               " leaves too little LDS for MLQ_SEQ_LDS_RING's weight ring");
+            }
+        }
         hipError_t e = mode == MLQ_SEQ_PIPELINED  ? mlq::chain_grid(g.qtype, g.lpr, g.lds_bytes, device, &g.grid)
                        : mode == MLQ_SEQ_LDS_RING ? mlq::ring_grid(g.qtype, g.lds_bytes, device, &g.grid)
                                                   : mlq::sequence_grid(g.qtype, g.lpr, g.lds_bytes, device, &g.grid);
