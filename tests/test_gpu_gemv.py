@@ -66,7 +66,10 @@ def test_gemv_full_shapes(hip, orc, shape):
 
 
 @pytest.mark.parametrize("shape", [(5, 13), (32, 64), (17, 65), (86, 32), (32, 86), (128, 32),
-                                   (1, 32), (3, 4095), (7, 33), (64, 4160), (40, 20000)],
+                                   (1, 32), (3, 4095), (7, 33), (64, 4160), (40, 20000),
+                                   # either side of the pair kernels' 64 KiB of x in LDS: Q8_0 584 / 586
+                                   # blocks, Q4 818 / 820 blocks (the wider one takes the byte-load kernel)
+                                   (16, 18688), (16, 18752), (16, 26176), (16, 26240)],
                          ids=lambda s: f"{s[0]}x{s[1]}")
 def test_gemv_small_and_ragged(hip, orc, shape):
     for fmt in FMTS:
