@@ -54,7 +54,11 @@ def test_gemm_256_tokens_two_splits(hip, orc, shape):
 
 @pytest.mark.parametrize("m,k,n", [(4096, 4096, 16), (64, 64, 2), (33, 4096, 17), (300, 896, 40),
                                    (4864, 896, 7), (17, 64, 100), (1000, 11008, 3), (520, 4096, 130),
-                                   (300, 896, 200), (200, 4096, 96)])
+                                   (300, 896, 200), (200, 4096, 96),
+                                   # either side of the in-kernel x split (up to 128 token rows)
+                                   (300, 4096, 128), (300, 4096, 129),
+                                   # 130 blocks per row: not a whole number of 4-block chunks
+                                   (300, 4160, 40), (300, 4160, 200)])
 def test_gemm_q4_1_and_ragged(hip, orc, m, k, n):
     for fmt, qt in FMTS.items():
         run(hip, orc, qt, m, k, n)
