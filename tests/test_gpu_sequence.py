@@ -221,6 +221,23 @@ def test_ring_stamps_need_the_measurement_build(hip):
         hip.ring_stamps()
 
 
+def test_ring_stamps_bench_leg(hip):
+    """The measurement build's boundary timestamps through `bench.py
+    --ring-stamps` (a child process loads libmlq_hip_stamps.so): two layers of
+    the sweep, every interval table printed for the three stamped workgroups."""
+    import os
+    import subprocess
+    if not os.path.exists(hip.STAMPS_LIB_PATH):
+        pytest.skip("the measurement build is not built (make -C mini-llama-cpp-release_amd stamps)")
+    repo = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    say("bench.py --ring-stamps, 2 layers")
+    r = subprocess.run([sys.executable, "bench.py", "--ring-stamps", "--layers", "2", "--steps", "2", "--warmup", "1"],
+                       cwd=repo, capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr[-2000:]
+    assert r.stdout.count("| grid barrier |") == 3, r.stdout[-2000:]
+    assert r.stdout.count("| loader: last unit in LDS |") == 3
+
+
 def test_validation_messages(hip):
     l1 = Lin(hip, oracle.Q4_0, 64, 128, 1)
     l2 = Lin(hip, oracle.Q4_0, 64, 256, 2)
